@@ -1,0 +1,204 @@
+/*
+ * C ABI of the MI355X TileInfer decode worker (gfx950).
+ *
+ * Plain structs, pointers and sizes only.  Every function returns 0 on success or a
+ * TI_ERR_* code; ti_error_string() names it and ti_last_error_message() gives the
+ * detail of the calling thread's last failure.
+ *
+ * Two layers are exported:
+ *  1. the launch boundary, replacing the reference's CUDA launcher
+ *     (tileinfer/src/runtime/detail/launch.cuh:10-96, worker_kernel.cu:223-284):
+ *     ti_describe_target, ti_exchange_words, ti_enqueue_worker, ti_enqueue_zero_unused_kv,
+ *     ti_enqueue_widen;
+ *  2. the runtime API (tileinfer/src/runtime/runtime.hpp:18-124 and plan.hpp:273-277)
+ *     as opaque handles, so that non-C++ hosts (Python ctypes, cgo) can drive it:
+ *     ti_load_plan … ti_context_collect.
+ */
+#ifndef TILEINFER_AMD_H
+#define TILEINFER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes ---------------------------------------------------------------- */
+enum {
+    TI_OK = 0,
+    TI_ERR_INVALID_ARGUMENT = 1, /* bad pointer/shape/step count (launch.cuh:74, worker_kernel.cu:243) */
+    TI_ERR_HIP = 2,              /* a HIP runtime call failed */
+    TI_ERR_PLAN = 3,             /* package rejected by the loader (plan.cpp:172-422) */
+    TI_ERR_RUNTIME = 4,          /* runtime API misuse or device-reported stop (sequence_context.cu) */
+    TI_ERR_NO_DEVICE = 5,
+};
+
+/* ---- launch records (plan.hpp:37-57, 114-122, 132-183, 189-195) ------------------ */
+enum {
+    TI_OP_BARRIER = 0,
+    TI_OP_QKV = 1,
+    TI_OP_ATTENTION_SCORES = 2,
+    TI_OP_ATTENTION_VALUES = 3,
+    TI_OP_OUTPUT_PROJECTION = 4,
+    TI_OP_FFN = 5,
+    TI_OP_FFN_REDUCE = 6,
+    TI_OP_EMBEDDING = 7,
+    TI_OP_FINAL_RMS_NORM = 8,
+    TI_OP_LOGITS = 9,
+};
+#define TI_NO_LAYER 0xffffffffu
+
+enum { TI_DTYPE_FLOAT32 = 0, TI_DTYPE_BFLOAT16 = 1 };
+
+typedef int32_t ti_token_id;
+
+typedef struct { uint32_t opcode, layer, begin, end, kv_head, chunk; } ti_task_record;
+typedef struct { uint32_t begin, count; } ti_worker_task_range;
+typedef struct {
+    uint32_t q, k, q_rot, attention, r, product, key, value;
+    uint32_t attn_norm, Wq, Wk, Wv, Wo, ffn_norm, Wgate, Wup, Wdown;
+} ti_layer_layout;
+typedef struct {
+    int32_t hidden_size, intermediate_size, query_heads, kv_heads, head_dim, max_context;
+    int32_t attention_chunks, attention_chunk_steps, attention_fused_steps, ffn_chunks;
+} ti_model_shape;
+typedef struct {
+    float rms_norm_eps, rope_theta, rope_factor, rope_low_freq_factor, rope_high_freq_factor,
+        rope_original_context;
+} ti_numeric_config;
+typedef struct {
+    int32_t layers, vocab_size, embedding_offset, layer_weights_offset, layer_weight_stride,
+        final_norm_offset, lm_head_offset, layer_kv_stride, full_stack;
+} ti_stack_config;
+typedef struct { float value; ti_token_id id; } ti_candidate; /* plan.hpp:185-189 */
+#define TI_NON_FINITE (-1)
+
+/* WorkerProgramView (launch.cuh:10-23): immutable device data of one uploaded model;
+ * `weights` is the device copy of weights.bin. */
+typedef struct {
+    const ti_task_record* instructions;
+    const ti_worker_task_range* streams; /* one per worker */
+    ti_layer_layout layout;
+    const void* weights;
+    const float* rotary_frequencies; /* head_dim / 2 */
+    ti_model_shape shape;
+    int32_t workers;
+    int32_t selection_slots;
+    ti_numeric_config numeric;
+    ti_stack_config stack;
+    int32_t weight_dtype;
+} ti_worker_program_view;
+
+/* WorkerBuffers (launch.cuh:31-45) plus the exchange area this worker synchronizes
+ * through.  `exchange` holds ti_exchange_words() 64-bit words, zeroed once at allocation;
+ * `epoch` must grow by at least ti_epochs_per_launch() between launches on one exchange area. */
+typedef struct {
+    void* input;
+    void* output;
+    void* scratch;
+    void* kv;
+    float* logits;
+    float* block_trace;
+    void* attention_scores;
+    float* attention_partials;
+    ti_candidate* selection;
+    float* ffn_trace;
+    uint64_t* timeline; /* unused by this worker; kept for layout parity */
+    uint64_t* exchange;
+    uint32_t epoch;
+} ti_worker_buffers;
+
+typedef struct { ti_token_id immediate; const ti_token_id* ids; int32_t steps; } ti_token_input; /* launch.cuh:49-54 */
+
+/* Status words of a generation request (launch.cuh:59-69). */
+enum { TI_STATUS_COUNT = 0, TI_STATUS_EOS = 1, TI_STATUS_ERROR = 2, TI_STATUS_WORDS = 3 };
+enum { TI_DEVICE_NO_ERROR = 0, TI_DEVICE_NON_FINITE = 1, TI_DEVICE_TOKEN_RANGE = 2, TI_DEVICE_SYNC_TIMEOUT = 3 };
+#define TI_MAX_LAUNCH_STEPS 64
+
+typedef struct { ti_token_id* generated; int32_t* status; int32_t first; ti_token_id eos_id; } ti_selection; /* launch.cuh:79-85 */
+
+/* Target (plan.hpp:207-224; worker_kernel.cu:253-284). */
+typedef struct {
+    char name[256];
+    char arch[64];
+    int32_t major, minor, sm_count, cooperative_launch, active_blocks_per_sm, registers_per_thread,
+        static_shared_bytes, max_threads_per_sm, threads_per_block, attention_shared_bytes;
+    uint64_t global_memory_bytes;
+    int32_t driver_version, runtime_version;
+    int32_t f32_registers, f32_shared_bytes, f32_active_blocks;
+    int32_t bf16_registers, bf16_shared_bytes, bf16_active_blocks;
+} ti_target;
+
+const char* ti_error_string(int code);
+const char* ti_last_error_message(void);
+const char* ti_abi(void);          /* "tileinfer-decoder-v10" (plan.hpp:16) */
+const char* ti_fingerprint(void);  /* this worker's compiled fingerprint */
+
+/* describe_target (plan.hpp:273, worker_kernel.cu:253-284): device 0 and the compiled worker. */
+int ti_describe_target(ti_target* out);
+
+/* 64-bit words of the exchange area one context needs for `shape`. */
+size_t ti_exchange_words(const ti_model_shape* shape, int32_t layers, int32_t selection_slots);
+uint32_t ti_epochs_per_launch(int32_t layers);
+
+/* detail::enqueue_worker (launch.cuh:87-88, worker_kernel.cu:240-249): one cooperative launch
+ * decoding token.steps ∈ [1, 64] consecutive positions from `position`.  `stream` is a
+ * hipStream_t (NULL = default stream).  Stream-ordered, never allocates. */
+int ti_enqueue_worker(void* stream, const ti_worker_program_view* program, const ti_worker_buffers* buffers,
+                      int32_t position, ti_token_input token, ti_selection selection);
+
+/* detail::enqueue_zero_unused_kv (launch.cuh:92-94, snapshot.cu:8-23,38-45). */
+int ti_enqueue_zero_unused_kv(void* stream, void* kv, int32_t dtype, size_t count, int32_t layers,
+                              int32_t layer_stride, int32_t width, int32_t capacity, int32_t key_offset,
+                              int32_t value_offset, int32_t prefix, const int32_t* generated_status);
+
+/* detail::enqueue_widen (activation_buffer.cuh:17-18, snapshot.cu:25-30,47-62): bf16 → f32. */
+int ti_enqueue_widen(void* stream, const void* source, int32_t dtype, size_t count, float* destination);
+
+/* ---- runtime API (runtime.hpp) ---------------------------------------------------- */
+typedef struct ti_plan ti_plan;        /* LoadedPlan (plan.hpp:238-266) */
+typedef struct ti_model ti_model;      /* DecoderModel */
+typedef struct ti_context ti_context;  /* SequenceContext */
+typedef struct ti_ticket ti_ticket;    /* Ticket */
+
+/* load_plan(package, describe_target(), verify_weights) (plan.hpp:276). */
+int ti_load_plan(const char* package, int32_t verify_weights, ti_plan** out);
+/* load_plan against a caller-supplied target (tests without a device, plan_loader_test.cpp:21-35). */
+int ti_load_plan_for_target(const char* package, const ti_target* target, int32_t verify_weights, ti_plan** out);
+void ti_plan_free(ti_plan* plan);
+/* JSON of --inspect-plan (main.cpp:62-107); valid until the next call on this thread. */
+const char* ti_plan_inspect_json(const ti_plan* plan);
+
+int ti_model_create(const ti_plan* plan, ti_model** out);
+void ti_model_free(ti_model* model);
+int ti_context_create(const ti_model* model, ti_context** out);
+void ti_context_free(ti_context* context);
+
+typedef struct { int32_t logits, kv, block_outputs; } ti_diagnostic_request;
+
+int ti_context_prefill(ti_context* context, const ti_token_id* ids, size_t count, ti_diagnostic_request diag,
+                       ti_ticket** out);
+int ti_context_decode(ti_context* context, ti_token_id id, ti_diagnostic_request diag, ti_ticket** out);
+/* eos_id < 0: none. */
+int ti_context_generate(ti_context* context, int32_t max_new_tokens, ti_token_id eos_id,
+                        ti_diagnostic_request diag, ti_ticket** out);
+int ti_context_reset(ti_context* context, ti_ticket** out);
+/* 1 ready, 0 not ready, <0 error (marks the context invalid). */
+int ti_context_ready(ti_context* context, const ti_ticket* ticket);
+
+enum { TI_STOP_NONE = 0, TI_STOP_LIMIT = 1, TI_STOP_EOS = 2 };
+typedef struct { int32_t count; int32_t position; int32_t stop_reason; double compute_us; } ti_completion;
+/* Waits; copies up to `capacity` generated ids into `generated`. */
+int ti_context_wait(ti_context* context, const ti_ticket* ticket, ti_completion* out, ti_token_id* generated,
+                    size_t capacity);
+/* Waits, then copies the ticket's diagnostics (sizes from ti_context_diagnostic_sizes). */
+int ti_context_diagnostic_sizes(const ti_context* context, size_t* logits, size_t* kv, size_t* block_outputs);
+int ti_context_collect(ti_context* context, const ti_ticket* ticket, float* logits, float* kv,
+                       float* block_outputs);
+void ti_ticket_free(ti_ticket* ticket);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

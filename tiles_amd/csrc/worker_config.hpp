@@ -1,0 +1,79 @@
+// Compile-time limits of the gfx950 decode worker and the layout of its exchange area,
+// shared by the kernel, the launcher and the host runtime.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "tileinfer_amd.h"
+
+namespace tiles {
+
+inline constexpr int kThreads = 1024;               // 16 wave64s per worker, one worker per CU
+inline constexpr int kMaxHidden = 4096;             // a task's input vector lives in LDS as FP32
+inline constexpr int kMaxHeadDim = 128;
+inline constexpr int kMaxGroup = 4;                 // query heads per K/V head (registers hold them all)
+inline constexpr int kMaxGroupTimesHeadDim = 512;   // attention P*V reduction in LDS (4 x 128)
+inline constexpr int kMaxTaskRows = 512;            // rows of one GEMV task kept in LDS
+// Shared bytes for one attention task's scores of all its query heads, in the package's
+// element type (the planner's chunk capacity, plan_core.py:91-97).  Held as FP32 in LDS.
+inline constexpr int kAttentionSharedBytes = 16384;
+inline constexpr int kRegionFloats = 9216;          // >= max(kThreads * 8, attention scores, P*V reduction)
+inline constexpr uint32_t kSpinLimit = 1u << 20;    // polls before a wait is declared stuck
+inline constexpr const char* kAbi = "tileinfer-decoder-v10";
+inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-flash-attention-v1-b1024";
+
+// Exchange phases within one (step, layer); the candidates use layer == layers.
+inline constexpr int kPhaseQKV = 0;
+inline constexpr int kPhaseAttn = 1;
+inline constexpr int kPhaseR = 2;
+inline constexpr int kPhaseFfn = 3;
+inline constexpr int kPhaseY = 4;
+inline constexpr int kPhaseCandidate = 0;
+inline constexpr int kPhases = 8;
+
+__host__ __device__ inline uint32_t epochs_per_step(int layers) { return static_cast<uint32_t>(layers + 1) * kPhases; }
+
+// Word offsets into the exchange area.  Each word: payload in bits 0-31 (one bf16 or fp32
+// element, or a candidate field), writer's epoch in bits 32-63.
+struct ExchangeLayout {
+    size_t control;      // [0]: nonzero once a worker declared a wait stuck
+    size_t hidden0, hidden1;  // layer outputs, alternating like the hidden buffers
+    size_t q, k, v;      // unrotated Q and K, V of the current position
+    size_t attn;         // merged attention output
+    size_t r;            // attention block output
+    size_t ffn;          // FP32 down partials, [ffn_chunks][hidden]
+    size_t candidates;   // greedy candidates, 2 words per slot
+    size_t counters;     // per (layer, kv_head): attention chunks finished
+    size_t total;
+    // A conditional, not an indexed array: a dynamic index into the launch record would put
+    // the whole record in scratch memory.
+    __host__ __device__ size_t hidden(int index) const { return index % 2 == 0 ? hidden0 : hidden1; }
+};
+
+__host__ __device__ inline ExchangeLayout exchange_layout(const ti_model_shape& s, int layers, int slots)
+{
+    ExchangeLayout x{};
+    const size_t d = static_cast<size_t>(s.hidden_size);
+    const size_t kvw = static_cast<size_t>(s.kv_heads) * s.head_dim;
+    x.control = 0;
+    x.hidden0 = 8;
+    x.hidden1 = x.hidden0 + d;
+    x.q = x.hidden1 + d;
+    x.k = x.q + d;
+    x.v = x.k + kvw;
+    x.attn = x.v + kvw;
+    x.r = x.attn + d;
+    x.ffn = x.r + d;
+    x.candidates = x.ffn + static_cast<size_t>(s.ffn_chunks) * d;
+    x.counters = x.candidates + 2 * static_cast<size_t>(slots > 0 ? slots : 1);
+    x.total = x.counters + static_cast<size_t>(layers) * s.kv_heads;
+    return x;
+}
+
+// Empty when the compiled worker supports the shape; otherwise the reason.
+std::string check_shape(const ti_model_shape& s, int dtype);
+std::string check_launch_shape(const ti_worker_program_view& p, const ti_worker_buffers& b, int position, int steps);
+
+} // namespace tiles

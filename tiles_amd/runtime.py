@@ -1,0 +1,262 @@
+"""Python binding of the decode worker's C ABI (include/tileinfer_amd.h) through ctypes.
+
+Mirrors the reference runtime API (tileinfer/src/runtime/runtime.hpp:18-124): ``load_plan``,
+``DecoderModel``, ``SequenceContext.enqueue_prefill / enqueue_decode / enqueue_generate /
+enqueue_reset / ready / wait / collect``.  Errors raise ``RuntimeError`` carrying the C++
+runtime's message (the reference's messages, e.g. "sequence context capacity reached").
+There is no fallback: without the built library every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+LIBRARY = Path(__file__).resolve().parent / "libtileinfer_amd.so"
+
+token_id = C.c_int32
+
+
+class TaskRecord(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("opcode", "layer", "begin", "end", "kv_head", "chunk")]
+
+
+class ModelShape(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("hidden_size", "intermediate_size", "query_heads", "kv_heads", "head_dim",
+                                         "max_context", "attention_chunks", "attention_chunk_steps",
+                                         "attention_fused_steps", "ffn_chunks")]
+
+
+class Target(C.Structure):
+    _fields_ = [("name", C.c_char * 256), ("arch", C.c_char * 64)] + [
+        (n, C.c_int32) for n in ("major", "minor", "sm_count", "cooperative_launch", "active_blocks_per_sm",
+                                 "registers_per_thread", "static_shared_bytes", "max_threads_per_sm",
+                                 "threads_per_block", "attention_shared_bytes")] + [
+        ("global_memory_bytes", C.c_uint64)] + [
+        (n, C.c_int32) for n in ("driver_version", "runtime_version", "f32_registers", "f32_shared_bytes",
+                                 "f32_active_blocks", "bf16_registers", "bf16_shared_bytes", "bf16_active_blocks")]
+
+
+class DiagnosticRequest(C.Structure):
+    _fields_ = [("logits", C.c_int32), ("kv", C.c_int32), ("block_outputs", C.c_int32)]
+
+
+class Completion(C.Structure):
+    _fields_ = [("count", C.c_int32), ("position", C.c_int32), ("stop_reason", C.c_int32), ("compute_us", C.c_double)]
+
+
+STOP_REASONS = {0: "none", 1: "limit", 2: "eos"}
+EXPORTS = ("ti_error_string", "ti_last_error_message", "ti_abi", "ti_fingerprint", "ti_describe_target",
+           "ti_exchange_words", "ti_epochs_per_launch", "ti_enqueue_worker", "ti_enqueue_zero_unused_kv",
+           "ti_enqueue_widen", "ti_load_plan", "ti_load_plan_for_target", "ti_plan_free", "ti_plan_inspect_json",
+           "ti_model_create", "ti_model_free", "ti_context_create", "ti_context_free", "ti_context_prefill",
+           "ti_context_decode", "ti_context_generate", "ti_context_reset", "ti_context_ready", "ti_context_wait",
+           "ti_context_diagnostic_sizes", "ti_context_collect", "ti_ticket_free")
+
+_lib = None
+
+
+def library() -> C.CDLL:
+    """The loaded C-ABI library; raises if it was not built (no CPU fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            raise RuntimeError(f"{LIBRARY} is missing: run python -m tiles_amd.build (hipcc, gfx950)")
+        lib = C.CDLL(str(LIBRARY), mode=os.RTLD_NOW | C.RTLD_GLOBAL)
+        P = C.c_void_p
+        lib.ti_error_string.restype = C.c_char_p
+        lib.ti_last_error_message.restype = C.c_char_p
+        lib.ti_abi.restype = C.c_char_p
+        lib.ti_fingerprint.restype = C.c_char_p
+        lib.ti_describe_target.argtypes = [C.POINTER(Target)]
+        lib.ti_exchange_words.argtypes = [C.POINTER(ModelShape), C.c_int32, C.c_int32]
+        lib.ti_exchange_words.restype = C.c_size_t
+        lib.ti_epochs_per_launch.argtypes = [C.c_int32]
+        lib.ti_epochs_per_launch.restype = C.c_uint32
+        lib.ti_load_plan.argtypes = [C.c_char_p, C.c_int32, C.POINTER(P)]
+        lib.ti_load_plan_for_target.argtypes = [C.c_char_p, C.POINTER(Target), C.c_int32, C.POINTER(P)]
+        lib.ti_plan_free.argtypes = [P]
+        lib.ti_plan_free.restype = None
+        lib.ti_plan_inspect_json.argtypes = [P]
+        lib.ti_plan_inspect_json.restype = C.c_char_p
+        lib.ti_model_create.argtypes = [P, C.POINTER(P)]
+        lib.ti_model_free.argtypes = [P]
+        lib.ti_model_free.restype = None
+        lib.ti_context_create.argtypes = [P, C.POINTER(P)]
+        lib.ti_context_free.argtypes = [P]
+        lib.ti_context_free.restype = None
+        lib.ti_context_prefill.argtypes = [P, C.POINTER(token_id), C.c_size_t, DiagnosticRequest, C.POINTER(P)]
+        lib.ti_context_decode.argtypes = [P, token_id, DiagnosticRequest, C.POINTER(P)]
+        lib.ti_context_generate.argtypes = [P, C.c_int32, token_id, DiagnosticRequest, C.POINTER(P)]
+        lib.ti_context_reset.argtypes = [P, C.POINTER(P)]
+        lib.ti_context_ready.argtypes = [P, P]
+        lib.ti_context_wait.argtypes = [P, P, C.POINTER(Completion), C.POINTER(token_id), C.c_size_t]
+        lib.ti_context_diagnostic_sizes.argtypes = [P, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        lib.ti_context_collect.argtypes = [P, P, C.POINTER(C.c_float), C.POINTER(C.c_float), C.POINTER(C.c_float)]
+        lib.ti_ticket_free.argtypes = [P]
+        lib.ti_ticket_free.restype = None
+        _lib = lib
+    return _lib
+
+
+def _check(code: int) -> None:
+    if code != 0:
+        message = library().ti_last_error_message().decode()
+        raise RuntimeError(message or library().ti_error_string(code).decode())
+
+
+def describe_target() -> Target:
+    target = Target()
+    _check(library().ti_describe_target(C.byref(target)))
+    return target
+
+
+def target_from_probe(probe: dict) -> Target:
+    """A Target matching a normalized probe document (for loading packages without a device,
+    as the reference's loader tests do with a fake capability)."""
+    t = Target()
+    device, executor = probe["device"], probe["executor"]
+    t.name = device.get("name", "").encode()[:255]
+    t.major, t.minor = device["compute_capability"]
+    t.sm_count = device["sm_count"]
+    t.cooperative_launch = 1 if device["cooperative_launch"] else 0
+    t.active_blocks_per_sm = executor["active_blocks_per_sm"]
+    t.threads_per_block = executor["threads_per_block"]
+    t.attention_shared_bytes = executor["attention_shared_bytes"]
+    return t
+
+
+class Plan:
+    """A validated package (LoadedPlan, plan.hpp:238-266)."""
+
+    def __init__(self, package: str | Path, verify_weights: bool = True, target: Target | None = None):
+        handle = C.c_void_p()
+        path = str(package).encode()
+        if target is None:
+            _check(library().ti_load_plan(path, int(verify_weights), C.byref(handle)))
+        else:
+            _check(library().ti_load_plan_for_target(path, C.byref(target), int(verify_weights), C.byref(handle)))
+        self._handle = handle
+
+    def inspect(self) -> dict:
+        import json
+
+        return json.loads(library().ti_plan_inspect_json(self._handle).decode())
+
+    def __del__(self):
+        if getattr(self, "_handle", None) and _lib is not None:
+            _lib.ti_plan_free(self._handle)
+            self._handle = None
+
+
+def load_plan(package: str | Path, verify_weights: bool = True) -> Plan:
+    return Plan(package, verify_weights)
+
+
+@dataclass
+class Result:
+    generated: list[int]
+    position: int
+    stop_reason: str
+    compute_us: float
+
+
+class Ticket:
+    def __init__(self, context: "SequenceContext", handle: C.c_void_p, kind: str, requested: int = 0):
+        self._context, self._handle, self.kind, self.requested = context, handle, kind, requested
+
+    def __del__(self):
+        if getattr(self, "_handle", None) and _lib is not None:
+            _lib.ti_ticket_free(self._handle)
+            self._handle = None
+
+
+class DecoderModel:
+    """Uploads one validated package; shareable by sequence contexts."""
+
+    def __init__(self, plan: Plan):
+        handle = C.c_void_p()
+        _check(library().ti_model_create(plan._handle, C.byref(handle)))
+        self._handle = handle
+        self.plan = plan
+
+    def create_context(self) -> "SequenceContext":
+        return SequenceContext(self)
+
+    def __del__(self):
+        if getattr(self, "_handle", None) and _lib is not None:
+            _lib.ti_model_free(self._handle)
+            self._handle = None
+
+
+class SequenceContext:
+    """One sequence's stream, K/V cache and tickets; calls must be serialized by the caller."""
+
+    def __init__(self, model: DecoderModel):
+        handle = C.c_void_p()
+        _check(library().ti_context_create(model._handle, C.byref(handle)))
+        self._handle = handle
+        self.model = model
+        sizes = [C.c_size_t() for _ in range(3)]
+        _check(library().ti_context_diagnostic_sizes(handle, *[C.byref(s) for s in sizes]))
+        self.logits_size, self.kv_size, self.blocks_size = (s.value for s in sizes)
+
+    def __del__(self):
+        if getattr(self, "_handle", None) and _lib is not None:
+            _lib.ti_context_free(self._handle)
+            self._handle = None
+
+    @staticmethod
+    def _request(logits=False, kv=False, block_outputs=False) -> DiagnosticRequest:
+        return DiagnosticRequest(int(logits), int(kv), int(block_outputs))
+
+    def enqueue_prefill(self, token_ids, logits=False, kv=False, block_outputs=False) -> Ticket:
+        ids = (token_id * len(token_ids))(*[int(t) for t in token_ids])
+        handle = C.c_void_p()
+        _check(library().ti_context_prefill(self._handle, ids, len(token_ids),
+                                            self._request(logits, kv, block_outputs), C.byref(handle)))
+        return Ticket(self, handle, "prefill")
+
+    def enqueue_decode(self, token: int, logits=False, kv=False, block_outputs=False) -> Ticket:
+        handle = C.c_void_p()
+        _check(library().ti_context_decode(self._handle, int(token), self._request(logits, kv, block_outputs),
+                                           C.byref(handle)))
+        return Ticket(self, handle, "prefill")
+
+    def enqueue_generate(self, max_new_tokens: int, eos_id: int | None = None, logits=False, kv=False,
+                         block_outputs=False) -> Ticket:
+        handle = C.c_void_p()
+        _check(library().ti_context_generate(self._handle, int(max_new_tokens), -1 if eos_id is None else int(eos_id),
+                                             self._request(logits, kv, block_outputs), C.byref(handle)))
+        return Ticket(self, handle, "generate", max(0, int(max_new_tokens)))
+
+    def enqueue_reset(self) -> Ticket:
+        handle = C.c_void_p()
+        _check(library().ti_context_reset(self._handle, C.byref(handle)))
+        return Ticket(self, handle, "reset")
+
+    def ready(self, ticket: Ticket) -> bool:
+        code = library().ti_context_ready(self._handle, ticket._handle)
+        if code < 0:
+            _check(-code)
+        return code == 1
+
+    def wait(self, ticket: Ticket) -> Result:
+        done = Completion()
+        ids = (token_id * max(1, ticket.requested))()
+        _check(library().ti_context_wait(self._handle, ticket._handle, C.byref(done), ids, ticket.requested))
+        return Result(list(ids[: done.count]) if ticket.requested else [], done.position,
+                      STOP_REASONS.get(done.stop_reason, "none"), done.compute_us)
+
+    def collect(self, ticket: Ticket) -> dict:
+        logits = np.zeros(self.logits_size, dtype=np.float32)
+        kv = np.zeros(self.kv_size, dtype=np.float32)
+        blocks = np.zeros(self.blocks_size, dtype=np.float32)
+        fp = C.POINTER(C.c_float)
+        _check(library().ti_context_collect(self._handle, ticket._handle, logits.ctypes.data_as(fp),
+                                            kv.ctypes.data_as(fp), blocks.ctypes.data_as(fp)))
+        return {"logits": logits, "kv": kv, "block_outputs": blocks}
