@@ -1,0 +1,185 @@
+"""Benchmark: bf16 batch-1 greedy decode of a random-init Llama-3.2-1B on one MI355X.
+
+Prints ONE JSON line (the driver's contract).  The workload named by BASELINE.json's metric:
+
+* ctx 1 (config 3, the headline ``value``): 1-token prompt, 256 new tokens, 64 per launch;
+* ctx 4096 (config 4): 4096 seeded uniform prompt tokens prefilled, then 64 new tokens in one
+  launch (reported under ``ctx4096``).
+
+A "step" is one token of decode (one pass of the hot path); ``ms_per_step`` = ``value``
+= ms/token of the generate launches, timed with HIP events on the context stream (prefill,
+setup and readback excluded, as the reference's ``tile_runtime bench``).  The roofline block
+prices the decoder_worker launches against HBM: algorithmic bytes = every weight byte plus
+32 KiB of K/V per visible position per token.  ``cpu_baseline`` times the PyTorch-eager CPU
+oracle (oracle/decoder.py) on the same bf16 weights, on a bounded sample of the same decode.
+"""
+
+from __future__ import annotations
+
+import argparse
+import gc
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+WEIGHT_BYTES = 2_471_628_800          # bf16 weights streamed per token
+KV_BYTES_PER_POSITION = 32_768        # 16 layers x (K + V) x 8 heads x 64 x 2 bytes
+PEAK_HBM_GBPS = 8000.0                # MI355X published HBM3E bandwidth
+
+
+def log(*args) -> None:
+    print(*args, file=sys.stderr, flush=True)
+
+
+def bytes_per_token(position: int) -> int:
+    """Algorithmic bytes to decode the token at `position` (visible prefix position + 1)."""
+    return WEIGHT_BYTES + (position + 1) * KV_BYTES_PER_POSITION
+
+
+def cpu_baseline(weights: dict, prompt: list[int], tokens: int) -> dict:
+    """The oracle's eager bf16 decode on the host cores: median ms per decoded token."""
+    import torch
+
+    from oracle import decoder as ref
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    spec = ref.Spec(hidden_size=2048, intermediate_size=8192, num_attention_heads=32, num_key_value_heads=8,
+                    head_dim=64, max_context=len(prompt) + tokens + 1, layers=16, vocab_size=128256)
+    cache = ref.StackCache.empty(spec, torch.bfloat16)
+    samples = []
+    with torch.inference_mode():
+        out = None
+        for token in prompt:
+            out = ref.decode_token(token, weights, spec, cache)
+        for _ in range(tokens):
+            token = ref.greedy(out["logits"])
+            start = time.perf_counter()
+            out = ref.decode_token(token, weights, spec, cache)
+            samples.append((time.perf_counter() - start) * 1e3)
+    ms = statistics.median(samples[1:] if len(samples) > 2 else samples)
+    return {"value": ms, "unit": "ms/token", "cores": threads, "kind": "port",
+            "sample": f"{tokens} greedy bf16 decode steps at ctx 1-{tokens + 1} of the same random-init "
+                      f"Llama-3.2-1B, PyTorch eager CPU oracle (oracle/decoder.py), median after the first"}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=4, help="timed 256-token ctx-1 generations")
+    parser.add_argument("--warmup", type=int, default=1)
+    parser.add_argument("--no-ctx4096", action="store_true")
+    parser.add_argument("--cpu-tokens", type=int, default=24)
+    parser.add_argument("--chunk-steps", type=int, default=128)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the decode worker is single-GPU); --gpus {args.gpus} is not supported",
+              file=sys.stderr)
+        return 2
+    steps = max(1, args.steps)
+
+    from tiles_amd import runtime as R
+    from tiles_amd import synthetic as S
+    from tiles_amd.tileplan import probe
+
+    target = probe.probe_library()
+    stream_gbps = R.measure_stream_read(2 << 30, 3)
+    log(f"measured stream read {stream_gbps:.1f} GB/s")
+    work = S.scratch_dir()
+    max_context = 4096 + 64
+    start = time.time()
+    spec, weights = S.llama_package(work / "llama", max_context, "bfloat16", seed=0, chunk_steps=args.chunk_steps,
+                                    target=target)
+    log(f"package built in {time.time() - start:.1f}s")
+    plan = R.load_plan(work / "llama", verify_weights=False)
+    model = R.DecoderModel(plan)
+    ctx = model.create_context()
+
+    # ctx 1: 1-token prompt, 256 new tokens (4 launches of 64)
+    new_tokens = 256
+    prompt = [S.BOS]
+    times, generated = [], None
+    for round_ in range(args.warmup + steps):
+        ctx.wait(ctx.enqueue_reset())
+        ctx.wait(ctx.enqueue_prefill(prompt))
+        result = ctx.wait(ctx.enqueue_generate(new_tokens))
+        if generated is None:
+            generated = result.generated
+        elif generated != result.generated:
+            raise RuntimeError("benchmark generated different tokens across rounds")
+        if round_ >= args.warmup:
+            times.append(result.compute_us)
+    mean_us = statistics.mean(times)
+    ms_per_token = mean_us / new_tokens / 1e3
+    positions = range(len(prompt), len(prompt) + new_tokens)
+    total_bytes = sum(bytes_per_token(p) for p in positions)
+    launches = (new_tokens + 63) // 64
+    achieved = total_bytes / (mean_us * 1e-6) / 1e9
+    floor_ms = total_bytes / new_tokens / (stream_gbps * 1e9) * 1e3
+    log(f"ctx1: {ms_per_token * 1e3:.1f} us/token, floor {floor_ms * 1e3:.1f} us")
+
+    ctx4096 = None
+    if not args.no_ctx4096:
+        long_prompt = S.prompt(4096, seed=4096)
+        ctx.wait(ctx.enqueue_reset())
+        start = time.time()
+        ctx.wait(ctx.enqueue_prefill(long_prompt))
+        prefill_s = time.time() - start
+        result = ctx.wait(ctx.enqueue_generate(64))
+        long_bytes = sum(bytes_per_token(p) for p in range(4096, 4096 + 64))
+        long_ms = result.compute_us / 64 / 1e3
+        long_floor = long_bytes / 64 / (stream_gbps * 1e9) * 1e3
+        ctx4096 = {"ms_per_token": long_ms, "tokens_per_second": 1e3 / long_ms,
+                   "floor_ms_per_token": long_floor, "fraction_of_floor": long_floor / long_ms,
+                   "achieved_GBps": long_bytes / (result.compute_us * 1e-6) / 1e9,
+                   "prefill_tokens": 4096, "prefill_s": prefill_s, "new_tokens": 64}
+        log(f"ctx4096: {long_ms * 1e3:.1f} us/token, floor {long_floor * 1e3:.1f} us")
+
+    # Release device objects while the HIP runtime is alive (profilers finalize at exit).
+    del ctx, model, plan
+    gc.collect()
+    baseline = None
+    if args.cpu_tokens > 0:
+        baseline = cpu_baseline(weights, prompt, args.cpu_tokens)
+        log(f"cpu baseline {baseline['value']:.1f} ms/token on {baseline['cores']} threads")
+    line = {
+        "metric": "ms/token bf16 batch-1 decode at ctx 1 & 4096; % of HBM byte floor",
+        "value": ms_per_token,
+        "unit": "ms/token",
+        "n_gpus": 1,
+        "steps": steps * new_tokens,
+        "warmup": args.warmup * new_tokens,
+        "ms_per_step": ms_per_token,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights, norm weights 1.0, seed 0)",
+        "config": {"workload": "Llama-3.2-1B bf16 batch-1 greedy decode, ctx 1: 1-token prompt, 256 new tokens, "
+                               "64 per persistent launch (BASELINE config 3); ctx 4096 under ctx4096 (config 4)",
+                   "global_batch": 1, "seq_len": len(prompt) + new_tokens, "parallelism": "none",
+                   "attention_chunk_steps": args.chunk_steps, "workers": target["launch"]["worker_count"]},
+        "tokens_per_second": 1e3 / ms_per_token,
+        "hbm_stream_read_GBps": stream_gbps,
+        "floor_ms_per_token": floor_ms,
+        "fraction_of_floor": floor_ms / ms_per_token,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBPS, "traffic": None,
+                     "kernel": "decoder_worker", "launches": launches * steps,
+                     "bytes_per_launch": total_bytes / launches, "avg_launch_us": mean_us / launches},
+        "ctx4096": ctx4096,
+        "cpu_baseline": baseline,
+        "generated_head": generated[:8],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

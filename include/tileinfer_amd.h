@@ -104,7 +104,7 @@ typedef struct {
     float* attention_partials;
     ti_candidate* selection;
     float* ffn_trace;
-    uint64_t* timeline; /* unused by this worker; kept for layout parity */
+    uint64_t* timeline; /* optional: 2 words per instruction, device clock at start and end (launch.cuh:25-28) */
     uint64_t* exchange;
     uint32_t epoch;
 } ti_worker_buffers;
@@ -156,6 +156,11 @@ int ti_enqueue_zero_unused_kv(void* stream, void* kv, int32_t dtype, size_t coun
 /* detail::enqueue_widen (activation_buffer.cuh:17-18, snapshot.cu:25-30,47-62): bf16 → f32. */
 int ti_enqueue_widen(void* stream, const void* source, int32_t dtype, size_t count, float* destination);
 
+/* Best streaming-read bandwidth (GB/s) of device 0 over a sweep of grid sizes, block sizes and
+ * loads in flight, reading a `bytes` buffer `repeats` times per configuration; the HBM rate the
+ * byte floor is quoted against (bandwidth_probe.cu:509-549, profile_timeline.py:41-42). */
+int ti_measure_stream_read(size_t bytes, int32_t repeats, double* best_gbps);
+
 /* ---- runtime API (runtime.hpp) ---------------------------------------------------- */
 typedef struct ti_plan ti_plan;        /* LoadedPlan (plan.hpp:238-266) */
 typedef struct ti_model ti_model;      /* DecoderModel */
@@ -196,6 +201,12 @@ int ti_context_wait(ti_context* context, const ti_ticket* ticket, ti_completion*
 int ti_context_diagnostic_sizes(const ti_context* context, size_t* logits, size_t* kv, size_t* block_outputs);
 int ti_context_collect(ti_context* context, const ti_ticket* ticket, float* logits, float* kv,
                        float* block_outputs);
+/* Timeline mode (diagnostic_context.cu:257-285, main.cpp --timeline-stack): while enabled, every
+ * launch stamps each instruction of its last step with the 100 MHz device clock at start and
+ * end.  ti_context_timeline copies 2 words per instruction (plan instruction order) after
+ * waiting for the context's queued work; `count` receives the number of instructions. */
+int ti_context_set_timeline(ti_context* context, int32_t enabled);
+int ti_context_timeline(ti_context* context, uint64_t* words, size_t capacity, size_t* count);
 void ti_ticket_free(ti_ticket* ticket);
 
 #ifdef __cplusplus

@@ -1,0 +1,241 @@
+"""GPU parity of the HIP decode worker against the CPU oracle (oracle/decoder.py).
+
+Cases follow the reference's GPU tests (tileinfer/tests/stack_regression.py:33-450,
+kernel_regression.py:111-297, decoder_regression.py:41-220):
+
+* decoder_m4 (3 layers, d=32, vocab 48): fp32 logits and K/V vs the frozen fixture; bf16 logits,
+  K/V and greedy tokens bit-exact vs the oracle on the same packed weights.
+* a small stack with a long context and 16-step attention chunks: the split-context merge
+  path (several chunks per head) vs the oracle, fp32 within 1e-4 relative.
+* random-init Llama-3.2-1B: fp32 per-step logits within 1e-4 relative (the north-star fp32
+  bar); bf16 within the measured noise floor of two valid eager orderings,
+  greedy tokens equal wherever the oracle's top-2 gap exceeds that floor.
+* generation semantics: multi-launch, EOS, capacity, vocabulary and non-finite-logit errors.
+"""
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decoder as ref
+from tiles_amd import runtime as R
+from tiles_amd import synthetic as S
+from tiles_amd.tileplan import package as K
+from tiles_amd.tileplan import plan as P
+from tiles_amd.tileplan import probe
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).parent / "golden"
+# bf16 Llama-3.2-1B: two valid eager orderings of the oracle (bf16 GEMV vs FP32-accumulated GEMV
+# rounded once) differ by up to 0.078 in a logit (measured, seed 0); the worker must stay within
+# twice that, and agree on the greedy token wherever the oracle's top-2 gap exceeds it.
+BF16_1B_NOISE_FLOOR = 0.08
+
+
+@pytest.fixture(scope="module")
+def target():
+    return probe.probe_library()
+
+
+@pytest.fixture(scope="module")
+def tmp(tmp_path_factory):
+    return tmp_path_factory.mktemp("gpu")
+
+
+def m4():
+    model = json.loads((GOLDEN / "decoder_m4" / "model.json").read_text())
+    block = P.BlockSpec(**{k: model[k] for k in P.BlockSpec.__dataclass_fields__ if k in model})
+    spec = P.StackSpec(block, model["layers"], model["vocab_size"], model["tie_word_embeddings"])
+    with np.load(GOLDEN / "decoder_m4" / "weights.npz", allow_pickle=False) as data:
+        weights = {k: torch.from_numpy(data[k].copy()) for k in data.files}
+    with np.load(GOLDEN / "decoder_m4" / "reference_cases.npz", allow_pickle=False) as data:
+        cases = {k: data[k].copy() for k in data.files}
+    return spec, weights, cases, ref.Spec.from_dict(model)
+
+
+def context_for(path):
+    plan = R.load_plan(path)
+    model = R.DecoderModel(plan)
+    return model, model.create_context()
+
+
+def kv_at(snapshot, spec: P.StackSpec, plan_dict, layer, position, which):
+    layout = {e["tensor"]: e["offset"] for e in plan_dict["storage"]["kv"]}
+    elem = P.weight_size(plan_dict["model"]["weight_dtype"])
+    width = spec.block.num_key_value_heads * spec.block.head_dim
+    stride = plan_dict["storage"]["stack"]["layer_kv_stride"] // elem
+    base = layer * stride + layout[P.TID[which]] // elem + position * width
+    return snapshot["kv"][base:base + width]
+
+
+def test_m4_fp32_matches_frozen_fixture(target, tmp):
+    spec, weights, cases, _ = m4()
+    K.build_stack_package(spec, weights, target, tmp / "m4_f32", "float32")
+    plan_dict = K.read_plan(tmp / "m4_f32")
+    _, ctx = context_for(tmp / "m4_f32")
+    for step, token in enumerate(cases["token_ids"].tolist()):
+        got = ctx.collect(ctx.enqueue_decode(token, logits=True, kv=True))
+        np.testing.assert_allclose(got["logits"], cases["logits"][step], atol=1e-4, rtol=1e-4)
+    for layer in range(spec.layers):
+        for p in range(len(cases["token_ids"])):
+            np.testing.assert_allclose(kv_at(got, spec, plan_dict, layer, p, "K"), cases["k_cache"][layer, 0, p].ravel(),
+                                       atol=1e-4, rtol=1e-4)
+            np.testing.assert_allclose(kv_at(got, spec, plan_dict, layer, p, "V"), cases["v_cache"][layer, 0, p].ravel(),
+                                       atol=1e-4, rtol=1e-4)
+    # unused cache rows are zeroed in the snapshot (snapshot.cu:8-23)
+    assert not kv_at(got, spec, plan_dict, 0, 5, "K").any()
+
+
+def test_m4_bf16_bit_exact_with_oracle(target, tmp):
+    spec, weights, cases, ospec = m4()
+    K.build_stack_package(spec, weights, target, tmp / "m4_bf16", "bfloat16")
+    packed = K.read_weights(tmp / "m4_bf16", spec, "bfloat16")
+    _, ctx = context_for(tmp / "m4_bf16")
+    cache = ref.StackCache.empty(ospec, torch.bfloat16)
+    for token in cases["token_ids"].tolist():
+        got = ctx.collect(ctx.enqueue_decode(token, logits=True))["logits"]
+        want = ref.decode_token(token, packed, ospec, cache)["logits"].float().numpy()
+        np.testing.assert_array_equal(got, want)
+    # greedy generation from a fresh one-token prefix
+    ctx.wait(ctx.enqueue_reset())
+    ctx.wait(ctx.enqueue_prefill([7]))
+    result = ctx.wait(ctx.enqueue_generate(5))
+    assert result.generated == ref.generate([7], 5, packed, ospec, torch.bfloat16)["tokens"]
+    assert result.stop_reason == "limit" and result.position == 6
+
+
+def small_stack(max_context, layers=2, vocab=512):
+    block = P.BlockSpec(hidden_size=256, intermediate_size=512, num_attention_heads=4, num_key_value_heads=1,
+                        head_dim=64, max_context=max_context)
+    return P.StackSpec(block, layers, vocab, True)
+
+
+def small_oracle_spec(spec: P.StackSpec) -> ref.Spec:
+    b = spec.block
+    return ref.Spec(hidden_size=b.hidden_size, intermediate_size=b.intermediate_size,
+                    num_attention_heads=b.num_attention_heads, num_key_value_heads=b.num_key_value_heads,
+                    head_dim=b.head_dim, max_context=b.max_context, layers=spec.layers, vocab_size=spec.vocab_size)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_split_context_attention_merge(target, tmp, dtype):
+    """Contexts of 17..200 steps over 16-step chunks: the split path with up to 13 chunks."""
+    spec = small_stack(240)
+    weights = K.random_weights(spec, seed=5, std=0.08, dtype=torch.float32)
+    K.build_stack_package(spec, weights, target, tmp / f"split_{dtype}", dtype, chunk_steps=16)
+    assert K.read_plan(tmp / f"split_{dtype}")["model"]["attention_chunks"] == 15
+    packed = K.read_weights(tmp / f"split_{dtype}", spec, dtype)
+    tdt = torch.float32 if dtype == "float32" else torch.bfloat16
+    ospec = small_oracle_spec(spec)
+    tokens = S.prompt(200, seed=11, vocab=spec.vocab_size)
+    _, ctx = context_for(tmp / f"split_{dtype}")
+    ctx.wait(ctx.enqueue_prefill(tokens[:-1]))
+    got = ctx.collect(ctx.enqueue_decode(tokens[-1], logits=True))["logits"]
+    cache = ref.StackCache.empty(ospec, tdt)
+    with torch.inference_mode():
+        for t in tokens:
+            want = ref.decode_token(t, packed, ospec, cache)["logits"].float().numpy()
+    if dtype == "float32":
+        np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
+    else:
+        # flash-style merge keeps unrounded chunk probabilities: bf16 logits differ by rounding only
+        assert np.abs(got - want).max() <= 0.1
+        assert int(got.argmax()) == int(want.argmax()) or np.sort(want)[-1] - np.sort(want)[-2] < 0.1
+
+
+def test_generation_semantics(target, tmp):
+    spec = small_stack(160, layers=1, vocab=300)
+    weights = K.random_weights(spec, seed=9, std=0.1, dtype=torch.float32)
+    K.build_stack_package(spec, weights, target, tmp / "gen", "float32")
+    packed = K.read_weights(tmp / "gen", spec, "float32")
+    ospec = small_oracle_spec(spec)
+    _, ctx = context_for(tmp / "gen")
+    # multi-launch generation (85 tokens = 64 + 21) after a 70-token prompt (kernel_regression.py)
+    prompt = S.prompt(70, seed=2, vocab=spec.vocab_size)
+    ctx.wait(ctx.enqueue_prefill(prompt))
+    result = ctx.wait(ctx.enqueue_generate(85))
+    oracle = ref.generate(prompt, 85, packed, ospec, torch.float32)
+    assert result.generated == oracle["tokens"]
+    assert result.position == 155 and result.stop_reason == "limit"
+    with pytest.raises(RuntimeError, match="sequence context capacity reached"):
+        ctx.enqueue_generate(6)
+    # EOS: stop at the first occurrence of a token the generation produces
+    eos = oracle["tokens"][3]
+    first = oracle["tokens"].index(eos)
+    ctx.wait(ctx.enqueue_reset())
+    ctx.wait(ctx.enqueue_prefill(prompt))
+    stopped = ctx.wait(ctx.enqueue_generate(40, eos_id=eos))
+    assert stopped.stop_reason == "eos" and stopped.generated == oracle["tokens"][: first + 1]
+    assert stopped.position == 70 + first + 1
+    # the sequence continues from the EOS position
+    more = ctx.wait(ctx.enqueue_generate(2))
+    assert more.position == stopped.position + 2
+    with pytest.raises(RuntimeError, match="token ID outside vocabulary"):
+        ctx.enqueue_decode(spec.vocab_size)
+    ctx.wait(ctx.enqueue_reset())
+    with pytest.raises(RuntimeError, match="generation requires a nonempty prefix"):
+        ctx.enqueue_generate(1)
+
+
+def test_non_finite_logits_stop_generation(target, tmp):
+    """NaN in an unused embedding row makes its logit NaN (stack_regression.py:259-271)."""
+    spec = small_stack(32, layers=1, vocab=300)
+    weights = K.random_weights(spec, seed=9, std=0.1, dtype=torch.float32)
+    weights["embedding"][299, 5] = float("nan")
+    K.build_stack_package(spec, weights, target, tmp / "nan", "float32")
+    _, ctx = context_for(tmp / "nan")
+    ctx.wait(ctx.enqueue_prefill([1, 2, 3]))
+    with pytest.raises(RuntimeError, match="generation stopped: non-finite logits"):
+        ctx.wait(ctx.enqueue_generate(3))
+    with pytest.raises(RuntimeError, match="reset required"):
+        ctx.enqueue_decode(1)
+    ctx.wait(ctx.enqueue_reset())
+    ctx.wait(ctx.enqueue_decode(1))
+
+
+@pytest.fixture(scope="module")
+def llama_weights():
+    return K.random_weights(P.llama32_1b(64), seed=0)
+
+
+def llama_oracle_spec(max_context):
+    return ref.Spec(hidden_size=2048, intermediate_size=8192, num_attention_heads=32, num_key_value_heads=8,
+                    head_dim=64, max_context=max_context, layers=16, vocab_size=128256)
+
+
+@pytest.mark.slow
+def test_llama_fp32_logits_within_1e4_relative(target, tmp, llama_weights):
+    weights = {k: v.float() for k, v in llama_weights.items()}
+    S.llama_package(tmp / "l1b_f32", 64, "float32", target=target, weights=weights, chunk_steps=64)
+    _, ctx = context_for(tmp / "l1b_f32")
+    ospec = llama_oracle_spec(64)
+    cache = ref.StackCache.empty(ospec, torch.float32)
+    for token in [S.BOS, 9906, 1917]:
+        got = ctx.collect(ctx.enqueue_decode(token, logits=True))["logits"]
+        with torch.inference_mode():
+            want = ref.decode_token(token, weights, ospec, cache)["logits"].numpy()
+        scale = np.abs(want).max()
+        assert np.abs(got - want).max() <= 1e-4 * scale, np.abs(got - want).max()
+        assert int(got.argmax()) == int(want.argmax())
+
+
+@pytest.mark.slow
+def test_llama_bf16_tokens_and_logits(target, tmp, llama_weights):
+    S.llama_package(tmp / "l1b_bf16", 64, "bfloat16", target=target, weights=llama_weights, chunk_steps=64)
+    _, ctx = context_for(tmp / "l1b_bf16")
+    ctx.wait(ctx.enqueue_prefill([S.BOS]))
+    generated = ctx.wait(ctx.enqueue_generate(8)).generated
+    ospec = llama_oracle_spec(64)
+    oracle = ref.generate([S.BOS], 8, llama_weights, ospec, torch.bfloat16, forced=generated)
+    ctx.wait(ctx.enqueue_reset())
+    for step, token in enumerate([S.BOS] + generated[:-1]):
+        got = ctx.collect(ctx.enqueue_decode(token, logits=True))["logits"]
+        want = oracle["logits"][step].numpy()
+        assert np.abs(got - want).max() <= 2 * BF16_1B_NOISE_FLOOR
+        top2 = np.sort(want)[-2:]
+        if top2[1] - top2[0] > BF16_1B_NOISE_FLOOR:
+            assert generated[step] == oracle["tokens"][step]

@@ -90,8 +90,11 @@ struct UploadedModel {
     ti_worker_program_view view{};
     size_t exchange_words = 0;
 
+    size_t instruction_count = 0;
+
     explicit UploadedModel(const LoadedPlan& plan) : meta()
     {
+        instruction_count = plan.instructions.size();
         meta.weight_dtype = plan.weight_dtype;
         meta.shape = plan.shape;
         meta.workers = plan.workers;
@@ -160,6 +163,9 @@ struct Context {
     hipStream_t stream = nullptr;
     DeviceBuffer input, output, scratch, kv, attention_scores, partials, logits, candidates, exchange, tokens, generated, status;
     DeviceBuffer block_trace;
+    DeviceBuffer timeline;
+    bool timeline_enabled = false;
+    size_t instruction_count = 0;
     PinnedBuffer ring;
     size_t ring_cursor = 0;
     uint32_t epoch = 1;
@@ -272,6 +278,7 @@ struct Context {
         b.attention_partials = partials.as<float>();
         b.selection = candidates.as<ti_candidate>();
         b.exchange = exchange.as<uint64_t>();
+        b.timeline = timeline_enabled ? timeline.as<uint64_t>() : nullptr;
         return b;
     }
 
@@ -690,3 +697,35 @@ extern "C" int ti_context_collect(ti_context* context, const ti_ticket* ticket, 
 }
 
 extern "C" void ti_ticket_free(ti_ticket* ticket) { delete ticket; }
+
+extern "C" int ti_context_set_timeline(ti_context* context, int32_t enabled)
+{
+    if (!context)
+        return TI_ERR_INVALID_ARGUMENT;
+    return guarded(TI_ERR_HIP, [&] {
+        auto& c = *context->context;
+        if (enabled && !c.timeline.ptr) {
+            c.timeline = tiles::DeviceBuffer(c.model->instruction_count * 2 * sizeof(uint64_t));
+            if (hipMemset(c.timeline.ptr, 0, c.timeline.bytes) != hipSuccess)
+                throw std::runtime_error("clear timeline");
+        }
+        c.timeline_enabled = enabled != 0;
+    });
+}
+
+extern "C" int ti_context_timeline(ti_context* context, uint64_t* words, size_t capacity, size_t* count)
+{
+    if (!context || !count)
+        return TI_ERR_INVALID_ARGUMENT;
+    return guarded(TI_ERR_HIP, [&] {
+        auto& c = *context->context;
+        *count = c.model->instruction_count;
+        if (!c.timeline.ptr || !words)
+            return;
+        if (hipStreamSynchronize(c.stream) != hipSuccess)
+            throw std::runtime_error("wait for timeline");
+        const size_t n = std::min(capacity, 2 * c.model->instruction_count);
+        if (hipMemcpy(words, c.timeline.ptr, n * sizeof(uint64_t), hipMemcpyDeviceToHost) != hipSuccess)
+            throw std::runtime_error("copy timeline");
+    });
+}

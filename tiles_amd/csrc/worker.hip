@@ -159,6 +159,7 @@ struct Launch {
     float* block_trace;
     float* ffn_trace;
     ti_candidate* selection_out;
+    uint64_t* timeline;
     uint64_t* exchange;
     ExchangeLayout xl;
     uint32_t epoch;
@@ -1081,6 +1082,12 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
             return;
         for (uint32_t index = stream.begin; index < stream.begin + stream.count; ++index) {
             const ti_task_record task = L.instructions[index];
+            if (task.opcode == TI_OP_BARRIER)
+                continue;  // waves synchronize through the exchange words
+            // Optional timeline: 100 MHz device clock (s_memrealtime) at start and end of
+            // every instruction of the launch's last step (diagnostic_context.cu:257-285).
+            if (L.timeline && threadIdx.x == 0)
+                L.timeline[2 * static_cast<size_t>(index)] = __builtin_amdgcn_s_memrealtime();
             switch (task.opcode) {
             case TI_OP_QKV: op_qkv(L, task, step, token, sh); break;
             case TI_OP_ATTENTION_SCORES: op_attention<BF16, kMaxGroup>(L, task, step, sh); break;
@@ -1096,9 +1103,11 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
             }
             case TI_OP_FINAL_RMS_NORM: op_final_rms_norm(L, task, step, sh); break;
             case TI_OP_LOGITS: op_logits(L, task, step, sh); break;
-            default: break;  // barrier and attention_values: no work in this worker
+            default: break;  // attention_values: no work in this worker
             }
             __syncthreads();
+            if (L.timeline && threadIdx.x == 0)
+                L.timeline[2 * static_cast<size_t>(index) + 1] = __builtin_amdgcn_s_memrealtime();
         }
         if (sh.aborted) {
             if (threadIdx.x == 0 && generating && blockIdx.x == 0)
@@ -1156,6 +1165,7 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     L.block_trace = b.block_trace;
     L.ffn_trace = b.ffn_trace;
     L.selection_out = b.selection;
+    L.timeline = b.timeline;
     L.exchange = b.exchange;
     L.xl = exchange_layout(p.shape, p.stack.layers, p.selection_slots);
     L.epoch = b.epoch;
@@ -1380,4 +1390,101 @@ extern "C" int ti_enqueue_widen(void* stream, const void* source, int32_t dtype,
         hipLaunchKernelGGL(widen<false>, dim3(1024), dim3(256), 0, s, source, count, destination);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? TI_OK : hip_fail(e, "widen launch");
+}
+
+// ---------------------------------------------------------------- streaming-read roofline
+
+namespace tiles {
+namespace {
+// Reads `n` 16-byte vectors with nontemporal loads, `unroll` independent loads per lane in
+// flight (the reference's stream_vectors probe, bandwidth_probe.cu:509-549, re-written).
+__global__ void stream_read(const u32x4* __restrict__ src, size_t n, int unroll, unsigned* sink)
+{
+    u32x4 acc = {0, 0, 0, 0};
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (unroll >= 8) {
+        for (; i + 7 * stride < n; i += 8 * stride) {
+            u32x4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                acc ^= v[u];
+        }
+    } else if (unroll >= 4) {
+        for (; i + 3 * stride < n; i += 4 * stride) {
+            u32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                acc ^= v[u];
+        }
+    }
+    for (; i < n; i += stride)
+        acc ^= __builtin_nontemporal_load(src + i);
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u)
+        sink[0] = 1;
+}
+} // namespace
+} // namespace tiles
+
+extern "C" int ti_measure_stream_read(size_t bytes, int32_t repeats, double* best_gbps)
+{
+    using namespace tiles;
+    if (!best_gbps || bytes < (1u << 20) || repeats < 1)
+        return fail(TI_ERR_INVALID_ARGUMENT, "invalid stream measurement request");
+    hipDeviceProp_t props{};
+    hipError_t e = hipGetDeviceProperties(&props, 0);
+    if (e != hipSuccess)
+        return hip_fail(e, "device query");
+    void* buffer = nullptr;
+    unsigned* sink = nullptr;
+    if ((e = hipMalloc(&buffer, bytes)) != hipSuccess)
+        return hip_fail(e, "stream buffer");
+    if ((e = hipMalloc(&sink, 64)) != hipSuccess) {
+        (void)hipFree(buffer);
+        return hip_fail(e, "stream sink");
+    }
+    hipEvent_t a = nullptr, b = nullptr;
+    double best = 0.0;
+    const size_t n = bytes / 16;
+    e = hipMemset(buffer, 1, bytes);
+    if (e == hipSuccess)
+        e = hipEventCreate(&a);
+    if (e == hipSuccess)
+        e = hipEventCreate(&b);
+    const int cus = props.multiProcessorCount;
+    const int grids[] = {1, 2, 4, 8, 16, 32};
+    const int blocks[] = {256, 1024};
+    const int unrolls[] = {1, 4, 8};
+    for (int g = 0; e == hipSuccess && g < 6; ++g)
+        for (int bl : blocks)
+            for (int u : unrolls) {
+                const dim3 grid(static_cast<unsigned>(cus * grids[g]));
+                hipLaunchKernelGGL(stream_read, grid, dim3(bl), 0, 0, static_cast<const u32x4*>(buffer), n, u, sink);
+                (void)hipEventRecord(a, 0);
+                for (int r = 0; r < repeats; ++r)
+                    hipLaunchKernelGGL(stream_read, grid, dim3(bl), 0, 0, static_cast<const u32x4*>(buffer), n, u, sink);
+                (void)hipEventRecord(b, 0);
+                if ((e = hipEventSynchronize(b)) != hipSuccess)
+                    break;
+                float ms = 0.0f;
+                (void)hipEventElapsedTime(&ms, a, b);
+                const double gbps = static_cast<double>(bytes) * repeats / (ms * 1e-3) / 1e9;
+                best = gbps > best ? gbps : best;
+            }
+    if (a)
+        (void)hipEventDestroy(a);
+    if (b)
+        (void)hipEventDestroy(b);
+    (void)hipFree(buffer);
+    (void)hipFree(sink);
+    if (e != hipSuccess)
+        return hip_fail(e, "stream measurement");
+    *best_gbps = best;
+    return TI_OK;
 }

@@ -52,10 +52,11 @@ class Completion(C.Structure):
 STOP_REASONS = {0: "none", 1: "limit", 2: "eos"}
 EXPORTS = ("ti_error_string", "ti_last_error_message", "ti_abi", "ti_fingerprint", "ti_describe_target",
            "ti_exchange_words", "ti_epochs_per_launch", "ti_enqueue_worker", "ti_enqueue_zero_unused_kv",
-           "ti_enqueue_widen", "ti_load_plan", "ti_load_plan_for_target", "ti_plan_free", "ti_plan_inspect_json",
+           "ti_enqueue_widen", "ti_measure_stream_read", "ti_load_plan", "ti_load_plan_for_target", "ti_plan_free", "ti_plan_inspect_json",
            "ti_model_create", "ti_model_free", "ti_context_create", "ti_context_free", "ti_context_prefill",
            "ti_context_decode", "ti_context_generate", "ti_context_reset", "ti_context_ready", "ti_context_wait",
-           "ti_context_diagnostic_sizes", "ti_context_collect", "ti_ticket_free")
+           "ti_context_diagnostic_sizes", "ti_context_collect", "ti_ticket_free", "ti_context_set_timeline",
+           "ti_context_timeline")
 
 _lib = None
 
@@ -77,6 +78,7 @@ def library() -> C.CDLL:
         lib.ti_exchange_words.restype = C.c_size_t
         lib.ti_epochs_per_launch.argtypes = [C.c_int32]
         lib.ti_epochs_per_launch.restype = C.c_uint32
+        lib.ti_measure_stream_read.argtypes = [C.c_size_t, C.c_int32, C.POINTER(C.c_double)]
         lib.ti_load_plan.argtypes = [C.c_char_p, C.c_int32, C.POINTER(P)]
         lib.ti_load_plan_for_target.argtypes = [C.c_char_p, C.POINTER(Target), C.c_int32, C.POINTER(P)]
         lib.ti_plan_free.argtypes = [P]
@@ -99,6 +101,8 @@ def library() -> C.CDLL:
         lib.ti_context_collect.argtypes = [P, P, C.POINTER(C.c_float), C.POINTER(C.c_float), C.POINTER(C.c_float)]
         lib.ti_ticket_free.argtypes = [P]
         lib.ti_ticket_free.restype = None
+        lib.ti_context_set_timeline.argtypes = [P, C.c_int32]
+        lib.ti_context_timeline.argtypes = [P, C.POINTER(C.c_uint64), C.c_size_t, C.POINTER(C.c_size_t)]
         _lib = lib
     return _lib
 
@@ -113,6 +117,13 @@ def describe_target() -> Target:
     target = Target()
     _check(library().ti_describe_target(C.byref(target)))
     return target
+
+
+def measure_stream_read(bytes_: int = 2 << 30, repeats: int = 3) -> float:
+    """Best streaming-read GB/s of the device (the roofline the byte floor is quoted against)."""
+    best = C.c_double()
+    _check(library().ti_measure_stream_read(bytes_, repeats, C.byref(best)))
+    return best.value
 
 
 def target_from_probe(probe: dict) -> Target:
@@ -251,6 +262,18 @@ class SequenceContext:
         _check(library().ti_context_wait(self._handle, ticket._handle, C.byref(done), ids, ticket.requested))
         return Result(list(ids[: done.count]) if ticket.requested else [], done.position,
                       STOP_REASONS.get(done.stop_reason, "none"), done.compute_us)
+
+    def set_timeline(self, enabled: bool) -> None:
+        _check(library().ti_context_set_timeline(self._handle, int(enabled)))
+
+    def timeline(self) -> np.ndarray:
+        """[instructions, 2] device-clock stamps (100 MHz) of the last launch's last step."""
+        count = C.c_size_t()
+        _check(library().ti_context_timeline(self._handle, None, 0, C.byref(count)))
+        words = np.zeros(2 * count.value, dtype=np.uint64)
+        _check(library().ti_context_timeline(self._handle, words.ctypes.data_as(C.POINTER(C.c_uint64)), words.size,
+                                             C.byref(count)))
+        return words.reshape(-1, 2)
 
     def collect(self, ticket: Ticket) -> dict:
         logits = np.zeros(self.logits_size, dtype=np.float32)
