@@ -104,7 +104,8 @@ typedef struct {
     float* attention_partials;
     ti_candidate* selection;
     float* ffn_trace;
-    uint64_t* timeline; /* optional: 2 words per instruction, device clock at start and end (launch.cuh:25-28) */
+    uint64_t* timeline; /* optional: 4 words per instruction (launch.cuh:25-28): device clock at start, first
+                           exchange read, inputs complete, end */
     uint64_t* exchange;
     uint32_t epoch;
 } ti_worker_buffers;
@@ -202,9 +203,11 @@ int ti_context_diagnostic_sizes(const ti_context* context, size_t* logits, size_
 int ti_context_collect(ti_context* context, const ti_ticket* ticket, float* logits, float* kv,
                        float* block_outputs);
 /* Timeline mode (diagnostic_context.cu:257-285, main.cpp --timeline-stack): while enabled, every
- * launch stamps each instruction of its last step with the 100 MHz device clock at start and
- * end.  ti_context_timeline copies 2 words per instruction (plan instruction order) after
- * waiting for the context's queued work; `count` receives the number of instructions. */
+ * launch stamps each instruction of its last step with the 100 MHz device clock at start, when
+ * its first exchange read returned, when its inputs were complete, and at its end (0 where an
+ * instruction read no exchange).  ti_context_timeline copies 4 words per instruction (plan
+ * instruction order) after waiting for the context's queued work; `count` receives the number
+ * of instructions. */
 int ti_context_set_timeline(ti_context* context, int32_t enabled);
 int ti_context_timeline(ti_context* context, uint64_t* words, size_t capacity, size_t* count);
 void ti_ticket_free(ti_ticket* ticket);

@@ -205,43 +205,86 @@ struct Shared {
     int flag;
     int aborted;
     int token;
+    uint64_t mark_read;   // timeline: when the instruction's first exchange read returned
+    uint64_t mark_ready;  // timeline: when its last exchange wait ended
 };
 
 // ---------------------------------------------------------------- exchange polling
 
-// Polls `count` exchange words from `src` (element index = word index) until each carries
-// `epoch`, storing payload-to-float conversions through `sink(index, payload)`.
+// Reads `count` (at most kMaxHidden) exchange words from `src` until each carries `epoch`
+// and hands each payload to `sink(index, payload)`.  Block-wide: every thread must call it.
+// The first read is optimistic (one coherent round trip when the producers are done).  If any
+// word is still missing, only wave 0 keeps polling, one "witness" word every `stride` words
+// (every producer writes a run of at least `stride` words), with a back-off; the block then
+// re-reads what was missing.  Polling the whole vector from every thread of every worker
+// floods the few memory channels that hold it and slows the producers themselves.
 template <typename Sink>
-__device__ __forceinline__ void poll_words(const uint64_t* src, int count, uint32_t epoch, uint64_t* exchange,
-                           const ExchangeLayout& xl, Shared& sh, Sink sink)
+__device__ __forceinline__ void poll_words(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
+                                          const ExchangeLayout& xl, Shared& sh, Sink sink)
 {
-    constexpr int kBatch = 4;
-    for (int base = 0; base < count; base += kBatch * kThreads) {
-        uint64_t w[kBatch];
+    constexpr int kBatch = (kMaxHidden + kThreads - 1) / kThreads;
+    const uint64_t done_word = static_cast<uint64_t>(epoch) << 32;
+    uint64_t w[kBatch];
+    bool ok = true;
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int index = base + k * kThreads + static_cast<int>(threadIdx.x);
-            w[k] = index < count ? coherent_load64(src + index) : (static_cast<uint64_t>(epoch) << 32);
-        }
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int index = base + k * kThreads + static_cast<int>(threadIdx.x);
+    for (int k = 0; k < kBatch; ++k) {
+        const int index = k * kThreads + static_cast<int>(threadIdx.x);
+        w[k] = index < count ? coherent_load64(src + index) : done_word;
+        ok &= static_cast<uint32_t>(w[k] >> 32) == epoch;
+    }
+    const bool all_present = __syncthreads_and(ok);
+    if (threadIdx.x == 0 && sh.mark_read == 0)
+        sh.mark_read = __builtin_amdgcn_s_memrealtime();
+    if (!all_present) {
+        if (threadIdx.x < 64) {
+            const int lane = threadIdx.x;
             uint32_t spins = 0;
-            while (static_cast<uint32_t>(w[k] >> 32) != epoch && !sh.aborted) {
-                __builtin_amdgcn_s_sleep(1);
-                w[k] = coherent_load64(src + index);
-                if ((++spins & 255u) == 0) {
-                    if (coherent_load64(exchange + xl.control) != 0 || spins > kSpinLimit) {
-                        sh.aborted = 1;
-                        coherent_store64(exchange + xl.control, 1);
-                    }
+            while (!sh.aborted) {
+                bool mine = true;
+                for (int j = lane; j * stride < count; j += 64)
+                    mine &= static_cast<uint32_t>(coherent_load64(src + j * stride) >> 32) == epoch;
+                if (lane == 0)
+                    mine &= static_cast<uint32_t>(coherent_load64(src + count - 1) >> 32) == epoch;
+                if (__all(mine))
+                    break;
+                __builtin_amdgcn_s_sleep(2);
+                if ((++spins & 63u) == 0 && lane == 0 &&
+                    (coherent_load64(exchange + xl.control) != 0 || spins > kSpinLimit)) {
+                    sh.aborted = 1;
+                    coherent_store64(exchange + xl.control, 1);
                 }
             }
-            if (index < count)
-                sink(index, static_cast<uint32_t>(w[k]));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int index = k * kThreads + static_cast<int>(threadIdx.x);
+            uint32_t spins = 0;
+            while (static_cast<uint32_t>(w[k] >> 32) != epoch && !sh.aborted) {
+                w[k] = coherent_load64(src + index);
+                if (static_cast<uint32_t>(w[k] >> 32) == epoch)
+                    break;
+                __builtin_amdgcn_s_sleep(2);
+                if ((++spins & 63u) == 0 && (coherent_load64(exchange + xl.control) != 0 || spins > kSpinLimit)) {
+                    sh.aborted = 1;
+                    coherent_store64(exchange + xl.control, 1);
+                }
+            }
         }
     }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+        const int index = k * kThreads + static_cast<int>(threadIdx.x);
+        if (index < count)
+            sink(index, static_cast<uint32_t>(w[k]));
+    }
+    if (threadIdx.x == 0)
+        sh.mark_ready = __builtin_amdgcn_s_memrealtime();
 }
+
+// Witness spacing of an exchange written by row tasks that split `n` rows over `workers`
+// (plan_core.py:275-278: every task gets at least n / workers rows).
+__device__ inline int row_stride(int n, int workers) { return n >= workers ? n / workers : 1; }
 
 template <bool BF16>
 __device__ inline void publish(uint64_t* dst, int index, float rounded, uint32_t epoch)
@@ -268,8 +311,8 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, in
         }
         return;
     }
-    poll_words(L.exchange + L.xl.hidden(layer % 2), d, L.epoch_of(step, layer - 1, kPhaseY), L.exchange, L.xl, sh,
-               [&](int i, uint32_t p) { dst[i] = Num<BF16>::from_payload(p); });
+    poll_words(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
+               L.exchange, L.xl, sh, [&](int i, uint32_t p) { dst[i] = Num<BF16>::from_payload(p); });
 }
 
 // One element of a layer's input, for residual additions.
@@ -323,39 +366,43 @@ __device__ __forceinline__ void rms_norm_lds(float* v, int d, const void* scale,
 
 // ---------------------------------------------------------------- GEMV over rows
 
-// Dot products of rows [r0, r1) of a row-major matrix (row length `cols`, row stride `stride`
-// elements) with the FP32 vector u (LDS).  One group of LR = min(64, vectors per row) lanes
-// owns a row; lanes hold their slice of u in registers.  `prepare` runs once, block-wide,
-// after the first pass's weight loads are issued and before u is read: it polls the inputs
-// and writes u, so weight latency overlaps the wait.  emit(row, dot) runs in the group's lane 0.
-template <bool BF16, int VPL, typename Prepare, typename Emit>
-__device__ __forceinline__ void gemv_rows(const void* matrix, size_t stride, int r0, int r1, int cols, const float* u,
-                          Prepare prepare, Emit emit)
+// Dot products of rows [r0, r1) of NM row-major matrices sharing a shape (row length `cols`,
+// row stride `stride` elements) with the FP32 vector u (LDS).  One group of
+// LR = min(64, vectors per row) lanes owns a row of every matrix; lanes hold their slice of u
+// in registers.  `prepare` runs once, block-wide, after the first pass's weight loads are
+// issued and before u is read: it polls the inputs and writes u, so weight latency overlaps
+// the wait.  emit(row, dots) runs in the group's lane 0 with one dot per matrix.
+template <bool BF16, int VPL, int NM, typename Prepare, typename Emit>
+__device__ __forceinline__ void gemv_rows(const void* const (&matrices)[NM], size_t stride, int r0, int r1, int cols,
+                                         const float* u, Prepare prepare, Emit emit)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
+    constexpr int kLoads = VPL * NM;
     const int nvec = cols / PV;
     const int LR = nvec < 64 ? nvec : 64;
     const int rows_per_wave = 64 / LR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane / LR, col = lane % LR;
     const size_t row_bytes = stride * N::kBytes;
-    const char* base = static_cast<const char*>(matrix);
     const int pass_rows = kWaves * rows_per_wave;
 
     auto row_of = [&](int pass) { return r0 + pass * pass_rows + wave * rows_per_wave + sub; };
     auto issue = [&](int row, u32x4* w) {
         const int safe = row < r1 ? row : r0;
-        const char* p = base + static_cast<size_t>(safe) * row_bytes + static_cast<size_t>(col) * 16;
 #pragma unroll
-        for (int k = 0; k < VPL; ++k)
-            w[k] = load_weights(p + static_cast<size_t>(k) * LR * 16);
+        for (int m = 0; m < NM; ++m) {
+            const char* p = static_cast<const char*>(matrices[m]) + static_cast<size_t>(safe) * row_bytes +
+                            static_cast<size_t>(col) * 16;
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+                w[m * VPL + k] = load_weights(p + static_cast<size_t>(k) * LR * 16);
+        }
     };
 
-    u32x4 w0[VPL];
-    const int first = row_of(0);
+    u32x4 w0[kLoads];
     if (r0 + wave * rows_per_wave < r1)
-        issue(first, w0);
+        issue(row_of(0), w0);
     prepare();
     float ur[VPL][PV];
 #pragma unroll
@@ -365,32 +412,36 @@ __device__ __forceinline__ void gemv_rows(const void* matrix, size_t stride, int
             ur[k][j] = u[(col + k * LR) * PV + j];
 
     auto finish = [&](int row, const u32x4* w) {
-        float acc = 0.0f;
+        float dots[NM];
 #pragma unroll
-        for (int k = 0; k < VPL; ++k)
+        for (int m = 0; m < NM; ++m) {
+            float acc = 0.0f;
 #pragma unroll
-            for (int j = 0; j < PV; ++j)
-                acc += N::elem(w[k], j) * ur[k][j];
-        acc = wave_sum(acc, LR);
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int j = 0; j < PV; ++j)
+                    acc += N::elem(w[m * VPL + k], j) * ur[k][j];
+            dots[m] = wave_sum(acc, LR);
+        }
         if (row < r1 && col == 0)
-            emit(row, acc);
+            emit(row, dots);
     };
 
     if (r0 + wave * rows_per_wave >= r1)
         return;
     int pass = 0;
-    if constexpr (VPL <= 4) {
+    if constexpr (kLoads <= 8) {
         // Two passes in flight: issue pass p + 1 before reducing pass p.
         while (true) {
             const bool more = r0 + (pass + 1) * pass_rows + wave * rows_per_wave < r1;
-            u32x4 w1[VPL];
+            u32x4 w1[kLoads];
             if (more)
                 issue(row_of(pass + 1), w1);
             finish(row_of(pass), w0);
             if (!more)
                 break;
 #pragma unroll
-            for (int k = 0; k < VPL; ++k)
+            for (int k = 0; k < kLoads; ++k)
                 w0[k] = w1[k];
             ++pass;
         }
@@ -405,18 +456,27 @@ __device__ __forceinline__ void gemv_rows(const void* matrix, size_t stride, int
     }
 }
 
-// Runtime vectors-per-lane dispatch (the loader admits 1..16).
-template <bool BF16, typename Prepare, typename Emit>
-__device__ __forceinline__ void gemv(const void* matrix, size_t stride, int r0, int r1, int cols, const float* u, Prepare prepare, Emit emit)
+// Runtime vectors-per-lane dispatch (the loader admits rows of 1..512 16-byte vectors).
+template <bool BF16, int NM, typename Prepare, typename Emit>
+__device__ __forceinline__ void gemv_n(const void* const (&matrices)[NM], size_t stride, int r0, int r1, int cols,
+                                      const float* u, Prepare prepare, Emit emit)
 {
     const int nvec = cols / Num<BF16>::kPerVec;
     const int vpl = nvec <= 64 ? 1 : nvec / 64;
     switch (vpl) {
-    case 1: gemv_rows<BF16, 1>(matrix, stride, r0, r1, cols, u, prepare, emit); break;
-    case 2: gemv_rows<BF16, 2>(matrix, stride, r0, r1, cols, u, prepare, emit); break;
-    case 4: gemv_rows<BF16, 4>(matrix, stride, r0, r1, cols, u, prepare, emit); break;
-    default: gemv_rows<BF16, 8>(matrix, stride, r0, r1, cols, u, prepare, emit); break;
+    case 1: gemv_rows<BF16, 1, NM>(matrices, stride, r0, r1, cols, u, prepare, emit); break;
+    case 2: gemv_rows<BF16, 2, NM>(matrices, stride, r0, r1, cols, u, prepare, emit); break;
+    case 4: gemv_rows<BF16, 4, NM>(matrices, stride, r0, r1, cols, u, prepare, emit); break;
+    default: gemv_rows<BF16, 8, NM>(matrices, stride, r0, r1, cols, u, prepare, emit); break;
     }
+}
+
+template <bool BF16, typename Prepare, typename Emit>
+__device__ __forceinline__ void gemv(const void* matrix, size_t stride, int r0, int r1, int cols, const float* u, Prepare prepare,
+                                    Emit emit)
+{
+    const void* const matrices[1] = {matrix};
+    gemv_n<BF16, 1>(matrices, stride, r0, r1, cols, u, prepare, [&](int row, const float* dots) { emit(row, dots[0]); });
 }
 
 // ---------------------------------------------------------------- operations
@@ -439,21 +499,17 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     };
     auto emit = [&](int row, float dot) {
         const float value = Num<BF16>::round(dot);
-        if (row < d) {
-            publish<BF16>(L.exchange + L.xl.q, row, value, epoch);
-        } else if (row < d + kvw) {
-            publish<BF16>(L.exchange + L.xl.k, row - d, value, epoch);
-        } else {
-            const int i = row - d - kvw;
+        if (row >= d + kvw) {
+            // V rows also go to the cache row of the current position, before publication.
             void* cache = L.cache(layer, L.layout.value);
-            const size_t index = static_cast<size_t>(position) * kvw + i;
+            const size_t index = static_cast<size_t>(position) * kvw + (row - d - kvw);
             if constexpr (BF16)
                 coherent_store16(static_cast<uint16_t*>(cache) + index, static_cast<uint16_t>(float_to_bf16_bits(value)));
             else
                 coherent_storef(static_cast<float*>(cache) + index, value);
             wait_stores();
-            publish<BF16>(L.exchange + L.xl.v, i, value, epoch);
         }
+        publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
     };
     // Rows may span Wq, Wk and Wv; run each matrix's part (they are separate regions).
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
@@ -502,10 +558,13 @@ __device__ inline void rope_pair(const float* src, float* dst, int pair, int hal
 // probabilities rounded to Scalar, P*V, published as the group's attention output.
 // Several chunks: each chunk keeps (max, sum of exp, unnormalized P*V) in FP32; the chunk
 // that finishes last (an atomic count per head group) merges all of them and publishes.
+// Cached K/V rows never change during a token, so the first block of them is loaded before
+// the task waits for this token's Q/K/V.
 template <bool BF16, int MG>
 __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     using N = Num<BF16>;
+    constexpr int PV = N::kPerVec;
     const ti_model_shape& s = L.shape;
     const int position = L.position + step;
     const int chunks = active_chunks(position, s);
@@ -522,29 +581,48 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const int begin = static_cast<int>(static_cast<int64_t>(length) * chunk / chunks);
     const int end = static_cast<int>(static_cast<int64_t>(length) * (chunk + 1) / chunks);
     const int span = end - begin;
-    const uint32_t in_epoch = L.epoch_of(step, layer, kPhaseQKV);
 
-    // Inputs: the group's Q heads, this head's K and V of the current position.
-    float* q_raw = sh.region;                   // [group][dh]
-    float* k_raw = sh.region + group * dh;      // [dh]
-    float* v_cur = sh.vcur;                     // [dh]
-    poll_words(L.exchange + L.xl.q + first_head * dh, group * dh, in_epoch, L.exchange, L.xl, sh,
-               [&](int i, uint32_t p) { q_raw[i] = N::from_payload(p); });
-    poll_words(L.exchange + L.xl.k + kv_head * dh, dh, in_epoch, L.exchange, L.xl, sh,
-               [&](int i, uint32_t p) { k_raw[i] = N::from_payload(p); });
-    poll_words(L.exchange + L.xl.v + kv_head * dh, dh, in_epoch, L.exchange, L.xl, sh,
-               [&](int i, uint32_t p) { v_cur[i] = N::from_payload(p); });
+    const int LRk = dh / PV;                 // lanes per K/V row (power of two, <= 16)
+    const int rows_per_wave = 64 / LRk;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane / LRk, col = lane % LRk;
+    const int block_rows = kWaves * rows_per_wave;
+    void* key_cache = L.cache(layer, L.layout.key);
+    const void* value_cache = L.cache(layer, L.layout.value);
+    const uint32_t layer_kv_bytes = static_cast<uint32_t>(static_cast<size_t>(s.max_context) * kvw * N::kBytes);
+    const __amdgpu_buffer_rsrc_t krsrc = make_rsrc(key_cache, layer_kv_bytes);
+    const __amdgpu_buffer_rsrc_t vrsrc = make_rsrc(value_cache, layer_kv_bytes);
+    auto row_time = [&](int first, int u) { return first + u * block_rows + wave * rows_per_wave + sub; };
+    auto load_rows = [&](__amdgpu_buffer_rsrc_t rsrc, int first, u32x4* raw) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int time = row_time(first, u);
+            const bool cached = time < end && time < position;
+            const uint32_t offset =
+                static_cast<uint32_t>((static_cast<size_t>(cached ? time : 0) * kvw + kv_head * dh + col * PV) * N::kBytes);
+            raw[u] = cached ? coherent_load128(rsrc, offset) : u32x4{0, 0, 0, 0};
+        }
+    };
+    u32x4 kfirst[2], vfirst[2];
+    load_rows(krsrc, begin, kfirst);
+    load_rows(vrsrc, begin, vfirst);
+
+    // This token's Q heads, K and V of the head group: one packed exchange block.
+    const int block = (group + 2) * dh;
+    float* incoming = sh.region;  // [group][dh] Q, [dh] K, [dh] V
+    poll_words(L.exchange + L.xl.qkv + static_cast<size_t>(kv_head) * block, block,
+               row_stride(s.hidden_size + 2 * kvw, L.workers), L.epoch_of(step, layer, kPhaseQKV), L.exchange, L.xl, sh,
+               [&](int i, uint32_t p) { incoming[i] = N::from_payload(p); });
     __syncthreads();
     const int half = dh / 2;
     for (int index = threadIdx.x; index < (group + 1) * half; index += kThreads) {
         const int head = index / half, pair = index - head * half;
         const float angle = static_cast<float>(position) * L.rope[pair];
-        const float* src = head < group ? q_raw + head * dh : k_raw;
-        rope_pair<BF16>(src, sh.rotated + head * dh, pair, half, angle);
+        rope_pair<BF16>(incoming + head * dh, sh.rotated + head * dh, pair, half, angle);
     }
+    for (int index = threadIdx.x; index < dh; index += kThreads)
+        sh.vcur[index] = incoming[(group + 1) * dh + index];
     __syncthreads();
-    void* key_cache = L.cache(layer, L.layout.key);
-    const void* value_cache = L.cache(layer, L.layout.value);
     if (chunk == 0) {
         for (int index = threadIdx.x; index < (group + 1) * dh; index += kThreads) {
             const float value = sh.rotated[index];
@@ -561,14 +639,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     }
 
     // Scores of rows [begin, end): LRk lanes hold one 16-byte slice of a K row each.
-    constexpr int PV = N::kPerVec;
-    const int LRk = dh / PV;                 // lanes per row (power of two, <= 16)
-    const int rows_per_wave = 64 / LRk;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane / LRk, col = lane % LRk;
     const float scale = 1.0f / sqrtf(static_cast<float>(dh));
     const float divisor = sqrtf(static_cast<float>(dh));
-    float* scores = sh.region;               // [group][span] (the inputs above are consumed)
+    float* scores = sh.region;  // [group][span] (the incoming block is consumed)
     float qreg[MG][PV];
 #pragma unroll
     for (int g = 0; g < MG; ++g)
@@ -579,24 +652,19 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 #pragma unroll
     for (int j = 0; j < PV; ++j)
         kcur[j] = sh.rotated[group * dh + col * PV + j];
-    __syncthreads();  // q_raw/k_raw are dead; scores may overwrite the region
-    const uint32_t layer_kv_bytes = static_cast<uint32_t>(static_cast<size_t>(s.max_context) * kvw * N::kBytes);
-    const __amdgpu_buffer_rsrc_t krsrc = make_rsrc(key_cache, layer_kv_bytes);
-    const __amdgpu_buffer_rsrc_t vrsrc = make_rsrc(value_cache, layer_kv_bytes);
-    const int block_rows = kWaves * rows_per_wave;
+    __syncthreads();  // incoming is dead; scores may overwrite the region
     for (int first = begin; first < end; first += 2 * block_rows) {
         u32x4 raw[2];
-        int time[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            time[u] = first + u * block_rows + wave * rows_per_wave + sub;
-            const bool cached = time[u] < end && time[u] < position;
-            const uint32_t offset = static_cast<uint32_t>(((static_cast<size_t>(cached ? time[u] : 0) * kvw) + kv_head * dh + col * PV) * N::kBytes);
-            raw[u] = cached ? coherent_load128(krsrc, offset) : u32x4{0, 0, 0, 0};
+        if (first == begin) {
+            raw[0] = kfirst[0];
+            raw[1] = kfirst[1];
+        } else {
+            load_rows(krsrc, first, raw);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const bool current = time[u] == position;
+            const int time = row_time(first, u);
+            const bool current = time == position;
 #pragma unroll
             for (int g = 0; g < MG; ++g) {
                 float dot = 0.0f;
@@ -604,9 +672,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 for (int j = 0; j < PV; ++j)
                     dot += (current ? kcur[j] : N::elem(raw[u], j)) * qreg[g][j];
                 dot = wave_sum(dot, LRk);
-                if (g < group && col == 0 && time[u] < end) {
+                if (g < group && col == 0 && time < end) {
                     const float rounded = N::round(dot);
-                    scores[g * span + time[u] - begin] = BF16 ? N::round(rounded * scale) : rounded / divisor;
+                    scores[g * span + time - begin] = BF16 ? N::round(rounded * scale) : rounded / divisor;
                 }
             }
         }
@@ -648,25 +716,24 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             acc[g][j] = 0.0f;
     for (int first = begin; first < end; first += 2 * block_rows) {
         u32x4 raw[2];
-        int time[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            time[u] = first + u * block_rows + wave * rows_per_wave + sub;
-            const bool cached = time[u] < end && time[u] < position;
-            const uint32_t offset = static_cast<uint32_t>(((static_cast<size_t>(cached ? time[u] : 0) * kvw) + kv_head * dh + col * PV) * N::kBytes);
-            raw[u] = cached ? coherent_load128(vrsrc, offset) : u32x4{0, 0, 0, 0};
+        if (first == begin) {
+            raw[0] = vfirst[0];
+            raw[1] = vfirst[1];
+        } else {
+            load_rows(vrsrc, first, raw);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            if (time[u] >= end)
+            const int time = row_time(first, u);
+            if (time >= end)
                 continue;
-            const bool current = time[u] == position;
+            const bool current = time == position;
 #pragma unroll
             for (int g = 0; g < MG; ++g) {
-                const float p = g < group ? scores[g * span + time[u] - begin] : 0.0f;
+                const float p = g < group ? scores[g * span + time - begin] : 0.0f;
 #pragma unroll
                 for (int j = 0; j < PV; ++j)
-                    acc[g][j] += p * (current ? v_cur[col * PV + j] : N::elem(raw[u], j));
+                    acc[g][j] += p * (current ? sh.vcur[col * PV + j] : N::elem(raw[u], j));
             }
         }
     }
@@ -705,9 +772,10 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         return;
     }
     // Partial of this chunk: [chunk][head][dh] then statistics [chunk][head][2].
-    float* partial = L.partials + (static_cast<size_t>(chunk) * s.query_heads + first_head) * dh;
-    float* stats = L.partials + static_cast<size_t>(s.attention_chunks) * s.query_heads * dh +
-                   (static_cast<size_t>(chunk) * s.query_heads + first_head) * 2;
+    float* partials = L.partials;
+    float* stats_base = L.partials + static_cast<size_t>(s.attention_chunks) * s.query_heads * dh;
+    float* partial = partials + (static_cast<size_t>(chunk) * s.query_heads + first_head) * dh;
+    float* stats = stats_base + (static_cast<size_t>(chunk) * s.query_heads + first_head) * 2;
     for (int index = threadIdx.x; index < group * dh; index += kThreads)
         coherent_storef(partial + index, out[index]);
     if (threadIdx.x < group) {
@@ -729,10 +797,10 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         const int head = first_head + threadIdx.x;
         float m = -INFINITY;
         for (int c = 0; c < chunks; ++c)
-            m = fmaxf(m, coherent_loadf(L.partials + static_cast<size_t>(s.attention_chunks) * s.query_heads * dh + (static_cast<size_t>(c) * s.query_heads + head) * 2));
+            m = fmaxf(m, coherent_loadf(stats_base + (static_cast<size_t>(c) * s.query_heads + head) * 2));
         float sum = 0.0f;
         for (int c = 0; c < chunks; ++c) {
-            const float* st = L.partials + static_cast<size_t>(s.attention_chunks) * s.query_heads * dh + (static_cast<size_t>(c) * s.query_heads + head) * 2;
+            const float* st = stats_base + (static_cast<size_t>(c) * s.query_heads + head) * 2;
             sum += coherent_loadf(st + 1) * expf(coherent_loadf(st) - m);
         }
         sh.small[2 * kMaxGroup + threadIdx.x] = m;
@@ -745,8 +813,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         const float m = sh.small[2 * kMaxGroup + g];
         float total = 0.0f;
         for (int c = 0; c < chunks; ++c) {
-            const float* st = L.partials + static_cast<size_t>(s.attention_chunks) * s.query_heads * dh + (static_cast<size_t>(c) * s.query_heads + head) * 2;
-            total += coherent_loadf(L.partials + (static_cast<size_t>(c) * s.query_heads + first_head) * dh + index) * expf(coherent_loadf(st) - m);
+            const float* st = stats_base + (static_cast<size_t>(c) * s.query_heads + head) * 2;
+            total += coherent_loadf(partials + (static_cast<size_t>(c) * s.query_heads + first_head) * dh + index) *
+                     expf(coherent_loadf(st) - m);
         }
         out[index] = total / sh.small[3 * kMaxGroup + g];
     }
@@ -768,7 +837,8 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     float* residual = sh.small;  // rows [begin, end)
     auto prepare = [&]() {
-        poll_words(L.exchange + L.xl.attn, d, L.epoch_of(step, layer, kPhaseAttn), L.exchange, L.xl, sh,
+        poll_words(L.exchange + L.xl.attn, d, (L.shape.query_heads / L.shape.kv_heads) * L.shape.head_dim,
+                   L.epoch_of(step, layer, kPhaseAttn), L.exchange, L.xl, sh,
                    [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
         for (int i = begin + static_cast<int>(threadIdx.x); i < end; i += kThreads)
             residual[i - begin] = hidden_element(L, layer, step, token, i, sh);
@@ -800,16 +870,17 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     float* up = sh.region + 2 * rows;       // [rows]
     const void* norm = L.layer_weight(layer, L.layout.ffn_norm);
     auto prepare = [&]() {
-        poll_words(L.exchange + L.xl.r, d, L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
+        poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
                    [&](int i, uint32_t p) { sh.vec[i] = N::from_payload(p); });
         __syncthreads();
         rms_norm_lds<BF16>(sh.vec, d, norm, L.numeric.rms_norm_eps, sh);
     };
-    // Gate rows then up rows, both into LDS, then the product.
-    gemv<BF16>(L.layer_weight(layer, L.layout.Wgate), d, begin, end, d, sh.vec, prepare,
-               [&](int row, float dot) { gate[row - begin] = N::round(dot); });
-    gemv<BF16>(L.layer_weight(layer, L.layout.Wup), d, begin, end, d, sh.vec, []() {},
-               [&](int row, float dot) { up[row - begin] = N::round(dot); });
+    // Gate and up rows in one pass (all their loads issue before the input wait).
+    const void* const gate_up[2] = {L.layer_weight(layer, L.layout.Wgate), L.layer_weight(layer, L.layout.Wup)};
+    gemv_n<BF16, 2>(gate_up, d, begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
+        gate[row - begin] = N::round(dots[0]);
+        up[row - begin] = N::round(dots[1]);
+    });
     __syncthreads();
     for (int i = threadIdx.x; i < rows; i += kThreads) {
         const float g = gate[i];
@@ -947,7 +1018,8 @@ __device__ __forceinline__ void final_normalized(const Launch<BF16>& L, int step
 {
     const int d = L.shape.hidden_size;
     const int layers = L.stack.layers;
-    poll_words(L.exchange + L.xl.hidden(layers % 2), d, L.epoch_of(step, layers - 1, kPhaseY), L.exchange, L.xl, sh,
+    poll_words(L.exchange + L.xl.hidden(layers % 2), d, row_stride(d, L.workers), L.epoch_of(step, layers - 1, kPhaseY),
+               L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
     __syncthreads();
     rms_norm_lds<BF16>(sh.vec, d, L.stack_weight(L.stack.final_norm_offset), L.numeric.rms_norm_eps, sh);
@@ -1084,10 +1156,14 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
             const ti_task_record task = L.instructions[index];
             if (task.opcode == TI_OP_BARRIER)
                 continue;  // waves synchronize through the exchange words
-            // Optional timeline: 100 MHz device clock (s_memrealtime) at start and end of
-            // every instruction of the launch's last step (diagnostic_context.cu:257-285).
-            if (L.timeline && threadIdx.x == 0)
-                L.timeline[2 * static_cast<size_t>(index)] = __builtin_amdgcn_s_memrealtime();
+            // Optional timeline: 100 MHz device clock (s_memrealtime) at the start of every
+            // instruction of the launch's last step, when its first exchange read returned,
+            // when its inputs were complete, and at its end (diagnostic_context.cu:257-285).
+            if (L.timeline && threadIdx.x == 0) {
+                L.timeline[4 * static_cast<size_t>(index)] = __builtin_amdgcn_s_memrealtime();
+                sh.mark_read = 0;
+                sh.mark_ready = 0;
+            }
             switch (task.opcode) {
             case TI_OP_QKV: op_qkv(L, task, step, token, sh); break;
             case TI_OP_ATTENTION_SCORES: op_attention<BF16, kMaxGroup>(L, task, step, sh); break;
@@ -1106,8 +1182,11 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
             default: break;  // attention_values: no work in this worker
             }
             __syncthreads();
-            if (L.timeline && threadIdx.x == 0)
-                L.timeline[2 * static_cast<size_t>(index) + 1] = __builtin_amdgcn_s_memrealtime();
+            if (L.timeline && threadIdx.x == 0) {
+                L.timeline[4 * static_cast<size_t>(index) + 1] = sh.mark_read;
+                L.timeline[4 * static_cast<size_t>(index) + 2] = sh.mark_ready;
+                L.timeline[4 * static_cast<size_t>(index) + 3] = __builtin_amdgcn_s_memrealtime();
+            }
         }
         if (sh.aborted) {
             if (threadIdx.x == 0 && generating && blockIdx.x == 0)

@@ -10,7 +10,7 @@
 
 namespace tiles {
 
-inline constexpr int kThreads = 1024;               // 16 wave64s per worker, one worker per CU
+inline constexpr int kThreads = 512;                // 8 wave64s per worker (2 per SIMD, 256 VGPRs each), one worker per CU
 inline constexpr int kMaxHidden = 4096;             // a task's input vector lives in LDS as FP32
 inline constexpr int kMaxHeadDim = 128;
 inline constexpr int kMaxGroup = 4;                 // query heads per K/V head (registers hold them all)
@@ -22,7 +22,7 @@ inline constexpr int kAttentionSharedBytes = 16384;
 inline constexpr int kRegionFloats = 9216;          // >= max(kThreads * 8, attention scores, P*V reduction)
 inline constexpr uint32_t kSpinLimit = 1u << 20;    // polls before a wait is declared stuck
 inline constexpr const char* kAbi = "tileinfer-decoder-v10";
-inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-flash-attention-v1-b1024";
+inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-flash-attention-v1-b512";
 
 // Exchange phases within one (step, layer); the candidates use layer == layers.
 inline constexpr int kPhaseQKV = 0;
@@ -40,7 +40,7 @@ __host__ __device__ inline uint32_t epochs_per_step(int layers) { return static_
 struct ExchangeLayout {
     size_t control;      // [0]: nonzero once a worker declared a wait stuck
     size_t hidden0, hidden1;  // layer outputs, alternating like the hidden buffers
-    size_t q, k, v;      // unrotated Q and K, V of the current position
+    size_t qkv;          // per K/V head: its group's unrotated Q, then K, then V of the current position
     size_t attn;         // merged attention output
     size_t r;            // attention block output
     size_t ffn;          // FP32 down partials, [ffn_chunks][hidden]
@@ -60,16 +60,26 @@ __host__ __device__ inline ExchangeLayout exchange_layout(const ti_model_shape& 
     x.control = 0;
     x.hidden0 = 8;
     x.hidden1 = x.hidden0 + d;
-    x.q = x.hidden1 + d;
-    x.k = x.q + d;
-    x.v = x.k + kvw;
-    x.attn = x.v + kvw;
+    x.qkv = x.hidden1 + d;
+    x.attn = x.qkv + d + 2 * kvw;
     x.r = x.attn + d;
     x.ffn = x.r + d;
     x.candidates = x.ffn + static_cast<size_t>(s.ffn_chunks) * d;
     x.counters = x.candidates + 2 * static_cast<size_t>(slots > 0 ? slots : 1);
     x.total = x.counters + static_cast<size_t>(layers) * s.kv_heads;
     return x;
+}
+
+// Word of [Q; K; V] projection row `row` in the packed per-head exchange block.
+__host__ __device__ inline int qkv_word(int row, const ti_model_shape& s)
+{
+    const int d = s.hidden_size, dh = s.head_dim, kvw = s.kv_heads * s.head_dim;
+    const int group = s.query_heads / s.kv_heads, block = (group + 2) * dh;
+    if (row < d)
+        return row / (group * dh) * block + row % (group * dh);
+    if (row < d + kvw)
+        return (row - d) / dh * block + group * dh + (row - d) % dh;
+    return (row - d - kvw) / dh * block + (group + 1) * dh + (row - d - kvw) % dh;
 }
 
 // Empty when the compiled worker supports the shape; otherwise the reason.

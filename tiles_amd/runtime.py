@@ -267,13 +267,14 @@ class SequenceContext:
         _check(library().ti_context_set_timeline(self._handle, int(enabled)))
 
     def timeline(self) -> np.ndarray:
-        """[instructions, 2] device-clock stamps (100 MHz) of the last launch's last step."""
+        """[instructions, 4] device-clock stamps (100 MHz) of the last launch's last step: start,
+        first exchange read returned, inputs complete, end."""
         count = C.c_size_t()
         _check(library().ti_context_timeline(self._handle, None, 0, C.byref(count)))
-        words = np.zeros(2 * count.value, dtype=np.uint64)
+        words = np.zeros(4 * count.value, dtype=np.uint64)
         _check(library().ti_context_timeline(self._handle, words.ctypes.data_as(C.POINTER(C.c_uint64)), words.size,
                                              C.byref(count)))
-        return words.reshape(-1, 2)
+        return words.reshape(-1, 4)
 
     def collect(self, ticket: Ticket) -> dict:
         logits = np.zeros(self.logits_size, dtype=np.float32)

@@ -10,8 +10,8 @@ from pathlib import Path
 from .plan import ABI, OPCODES
 
 # The compiled gfx950 worker's constants (tiles_amd/csrc/worker_config.hpp).
-FINGERPRINT = "decoder-gfx950-wave64-exchange-flash-attention-v1-b1024"
-THREADS = 1024
+FINGERPRINT = "decoder-gfx950-wave64-exchange-flash-attention-v1-b512"
+THREADS = 512
 ATTENTION_SHARED_BYTES = 16384
 
 

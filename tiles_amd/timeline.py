@@ -67,11 +67,14 @@ def budget(plan: dict, stamps: np.ndarray, position: int, stream_gbps: float) ->
         opcode_of_wave[task["wave"]] = task["opcode"].rsplit("_", 1)[0]
     starts: dict[int, list[int]] = defaultdict(list)
     ends: dict[int, list[int]] = defaultdict(list)
-    for (worker, wave, task), (start, end) in zip(imap, stamps):
+    last: dict[int, tuple] = {}
+    for (worker, wave, task), (start, read, ready, end) in zip(imap, stamps):
         if task < 0 or start == 0:
             continue
         starts[wave].append(int(start))
         ends[wave].append(int(end))
+        if wave not in last or end > last[wave][3]:
+            last[wave] = (int(start), int(read), int(ready), int(end))
     waves = sorted(ends)
     origin = min(min(starts[w]) for w in waves)
     bytes_ = wave_bytes(plan, position)
@@ -83,8 +86,13 @@ def budget(plan: dict, stamps: np.ndarray, position: int, stream_gbps: float) ->
         share = (end - previous) * TICK_NS / 1e3
         ideal = bytes_.get(w, 0) / (stream_gbps * 1e9) * 1e6
         op = opcode_of_wave[w]
+        s0, r0, q0, e0 = last[w]
         rows.append({"wave": w, "opcode": op, "us": share, "ideal_us": ideal,
-                     "span_us": (end - min(starts[w])) * TICK_NS / 1e3})
+                     "span_us": (end - min(starts[w])) * TICK_NS / 1e3,
+                     # the wave's last-finishing task: start→first read, →inputs ready, →end
+                     "last_task_us": [(r0 - s0) * TICK_NS / 1e3 if r0 else None,
+                                      (q0 - s0) * TICK_NS / 1e3 if q0 else None, (e0 - s0) * TICK_NS / 1e3],
+                     "last_start_after_previous_us": (s0 - previous) * TICK_NS / 1e3})
         by_opcode[op]["us"] += share
         by_opcode[op]["ideal_us"] += ideal
         by_opcode[op]["waves"] += 1
