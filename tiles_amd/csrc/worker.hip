@@ -5,138 +5,34 @@
 // Synchronization.  The reference separates waves with a grid barrier
 // (worker_kernel.cu:105-107,191-192).  On MI355X a flat 256-block barrier costs 4.2 us and a
 // contention-spread one 1.9 us, plus a store-acknowledge and a reload around it, against a
-// token floor of about 344 us over ~83 waves.  This worker therefore synchronizes through an
+// token floor of about 342 us over ~83 waves.  This worker therefore synchronizes through an
 // exchange area of 64-bit words, each holding one element of a wave's output in its low half
 // and the epoch of the token/layer/phase that wrote it in its high half.  A producer stores
 // the word with one device-coherent (sc1) 64-bit store, which is single-copy atomic, and a
-// consumer polls the words it needs with device-coherent loads until every epoch matches:
-// data and "arrived" travel together, so a dependency costs one coherent round trip.
-// Every producer waits for its earlier side-effect stores (the K/V cache rows) to complete
-// (s_waitcnt vmcnt(0)) before publishing, so a consumer that sees an epoch also sees them.
-// The plan's barrier records therefore compile to nothing; the wave order they encode still
-// decides which worker runs which task.
+// consumer reads the words it needs with device-coherent loads until every epoch matches:
+// data and "arrived" travel together.  Every producer waits for its earlier side-effect
+// stores (K/V cache rows, attention partials) to complete (s_waitcnt vmcnt(0)) before
+// publishing, so a consumer that sees an epoch also sees them.  The plan's barrier records
+// compile to nothing; the wave order still decides which worker runs which task.
 //
-// Each operation issues its first weight loads (nontemporal, 16 bytes per lane) before it
-// polls its inputs, so HBM latency overlaps the wait.  Weights are bf16 or fp32 with FP32
-// accumulation; every bf16 rounding point follows the eager-PyTorch contract of the
-// reference (docs/architecture.md:284-312; ops.cuh rounding sites cited per function).
-#include <hip/hip_runtime.h>
-
-#include <cstdint>
-#include <cstdio>
-#include <cstring>
+// Each operation issues its weight loads (nontemporal, 16 bytes per lane, several passes in
+// flight) before it waits for its inputs, so HBM latency overlaps the wait.  The kernel is
+// instantiated per storage type and per number of 16-byte vectors a lane holds of a hidden
+// row (VPL), so each instantiation carries one GEMV shape and stays small in the instruction
+// cache.  Every bf16 rounding point follows the eager-PyTorch contract of the reference
+// (docs/architecture.md:284-312; ops.cuh sites cited per function).
 #include <string>
-#include <type_traits>
+#include <vector>
 
+#include "device_common.hpp"
 #include "tileinfer_amd.h"
 #include "worker_config.hpp"
 
 namespace tiles {
 namespace {
 
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-
 constexpr int kWaves = kThreads / 64;
-
-// ---------------------------------------------------------------- scalar helpers
-
-__device__ inline float bf16_bits_to_float(uint32_t bits) { return __uint_as_float(bits << 16); }
-
-__device__ inline uint32_t float_to_bf16_bits(float value)
-{
-    // Round to nearest even; NaN stays a quiet NaN.
-    const uint32_t u = __float_as_uint(value);
-    if ((u & 0x7fffffffu) > 0x7f800000u)
-        return (u >> 16) | 0x40u;
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
-
-template <bool BF16>
-struct Num {
-    using T = std::conditional_t<BF16, uint16_t, float>;
-    static constexpr int kBytes = BF16 ? 2 : 4;
-    static constexpr int kPerVec = 16 / kBytes;  // elements per 16-byte vector
-    __device__ static float round(float v)
-    {
-        if constexpr (BF16)
-            return bf16_bits_to_float(float_to_bf16_bits(v));
-        else
-            return v;
-    }
-    __device__ static float load(const void* base, size_t index)
-    {
-        if constexpr (BF16)
-            return bf16_bits_to_float(static_cast<const uint16_t*>(base)[index]);
-        else
-            return static_cast<const float*>(base)[index];
-    }
-    __device__ static void store(void* base, size_t index, float v)
-    {
-        if constexpr (BF16)
-            static_cast<uint16_t*>(base)[index] = static_cast<uint16_t>(float_to_bf16_bits(v));
-        else
-            static_cast<float*>(base)[index] = v;
-    }
-    // An element of a 16-byte vector, widened to FP32.
-    __device__ static float elem(const u32x4& v, int j)
-    {
-        if constexpr (BF16)
-            return __uint_as_float((j & 1) ? (v[j >> 1] & 0xffff0000u) : (v[j >> 1] << 16));
-        else
-            return __uint_as_float(v[j]);
-    }
-    // The 32-bit payload of a rounded value in an exchange word.
-    __device__ static uint32_t payload(float rounded)
-    {
-        if constexpr (BF16)
-            return float_to_bf16_bits(rounded);
-        else
-            return __float_as_uint(rounded);
-    }
-    __device__ static float from_payload(uint32_t p)
-    {
-        if constexpr (BF16)
-            return bf16_bits_to_float(p & 0xffffu);
-        else
-            return __uint_as_float(p);
-    }
-};
-
-__device__ inline u32x4 load_weights(const void* p) { return __builtin_nontemporal_load(static_cast<const u32x4*>(p)); }
-
-__device__ inline void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
-
-// Device-coherent 32/64-bit accesses (global_load/store ... sc1).
-__device__ inline uint64_t coherent_load64(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline void coherent_store64(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline float coherent_loadf(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline void coherent_storef(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline uint32_t coherent_load32(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline void coherent_store32(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline void coherent_store16(uint16_t* p, uint16_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-
-// 16-byte device-coherent load of K/V rows through a buffer resource (sc1).
-__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
-}
-__device__ inline u32x4 coherent_load128(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset)
-{
-    return __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 16);
-}
-
-__device__ inline float wave_sum(float v, int width)
-{
-    for (int offset = width >> 1; offset > 0; offset >>= 1)
-        v += __shfl_xor(v, offset);
-    return v;
-}
-__device__ inline float wave_max(float v, int width)
-{
-    for (int offset = width >> 1; offset > 0; offset >>= 1)
-        v = fmaxf(v, __shfl_xor(v, offset));
-    return v;
-}
+constexpr int kDownBatch = 8;  // Wdown^T rows a thread keeps in flight in an FFN task
 
 // ---------------------------------------------------------------- launch record
 
@@ -172,13 +68,13 @@ struct Launch {
     int workers;
 
     __device__ size_t kv_width() const { return static_cast<size_t>(shape.kv_heads) * shape.head_dim; }
-    __device__ const void* layer_weight(int layer, uint32_t offset) const
+    __device__ const char* layer_weight(int layer, uint32_t offset) const
     {
         const size_t element = static_cast<size_t>(stack.layer_weights_offset) +
                                static_cast<size_t>(layer) * stack.layer_weight_stride + offset;
         return static_cast<const char*>(weights) + element * Num<BF16>::kBytes;
     }
-    __device__ const void* stack_weight(size_t element) const
+    __device__ const char* stack_weight(size_t element) const
     {
         return static_cast<const char*>(weights) + element * Num<BF16>::kBytes;
     }
@@ -196,12 +92,16 @@ struct Launch {
 };
 
 struct Shared {
-    float vec[kMaxHidden];          // a task's input vector (normalized), FP32 values of Scalar
-    float region[kRegionFloats];    // scores/probabilities, reductions, FFN product
-    float small[kMaxTaskRows];      // reductions over waves, softmax statistics, residual rows
+    float vec[kMaxHidden];        // a task's input vector, FP32 values of the storage type
+    float region[kRegionFloats];  // scores/probabilities, reductions, FFN gate/up/product
+    float xsave[kMaxHidden];      // the layer input this worker last read, before the norm
+    float rsave[kMaxHidden];      // the attention block output this worker last read
+    float small[kMaxTaskRows];    // reductions over waves, softmax statistics, residual rows
     float rotated[(kMaxGroup + 1) * kMaxHeadDim];
     float vcur[kMaxHeadDim];
     ti_candidate candidates[kWaves];
+    uint32_t xsave_tag;  // epoch_of(step, layer, kPhaseQKV) of xsave's contents, 0 when empty
+    uint32_t rsave_tag;  // epoch_of(step, layer, kPhaseR) of rsave's contents
     int flag;
     int aborted;
     int token;
@@ -210,6 +110,20 @@ struct Shared {
 };
 
 // ---------------------------------------------------------------- exchange polling
+
+// Every 64th spin of a wait checks the shared abort word and the spin limit; a stuck wait
+// sets it so that every worker leaves its loops and the kernel drains.
+__device__ inline bool stuck(uint64_t* exchange, const ExchangeLayout& xl, uint32_t spins, Shared& sh)
+{
+    if (sh.aborted)
+        return true;
+    if ((spins & 63u) == 0 && (coherent_load64(exchange + xl.control) != 0 || spins > kSpinLimit)) {
+        sh.aborted = 1;
+        coherent_store64(exchange + xl.control, 1);
+        return true;
+    }
+    return false;
+}
 
 // Reads `count` (at most kMaxHidden) exchange words from `src` until each carries `epoch`
 // and hands each payload to `sink(index, payload)`.  Block-wide: every thread must call it.
@@ -239,7 +153,7 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
         if (threadIdx.x < 64) {
             const int lane = threadIdx.x;
             uint32_t spins = 0;
-            while (!sh.aborted) {
+            while (true) {
                 bool mine = true;
                 for (int j = lane; j * stride < count; j += 64)
                     mine &= static_cast<uint32_t>(coherent_load64(src + j * stride) >> 32) == epoch;
@@ -248,11 +162,10 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
                 if (__all(mine))
                     break;
                 __builtin_amdgcn_s_sleep(2);
-                if ((++spins & 63u) == 0 && lane == 0 &&
-                    (coherent_load64(exchange + xl.control) != 0 || spins > kSpinLimit)) {
-                    sh.aborted = 1;
-                    coherent_store64(exchange + xl.control, 1);
-                }
+                if (lane == 0)
+                    stuck(exchange, xl, ++spins, sh);
+                if (__any(sh.aborted))
+                    break;
             }
         }
         __syncthreads();
@@ -265,10 +178,7 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
                 if (static_cast<uint32_t>(w[k] >> 32) == epoch)
                     break;
                 __builtin_amdgcn_s_sleep(2);
-                if ((++spins & 63u) == 0 && (coherent_load64(exchange + xl.control) != 0 || spins > kSpinLimit)) {
-                    sh.aborted = 1;
-                    coherent_store64(exchange + xl.control, 1);
-                }
+                stuck(exchange, xl, ++spins, sh);
             }
         }
     }
@@ -282,9 +192,19 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
         sh.mark_ready = __builtin_amdgcn_s_memrealtime();
 }
 
-// Witness spacing of an exchange written by row tasks that split `n` rows over `workers`
-// (plan_core.py:275-278: every task gets at least n / workers rows).
-__device__ inline int row_stride(int n, int workers) { return n >= workers ? n / workers : 1; }
+// One exchange word, waited for by the calling thread alone.
+__device__ inline uint32_t poll_one(const uint64_t* src, uint32_t epoch, uint64_t* exchange, const ExchangeLayout& xl,
+                                    Shared& sh)
+{
+    uint64_t w = coherent_load64(src);
+    uint32_t spins = 0;
+    while (static_cast<uint32_t>(w >> 32) != epoch && !sh.aborted) {
+        __builtin_amdgcn_s_sleep(2);
+        w = coherent_load64(src);
+        stuck(exchange, xl, ++spins, sh);
+    }
+    return static_cast<uint32_t>(w);
+}
 
 template <bool BF16>
 __device__ inline void publish(uint64_t* dst, int index, float rounded, uint32_t epoch)
@@ -292,51 +212,59 @@ __device__ inline void publish(uint64_t* dst, int index, float rounded, uint32_t
     coherent_store64(dst + index, (static_cast<uint64_t>(epoch) << 32) | Num<BF16>::payload(rounded));
 }
 
-// ---------------------------------------------------------------- layer input
+// Witness spacing of an exchange written by row tasks that split `n` rows over `workers`
+// (plan_core.py:275-278: every task gets at least n / workers rows).
+__device__ inline int row_stride(int n, int workers) { return n >= workers ? n / workers : 1; }
 
-// The hidden state a layer reads: the token's embedding row for a stack's first layer, the
-// host-written input of a block package, or the previous layer's exchanged output.
+// ---------------------------------------------------------------- layer input and residuals
+
+// The hidden state a layer reads, into dst (FP32): the token's embedding row for a stack's
+// first layer, the host-written input of a block package, or the previous layer's output.
+// A copy stays in sh.xsave for the layer's residual addition.
 template <bool BF16>
-__device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, int step, ti_token_id token, float* dst, Shared& sh)
+__device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, int step, ti_token_id token, float* dst,
+                                           Shared& sh)
 {
     const int d = L.shape.hidden_size;
     if (layer == 0) {
-        if (L.stack.full_stack) {
-            const void* row = L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) + static_cast<size_t>(token) * d);
-            for (int i = threadIdx.x; i < d; i += kThreads)
-                dst[i] = Num<BF16>::load(row, i);
-        } else {
-            for (int i = threadIdx.x; i < d; i += kThreads)
-                dst[i] = Num<BF16>::load(L.input, i);
-        }
-        return;
+        const void* row = L.stack.full_stack
+                              ? static_cast<const void*>(L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) +
+                                                                        static_cast<size_t>(token) * d))
+                              : L.input;
+        for (int i = threadIdx.x; i < d; i += kThreads)
+            dst[i] = sh.xsave[i] = Num<BF16>::load(row, i);
+    } else {
+        poll_words(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
+                   L.exchange, L.xl, sh, [&](int i, uint32_t p) { dst[i] = sh.xsave[i] = Num<BF16>::from_payload(p); });
     }
-    poll_words(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
-               L.exchange, L.xl, sh, [&](int i, uint32_t p) { dst[i] = Num<BF16>::from_payload(p); });
+    if (threadIdx.x == 0)
+        sh.xsave_tag = L.epoch_of(step, layer, kPhaseQKV);
 }
 
-// One element of a layer's input, for residual additions.
+// Element i of a layer's input (the attention block's residual).
 template <bool BF16>
-__device__ __forceinline__ float hidden_element(const Launch<BF16>& L, int layer, int step, ti_token_id token, int i, Shared& sh)
+__device__ __forceinline__ float input_element(const Launch<BF16>& L, int layer, int step, ti_token_id token, int i,
+                                              Shared& sh)
 {
-    if (layer == 0) {
-        if (L.stack.full_stack)
-            return Num<BF16>::load(L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) + static_cast<size_t>(token) * L.shape.hidden_size), i);
-        return Num<BF16>::load(L.input, i);
-    }
-    const uint64_t* src = L.exchange + L.xl.hidden(layer % 2) + i;
-    const uint32_t epoch = L.epoch_of(step, layer - 1, kPhaseY);
-    uint64_t w = coherent_load64(src);
-    uint32_t spins = 0;
-    while (static_cast<uint32_t>(w >> 32) != epoch && !sh.aborted) {
-        __builtin_amdgcn_s_sleep(1);
-        w = coherent_load64(src);
-        if (++spins > kSpinLimit) {
-            sh.aborted = 1;
-            coherent_store64(L.exchange + L.xl.control, 1);
-        }
-    }
-    return Num<BF16>::from_payload(static_cast<uint32_t>(w));
+    if (sh.xsave_tag == L.epoch_of(step, layer, kPhaseQKV))
+        return sh.xsave[i];
+    if (layer == 0)
+        return L.stack.full_stack
+                   ? Num<BF16>::load(L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) +
+                                                    static_cast<size_t>(token) * L.shape.hidden_size),
+                                     i)
+                   : Num<BF16>::load(L.input, i);
+    return Num<BF16>::from_payload(
+        poll_one(L.exchange + L.xl.hidden(layer % 2) + i, L.epoch_of(step, layer - 1, kPhaseY), L.exchange, L.xl, sh));
+}
+
+// Element i of a layer's attention block output (the FFN's residual).
+template <bool BF16>
+__device__ __forceinline__ float attention_output_element(const Launch<BF16>& L, int layer, int step, int i, Shared& sh)
+{
+    if (sh.rsave_tag == L.epoch_of(step, layer, kPhaseR))
+        return sh.rsave[i];
+    return Num<BF16>::from_payload(poll_one(L.exchange + L.xl.r + i, L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh));
 }
 
 // ---------------------------------------------------------------- RMSNorm (ops.cuh:145-219)
@@ -366,170 +294,142 @@ __device__ __forceinline__ void rms_norm_lds(float* v, int d, const void* scale,
 
 // ---------------------------------------------------------------- GEMV over rows
 
-// Dot products of rows [r0, r1) of NM row-major matrices sharing a shape (row length `cols`,
-// row stride `stride` elements) with the FP32 vector u (LDS).  One group of
-// LR = min(64, vectors per row) lanes owns a row of every matrix; lanes hold their slice of u
-// in registers.  `prepare` runs once, block-wide, after the first pass's weight loads are
-// issued and before u is read: it polls the inputs and writes u, so weight latency overlaps
-// the wait.  emit(row, dots) runs in the group's lane 0 with one dot per matrix.
-template <bool BF16, int VPL, int NM, typename Prepare, typename Emit>
-__device__ __forceinline__ void gemv_rows(const void* const (&matrices)[NM], size_t stride, int r0, int r1, int cols,
-                                         const float* u, Prepare prepare, Emit emit)
+// Rows of a hidden-width matrix are owned by lane groups: LR = min(64, vectors per row) lanes
+// per row, each holding VPL 16-byte vectors of it; a wave pass covers 64 / LR rows.
+template <bool BF16>
+struct RowGeometry {
+    int lr, rows_per_wave, pass_rows, wave, sub, col;
+    __device__ explicit RowGeometry(int cols)
+    {
+        const int nvec = cols / Num<BF16>::kPerVec;
+        lr = nvec < 64 ? nvec : 64;
+        rows_per_wave = 64 / lr;
+        pass_rows = kWaves * rows_per_wave;
+        const int lane = threadIdx.x & 63;
+        wave = threadIdx.x >> 6;
+        sub = lane / lr;
+        col = lane % lr;
+    }
+    __device__ int first_row(int r0, int pass) const { return r0 + pass * pass_rows + wave * rows_per_wave; }
+};
+
+// Dot products of rows [r0, r1) of NM matrices of hidden width with the FP32 vector u (LDS).
+// row_ptr(m, row) is the address of a row of matrix m.  D passes of loads are in flight; all
+// D issue before `prepare`, which runs block-wide, waits for the task's inputs and writes u,
+// so weight latency overlaps the wait.  emit(row, dots) runs in each row group's lane 0 with
+// one dot per matrix.
+template <bool BF16, int VPL, int NM, typename RowPtr, typename Prepare, typename Emit>
+__device__ __forceinline__ void gemv(RowPtr row_ptr, int r0, int r1, int cols, const float* u, Prepare prepare, Emit emit)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
-    constexpr int kLoads = VPL * NM;
-    const int nvec = cols / PV;
-    const int LR = nvec < 64 ? nvec : 64;
-    const int rows_per_wave = 64 / LR;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane / LR, col = lane % LR;
-    const size_t row_bytes = stride * N::kBytes;
-    const int pass_rows = kWaves * rows_per_wave;
-
-    auto row_of = [&](int pass) { return r0 + pass * pass_rows + wave * rows_per_wave + sub; };
-    auto issue = [&](int row, u32x4* w) {
+    constexpr int K = VPL * NM;
+    constexpr int D = K <= 4 ? 4 : (K <= 8 ? 2 : 1);
+    const RowGeometry<BF16> g(cols);
+    auto active = [&](int pass) { return g.first_row(r0, pass) < r1; };
+    auto issue = [&](int pass, u32x4* w) {
+        const int row = g.first_row(r0, pass) + g.sub;
         const int safe = row < r1 ? row : r0;
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-            const char* p = static_cast<const char*>(matrices[m]) + static_cast<size_t>(safe) * row_bytes +
-                            static_cast<size_t>(col) * 16;
+            const char* p = row_ptr(m, safe) + static_cast<size_t>(g.col) * 16;
 #pragma unroll
             for (int k = 0; k < VPL; ++k)
-                w[m * VPL + k] = load_weights(p + static_cast<size_t>(k) * LR * 16);
+                w[m * VPL + k] = load_weights(p + static_cast<size_t>(k) * g.lr * 16);
         }
     };
-
-    u32x4 w0[kLoads];
-    if (r0 + wave * rows_per_wave < r1)
-        issue(row_of(0), w0);
+    u32x4 w[D][K];
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+        if (active(s))
+            issue(s, w[s]);
     prepare();
     float ur[VPL][PV];
 #pragma unroll
     for (int k = 0; k < VPL; ++k)
 #pragma unroll
         for (int j = 0; j < PV; ++j)
-            ur[k][j] = u[(col + k * LR) * PV + j];
-
-    auto finish = [&](int row, const u32x4* w) {
-        float dots[NM];
+            ur[k][j] = u[(g.col + k * g.lr) * PV + j];
+    for (int base = 0; active(base); base += D) {
 #pragma unroll
-        for (int m = 0; m < NM; ++m) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < VPL; ++k)
-#pragma unroll
-                for (int j = 0; j < PV; ++j)
-                    acc += N::elem(w[m * VPL + k], j) * ur[k][j];
-            dots[m] = wave_sum(acc, LR);
-        }
-        if (row < r1 && col == 0)
-            emit(row, dots);
-    };
-
-    if (r0 + wave * rows_per_wave >= r1)
-        return;
-    int pass = 0;
-    if constexpr (kLoads <= 8) {
-        // Two passes in flight: issue pass p + 1 before reducing pass p.
-        while (true) {
-            const bool more = r0 + (pass + 1) * pass_rows + wave * rows_per_wave < r1;
-            u32x4 w1[kLoads];
-            if (more)
-                issue(row_of(pass + 1), w1);
-            finish(row_of(pass), w0);
-            if (!more)
+        for (int s = 0; s < D; ++s) {
+            const int pass = base + s;
+            if (!active(pass))
                 break;
+            float dots[NM];
 #pragma unroll
-            for (int k = 0; k < kLoads; ++k)
-                w0[k] = w1[k];
-            ++pass;
-        }
-    } else {
-        while (true) {
-            finish(row_of(pass), w0);
-            ++pass;
-            if (r0 + pass * pass_rows + wave * rows_per_wave >= r1)
-                break;
-            issue(row_of(pass), w0);
+            for (int m = 0; m < NM; ++m) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                    for (int j = 0; j < PV; ++j)
+                        acc += N::elem(w[s][m * VPL + k], j) * ur[k][j];
+                dots[m] = wave_sum(acc, g.lr);
+            }
+            if (active(pass + D))
+                issue(pass + D, w[s]);
+            const int row = g.first_row(r0, pass) + g.sub;
+            if (row < r1 && g.col == 0)
+                emit(row, dots);
         }
     }
-}
-
-// Runtime vectors-per-lane dispatch (the loader admits rows of 1..512 16-byte vectors).
-template <bool BF16, int NM, typename Prepare, typename Emit>
-__device__ __forceinline__ void gemv_n(const void* const (&matrices)[NM], size_t stride, int r0, int r1, int cols,
-                                      const float* u, Prepare prepare, Emit emit)
-{
-    const int nvec = cols / Num<BF16>::kPerVec;
-    const int vpl = nvec <= 64 ? 1 : nvec / 64;
-    switch (vpl) {
-    case 1: gemv_rows<BF16, 1, NM>(matrices, stride, r0, r1, cols, u, prepare, emit); break;
-    case 2: gemv_rows<BF16, 2, NM>(matrices, stride, r0, r1, cols, u, prepare, emit); break;
-    case 4: gemv_rows<BF16, 4, NM>(matrices, stride, r0, r1, cols, u, prepare, emit); break;
-    default: gemv_rows<BF16, 8, NM>(matrices, stride, r0, r1, cols, u, prepare, emit); break;
-    }
-}
-
-template <bool BF16, typename Prepare, typename Emit>
-__device__ __forceinline__ void gemv(const void* matrix, size_t stride, int r0, int r1, int cols, const float* u, Prepare prepare,
-                                    Emit emit)
-{
-    const void* const matrices[1] = {matrix};
-    gemv_n<BF16, 1>(matrices, stride, r0, r1, cols, u, prepare, [&](int row, const float* dots) { emit(row, dots[0]); });
 }
 
 // ---------------------------------------------------------------- operations
 
-// [Q; K; V] rows of the normalized layer input (ops.cuh:266-289): Q and K round to Scalar and
-// are published unrotated; V rows also go to the cache row of the current position.
-template <bool BF16>
+// [Q; K; V] rows of the normalized layer input (ops.cuh:266-289): Q and K round to the storage
+// type and are published unrotated; V rows also go to the cache row of the current position,
+// and their words are published once those stores completed.
+template <bool BF16, int VPL>
 __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_record& t, int step, ti_token_id token, Shared& sh)
 {
+    using N = Num<BF16>;
     const int d = L.shape.hidden_size;
     const int kvw = static_cast<int>(L.kv_width());
     const int layer = static_cast<int>(t.layer);
     const int position = L.position + step;
+    const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseQKV);
-    const void* norm = L.layer_weight(layer, L.layout.attn_norm);
+    const char* wq = L.layer_weight(layer, L.layout.Wq);
+    const char* wk = L.layer_weight(layer, L.layout.Wk);
+    const char* wv = L.layer_weight(layer, L.layout.Wv);
+    const size_t row_bytes = static_cast<size_t>(d) * N::kBytes;
+    // Rows may span Wq, Wk and Wv, which are separate regions of the layer's weights.
+    auto row_ptr = [&](int, int row) {
+        return row < d         ? wq + static_cast<size_t>(row) * row_bytes
+               : row < d + kvw ? wk + static_cast<size_t>(row - d) * row_bytes
+                               : wv + static_cast<size_t>(row - d - kvw) * row_bytes;
+    };
     auto prepare = [&]() {
         load_hidden(L, layer, step, token, sh.vec, sh);
         __syncthreads();
-        rms_norm_lds<BF16>(sh.vec, d, norm, L.numeric.rms_norm_eps, sh);
+        rms_norm_lds<BF16>(sh.vec, d, L.layer_weight(layer, L.layout.attn_norm), L.numeric.rms_norm_eps, sh);
     };
-    auto emit = [&](int row, float dot) {
-        const float value = Num<BF16>::round(dot);
-        if (row >= d + kvw) {
-            // V rows also go to the cache row of the current position, before publication.
-            void* cache = L.cache(layer, L.layout.value);
-            const size_t index = static_cast<size_t>(position) * kvw + (row - d - kvw);
-            if constexpr (BF16)
-                coherent_store16(static_cast<uint16_t*>(cache) + index, static_cast<uint16_t>(float_to_bf16_bits(value)));
-            else
-                coherent_storef(static_cast<float*>(cache) + index, value);
-            wait_stores();
-        }
-        publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
-    };
-    // Rows may span Wq, Wk and Wv; run each matrix's part (they are separate regions).
-    const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
-    struct Part { uint32_t offset; int first, last, shift; };
-    Part parts[3] = {{L.layout.Wq, 0, d, 0}, {L.layout.Wk, d, d + kvw, d}, {L.layout.Wv, d + kvw, d + 2 * kvw, d + kvw}};
-    bool prepared = false;
-    for (int p = 0; p < 3; ++p) {
-        const int lo = begin > parts[p].first ? begin : parts[p].first;
-        const int hi = end < parts[p].last ? end : parts[p].last;
-        if (lo >= hi)
-            continue;
-        const void* m = L.layer_weight(layer, parts[p].offset);
-        const int shift = parts[p].shift;
-        if (!prepared) {
-            gemv<BF16>(m, d, lo - shift, hi - shift, d, sh.vec, prepare, [&](int row, float dot) { emit(row + shift, dot); });
-            prepared = true;
-        } else {
-            gemv<BF16>(m, d, lo - shift, hi - shift, d, sh.vec, []() {}, [&](int row, float dot) { emit(row + shift, dot); });
-        }
+    float* staged_v = sh.small;  // this task's V rows, published after their cache stores
+    gemv<BF16, VPL, 1>(row_ptr, begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
+        const float value = N::round(dots[0]);
+        if (row < d + kvw)
+            publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
+        else
+            staged_v[row - begin] = value;
+    });
+    const int first_v = begin > d + kvw ? begin : d + kvw;
+    if (end <= first_v)
+        return;
+    __syncthreads();
+    void* cache = L.cache(layer, L.layout.value);
+    for (int row = first_v + static_cast<int>(threadIdx.x); row < end; row += kThreads) {
+        const size_t index = static_cast<size_t>(position) * kvw + (row - d - kvw);
+        if constexpr (BF16)
+            coherent_store16(static_cast<uint16_t*>(cache) + index,
+                             static_cast<uint16_t>(float_to_bf16_bits(staged_v[row - begin])));
+        else
+            coherent_storef(static_cast<float*>(cache) + index, staged_v[row - begin]);
     }
+    wait_stores();
+    for (int row = first_v + static_cast<int>(threadIdx.x); row < end; row += kThreads)
+        publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), staged_v[row - begin], epoch);
 }
 
 __device__ inline int active_chunks(int position, const ti_model_shape& s)
@@ -555,16 +455,17 @@ __device__ inline void rope_pair(const float* src, float* dst, int pair, int hal
 // One K/V head and context chunk of decode attention (ops.cuh:574-673, re-designed):
 // RoPE of the group's query heads and current K; chunk 0 stores rotated K into the cache.
 // One active chunk (a prefix of at most attention_fused_steps): scores, exact softmax,
-// probabilities rounded to Scalar, P*V, published as the group's attention output.
+// probabilities rounded to the storage type, P*V, published as the group's attention output.
 // Several chunks: each chunk keeps (max, sum of exp, unnormalized P*V) in FP32; the chunk
 // that finishes last (an atomic count per head group) merges all of them and publishes.
 // Cached K/V rows never change during a token, so the first block of them is loaded before
 // the task waits for this token's Q/K/V.
-template <bool BF16, int MG>
+template <bool BF16>
 __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
+    constexpr int MG = kMaxGroup;
     const ti_model_shape& s = L.shape;
     const int position = L.position + step;
     const int chunks = active_chunks(position, s);
@@ -582,7 +483,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const int end = static_cast<int>(static_cast<int64_t>(length) * (chunk + 1) / chunks);
     const int span = end - begin;
 
-    const int LRk = dh / PV;                 // lanes per K/V row (power of two, <= 16)
+    const int LRk = dh / PV;  // lanes per K/V row (a power of two <= 16)
     const int rows_per_wave = 64 / LRk;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane / LRk, col = lane % LRk;
@@ -754,21 +655,20 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 for (int j = 0; j < PV; ++j)
                     reduction[(wave * group + g) * dh + col * PV + j] = acc[g][j];
     __syncthreads();
-    float* out = sh.region + kWaves * group * dh;  // [group][dh] FP32 output of this chunk
-    for (int index = threadIdx.x; index < group * dh; index += kThreads) {
-        float total = 0.0f;
+    // group * dh <= kThreads: each thread owns at most one output element.
+    const int mine = threadIdx.x;
+    const bool owner = mine < group * dh;
+    float out = 0.0f;
+    if (owner)
         for (int w = 0; w < kWaves; ++w)
-            total += reduction[w * group * dh + index];
-        out[index] = total;
-    }
-    __syncthreads();
+            out += reduction[w * group * dh + mine];
 
     const uint32_t out_epoch = L.epoch_of(step, layer, kPhaseAttn);
     uint64_t* attn = L.exchange + L.xl.attn + first_head * dh;
     if (fused) {
         wait_stores();  // the K row is in the cache before anyone sees this output
-        for (int index = threadIdx.x; index < group * dh; index += kThreads)
-            publish<BF16>(attn, index, N::round(out[index]), out_epoch);
+        if (owner)
+            publish<BF16>(attn, mine, N::round(out), out_epoch);
         return;
     }
     // Partial of this chunk: [chunk][head][dh] then statistics [chunk][head][2].
@@ -776,8 +676,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     float* stats_base = L.partials + static_cast<size_t>(s.attention_chunks) * s.query_heads * dh;
     float* partial = partials + (static_cast<size_t>(chunk) * s.query_heads + first_head) * dh;
     float* stats = stats_base + (static_cast<size_t>(chunk) * s.query_heads + first_head) * 2;
-    for (int index = threadIdx.x; index < group * dh; index += kThreads)
-        coherent_storef(partial + index, out[index]);
+    if (owner)
+        coherent_storef(partial + mine, out);
     if (threadIdx.x < group) {
         coherent_storef(stats + threadIdx.x * 2, stat_max[threadIdx.x]);
         coherent_storef(stats + threadIdx.x * 2 + 1, stat_sum[threadIdx.x]);
@@ -792,95 +692,137 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     __syncthreads();
     if (!sh.flag)
         return;
-    // Last chunk of this head group: merge every chunk in chunk order.
-    if (threadIdx.x < group) {
-        const int head = first_head + threadIdx.x;
+    // The last chunk of this head group merges every chunk.  Wave g gathers head g's chunk
+    // statistics (one load per lane and chunk, all in flight together) into LDS:
+    // M = max_c max_c', S = sum_c sum_c exp(max_c - M), weight_c = exp(max_c - M).
+    float* weight = sh.region;                   // [chunks][group]
+    float* chunk_sum = sh.region + chunks * group;  // [chunks][group]
+    if (wave < group) {
         float m = -INFINITY;
-        for (int c = 0; c < chunks; ++c)
-            m = fmaxf(m, coherent_loadf(stats_base + (static_cast<size_t>(c) * s.query_heads + head) * 2));
-        float sum = 0.0f;
-        for (int c = 0; c < chunks; ++c) {
-            const float* st = stats_base + (static_cast<size_t>(c) * s.query_heads + head) * 2;
-            sum += coherent_loadf(st + 1) * expf(coherent_loadf(st) - m);
+        for (int c = lane; c < chunks; c += 64) {
+            const float* st = stats_base + (static_cast<size_t>(c) * s.query_heads + first_head + wave) * 2;
+            const float cm = coherent_loadf(st), cs = coherent_loadf(st + 1);
+            weight[c * group + wave] = cm;
+            chunk_sum[c * group + wave] = cs;
+            m = fmaxf(m, cm);
         }
-        sh.small[2 * kMaxGroup + threadIdx.x] = m;
-        sh.small[3 * kMaxGroup + threadIdx.x] = sum;
+        m = wave_max(m, 64);
+        float total = 0.0f;
+        for (int c = lane; c < chunks; c += 64) {
+            const float e = expf(weight[c * group + wave] - m);
+            weight[c * group + wave] = e;
+            total += chunk_sum[c * group + wave] * e;
+        }
+        total = wave_sum(total, 64);
+        if (lane == 0)
+            sh.small[2 * kMaxGroup + wave] = total;
     }
     __syncthreads();
-    for (int index = threadIdx.x; index < group * dh; index += kThreads) {
-        const int g = index / dh;
-        const int head = first_head + g;
-        const float m = sh.small[2 * kMaxGroup + g];
+    if (owner) {
+        const int g = mine / dh;
+        const float* column = partials + static_cast<size_t>(first_head) * dh + mine;
+        const size_t chunk_stride = static_cast<size_t>(s.query_heads) * dh;
         float total = 0.0f;
-        for (int c = 0; c < chunks; ++c) {
-            const float* st = stats_base + (static_cast<size_t>(c) * s.query_heads + head) * 2;
-            total += coherent_loadf(partials + (static_cast<size_t>(c) * s.query_heads + first_head) * dh + index) *
-                     expf(coherent_loadf(st) - m);
+        int c = 0;
+        for (; c + 4 <= chunks; c += 4) {
+            float v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                v[k] = coherent_loadf(column + (c + k) * chunk_stride);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                total += v[k] * weight[(c + k) * group + g];
         }
-        out[index] = total / sh.small[3 * kMaxGroup + g];
+        for (; c < chunks; ++c)
+            total += coherent_loadf(column + c * chunk_stride) * weight[c * group + g];
+        out = total / sh.small[2 * kMaxGroup + g];
     }
     if (threadIdx.x == 0)
         coherent_store64(counter, 0);
     wait_stores();
     __syncthreads();
-    for (int index = threadIdx.x; index < group * dh; index += kThreads)
-        publish<BF16>(attn, index, N::round(out[index]), out_epoch);
+    if (owner)
+        publish<BF16>(attn, mine, N::round(out), out_epoch);
 }
 
 // Wo rows plus the residual (ops.cuh:718-734): r = round(round(Wo a) + x).
-template <bool BF16>
-__device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, const ti_task_record& t, int step, ti_token_id token, Shared& sh)
+template <bool BF16, int VPL>
+__device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, const ti_task_record& t, int step,
+                                                    ti_token_id token, Shared& sh)
 {
+    using N = Num<BF16>;
     const int d = L.shape.hidden_size;
     const int layer = static_cast<int>(t.layer);
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseR);
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     float* residual = sh.small;  // rows [begin, end)
+    const char* wo = L.layer_weight(layer, L.layout.Wo);
+    const size_t row_bytes = static_cast<size_t>(d) * N::kBytes;
     auto prepare = [&]() {
+        for (int i = begin + static_cast<int>(threadIdx.x); i < end; i += kThreads)
+            residual[i - begin] = input_element(L, layer, step, token, i, sh);
         poll_words(L.exchange + L.xl.attn, d, (L.shape.query_heads / L.shape.kv_heads) * L.shape.head_dim,
                    L.epoch_of(step, layer, kPhaseAttn), L.exchange, L.xl, sh,
-                   [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
-        for (int i = begin + static_cast<int>(threadIdx.x); i < end; i += kThreads)
-            residual[i - begin] = hidden_element(L, layer, step, token, i, sh);
+                   [&](int i, uint32_t p) { sh.vec[i] = N::from_payload(p); });
         __syncthreads();
         if (begin == 0)
             for (int i = threadIdx.x; i < d; i += kThreads)
-                Num<BF16>::store(L.scratch, L.layout.attention + i, sh.vec[i]);
+                N::store(L.scratch, L.layout.attention + i, sh.vec[i]);
     };
-    gemv<BF16>(L.layer_weight(layer, L.layout.Wo), d, begin, end, d, sh.vec, prepare, [&](int row, float dot) {
-        const float r = Num<BF16>::round(Num<BF16>::round(dot) + residual[row - begin]);
-        Num<BF16>::store(L.scratch, L.layout.r + row, r);
-        publish<BF16>(L.exchange + L.xl.r, row, r, epoch);
-    });
+    gemv<BF16, VPL, 1>([&](int, int row) { return wo + static_cast<size_t>(row) * row_bytes; }, begin, end, d, sh.vec,
+                       prepare, [&](int row, const float* dots) {
+                           const float r = N::round(N::round(dots[0]) + residual[row - begin]);
+                           N::store(L.scratch, L.layout.r + row, r);
+                           publish<BF16>(L.exchange + L.xl.r, row, r, epoch);
+                       });
 }
 
 // One FFN product chunk (ops.cuh:739-813): z = RMSNorm(r); p = round(round(silu(round(gate)))
 // * round(up)) for rows [begin, end); then the chunk's FP32 down partial over every output,
-// published for the reduce wave.  Wdown is stored transposed, [intermediate, hidden].
-template <bool BF16>
+// published for the reduce wave.  Wdown is stored transposed, [intermediate, hidden]: a thread
+// owns one 16-byte column slice and a residue class of the chunk's rows, and issues the loads
+// of its first kDownBatch rows before the task waits for r.
+template <bool BF16, int VPL>
 __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     using N = Num<BF16>;
+    constexpr int PV = N::kPerVec;
     const int d = L.shape.hidden_size;
     const int layer = static_cast<int>(t.layer);
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     const int rows = end - begin;
-    float* product = sh.region;             // [rows]
-    float* gate = sh.region + rows;         // [rows]
-    float* up = sh.region + 2 * rows;       // [rows]
-    const void* norm = L.layer_weight(layer, L.layout.ffn_norm);
-    auto prepare = [&]() {
-        poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
-                   [&](int i, uint32_t p) { sh.vec[i] = N::from_payload(p); });
-        __syncthreads();
-        rms_norm_lds<BF16>(sh.vec, d, norm, L.numeric.rms_norm_eps, sh);
+    float* product = sh.region;        // [rows]
+    float* gate = sh.region + rows;    // [rows]
+    float* up = sh.region + 2 * rows;  // [rows]
+    const int nvec = d / PV;
+    const int groups = kThreads / nvec;  // >= 1 and exact: the loader bounds hidden_size to powers of two
+    const int col = threadIdx.x % nvec, grp = threadIdx.x / nvec;
+    const size_t row_bytes = static_cast<size_t>(d) * N::kBytes;
+    const char* wdown = L.layer_weight(layer, L.layout.Wdown) + static_cast<size_t>(col) * 16;
+    u32x4 dw[kDownBatch];
+    auto issue_down = [&](int first_k) {
+#pragma unroll
+        for (int k = 0; k < kDownBatch; ++k) {
+            const int i = grp + (first_k + k) * groups;
+            dw[k] = i < rows ? load_weights(wdown + static_cast<size_t>(begin + i) * row_bytes) : u32x4{0, 0, 0, 0};
+        }
     };
-    // Gate and up rows in one pass (all their loads issue before the input wait).
-    const void* const gate_up[2] = {L.layer_weight(layer, L.layout.Wgate), L.layer_weight(layer, L.layout.Wup)};
-    gemv_n<BF16, 2>(gate_up, d, begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
-        gate[row - begin] = N::round(dots[0]);
-        up[row - begin] = N::round(dots[1]);
-    });
+    const char* wgate = L.layer_weight(layer, L.layout.Wgate);
+    const char* wup = L.layer_weight(layer, L.layout.Wup);
+    auto prepare = [&]() {
+        issue_down(0);
+        poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
+                   [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
+        if (threadIdx.x == 0)
+            sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
+        __syncthreads();
+        rms_norm_lds<BF16>(sh.vec, d, L.layer_weight(layer, L.layout.ffn_norm), L.numeric.rms_norm_eps, sh);
+    };
+    gemv<BF16, VPL, 2>([&](int m, int row) { return (m == 0 ? wgate : wup) + static_cast<size_t>(row) * row_bytes; }, begin,
+                       end, d, sh.vec, prepare, [&](int row, const float* dots) {
+                           gate[row - begin] = N::round(dots[0]);
+                           up[row - begin] = N::round(dots[1]);
+                       });
     __syncthreads();
     for (int i = threadIdx.x; i < rows; i += kThreads) {
         const float g = gate[i];
@@ -890,43 +832,28 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
         N::store(L.scratch, L.layout.product + begin + i, p);
     }
     __syncthreads();
-    // Down partial: a thread owns one 16-byte column slice of Wdown^T and a residue class of rows.
-    constexpr int PV = N::kPerVec;
-    const int nvec = d / PV;
-    const int groups = kThreads / nvec;  // >= 1 (the loader bounds hidden_size)
-    const int col = threadIdx.x % nvec, grp = threadIdx.x / nvec;
     float acc[PV];
 #pragma unroll
     for (int j = 0; j < PV; ++j)
         acc[j] = 0.0f;
-    const char* wd = static_cast<const char*>(L.layer_weight(layer, L.layout.Wdown));
-    if (grp < groups) {
-        int i = grp;
-        for (; i + groups < rows; i += 2 * groups) {
-            const u32x4 a = load_weights(wd + (static_cast<size_t>(begin + i) * d + col * PV) * N::kBytes);
-            const u32x4 b = load_weights(wd + (static_cast<size_t>(begin + i + groups) * d + col * PV) * N::kBytes);
-            const float pa = product[i], pb = product[i + groups];
+    const int per_thread = (rows + groups - 1) / groups;
+    for (int first_k = 0; first_k < per_thread; first_k += kDownBatch) {
+        if (first_k > 0)
+            issue_down(first_k);
+#pragma unroll
+        for (int k = 0; k < kDownBatch; ++k) {
+            const int i = grp + (first_k + k) * groups;
+            const float p = i < rows ? product[i] : 0.0f;
 #pragma unroll
             for (int j = 0; j < PV; ++j)
-                acc[j] += N::elem(a, j) * pa;
-#pragma unroll
-            for (int j = 0; j < PV; ++j)
-                acc[j] += N::elem(b, j) * pb;
-        }
-        for (; i < rows; i += groups) {
-            const u32x4 a = load_weights(wd + (static_cast<size_t>(begin + i) * d + col * PV) * N::kBytes);
-            const float pa = product[i];
-#pragma unroll
-            for (int j = 0; j < PV; ++j)
-                acc[j] += N::elem(a, j) * pa;
+                acc[j] += N::elem(dw[k], j) * p;
         }
     }
     __syncthreads();  // product is dead
     float* reduction = sh.region;  // [groups][d]
-    if (grp < groups)
 #pragma unroll
-        for (int j = 0; j < PV; ++j)
-            reduction[grp * d + col * PV + j] = acc[j];
+    for (int j = 0; j < PV; ++j)
+        reduction[grp * d + col * PV + j] = acc[j];
     __syncthreads();
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseFfn);
     uint64_t* partials = L.exchange + L.xl.ffn + static_cast<size_t>(t.chunk) * d;
@@ -939,17 +866,20 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
 }
 
 // y rows: the chunks' FP32 down partials summed, rounded before the residual (ops.cuh:820-838).
+// TPR lanes (a power of two <= 64) sum one row; each lane issues up to kPerLane chunk reads
+// at once and only falls back to waiting when some chunk has not arrived.
 template <bool BF16>
 __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     using N = Num<BF16>;
+    constexpr int kPerLane = 8;
     const ti_model_shape& s = L.shape;
     const int d = s.hidden_size;
     const int layer = static_cast<int>(t.layer);
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     const int rows = end - begin;
     const uint32_t in_epoch = L.epoch_of(step, layer, kPhaseFfn);
-    // TPR lanes (a power of two <= 64) sum one row's chunks.
+    const uint64_t present = static_cast<uint64_t>(in_epoch) << 32;
     int tpr = 64;
     while (tpr > 1 && tpr * rows > kThreads)
         tpr >>= 1;
@@ -958,39 +888,31 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
     const uint64_t* base = L.exchange + L.xl.ffn;
     for (int first = 0; first < rows; first += slots) {
         const int row = begin + first + slot;
+        const bool row_ok = first + slot < rows;
         float total = 0.0f;
-        if (first + slot < rows) {
-            for (int c = lane; c < s.ffn_chunks; c += tpr) {
-                const uint64_t* src = base + static_cast<size_t>(c) * d + row;
-                uint64_t w = coherent_load64(src);
-                uint32_t spins = 0;
-                while (static_cast<uint32_t>(w >> 32) != in_epoch && !sh.aborted) {
-                    __builtin_amdgcn_s_sleep(1);
-                    w = coherent_load64(src);
-                    if (++spins > kSpinLimit) {
-                        sh.aborted = 1;
-                        coherent_store64(L.exchange + L.xl.control, 1);
-                    }
-                }
-                total += __uint_as_float(static_cast<uint32_t>(w));
+        for (int c0 = 0; c0 < s.ffn_chunks; c0 += kPerLane * tpr) {
+            uint64_t w[kPerLane];
+            bool ok = true;
+#pragma unroll
+            for (int k = 0; k < kPerLane; ++k) {
+                const int c = c0 + lane + k * tpr;
+                w[k] = row_ok && c < s.ffn_chunks ? coherent_load64(base + static_cast<size_t>(c) * d + row) : present;
+                ok &= static_cast<uint32_t>(w[k] >> 32) == in_epoch;
             }
+            if (!ok) {
+#pragma unroll
+                for (int k = 0; k < kPerLane; ++k)
+                    if (static_cast<uint32_t>(w[k] >> 32) != in_epoch)
+                        w[k] = present | poll_one(base + static_cast<size_t>(c0 + lane + k * tpr) * d + row, in_epoch,
+                                                  L.exchange, L.xl, sh);
+            }
+#pragma unroll
+            for (int k = 0; k < kPerLane; ++k)
+                total += __uint_as_float(static_cast<uint32_t>(w[k]));  // absent chunks carry +0.0
         }
         total = wave_sum(total, tpr);
-        float r = 0.0f;
-        if (first + slot < rows && lane == 0) {
-            const uint64_t* src = L.exchange + L.xl.r + row;
-            const uint32_t r_epoch = L.epoch_of(step, layer, kPhaseR);
-            uint64_t w = coherent_load64(src);
-            uint32_t spins = 0;
-            while (static_cast<uint32_t>(w >> 32) != r_epoch && !sh.aborted) {
-                __builtin_amdgcn_s_sleep(1);
-                w = coherent_load64(src);
-                if (++spins > kSpinLimit) {
-                    sh.aborted = 1;
-                    coherent_store64(L.exchange + L.xl.control, 1);
-                }
-            }
-            r = N::from_payload(static_cast<uint32_t>(w));
+        if (row_ok && lane == 0) {
+            const float r = attention_output_element(L, layer, step, row, sh);
             const float projected = N::round(total);
             const float y = N::round(projected + r);
             void* hidden = (layer + 1) % 2 == 0 ? L.input : L.output;
@@ -1019,8 +941,7 @@ __device__ __forceinline__ void final_normalized(const Launch<BF16>& L, int step
     const int d = L.shape.hidden_size;
     const int layers = L.stack.layers;
     poll_words(L.exchange + L.xl.hidden(layers % 2), d, row_stride(d, L.workers), L.epoch_of(step, layers - 1, kPhaseY),
-               L.exchange, L.xl, sh,
-               [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
+               L.exchange, L.xl, sh, [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
     __syncthreads();
     rms_norm_lds<BF16>(sh.vec, d, L.stack_weight(L.stack.final_norm_offset), L.numeric.rms_norm_eps, sh);
 }
@@ -1035,21 +956,24 @@ __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const t
 }
 
 // Vocabulary rows [begin, end) of the LM head and their greedy candidate (ops.cuh:851-889):
-// logits round to Scalar, then widen; the largest value wins, the lowest ID among equals,
-// and any non-finite logit makes the candidate kNonFinite.
-template <bool BF16>
+// logits round to the storage type, then widen; the largest value wins, the lowest ID among
+// equals, and any non-finite logit makes the candidate kNonFinite.
+template <bool BF16, int VPL>
 __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     const int d = L.shape.hidden_size;
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     ti_candidate best{-INFINITY, 0x7fffffff};
-    auto prepare = [&]() { final_normalized(L, step, sh); };
-    gemv<BF16>(L.stack_weight(L.stack.lm_head_offset), d, begin, end, d, sh.vec, prepare, [&](int row, float dot) {
-        const float logit = Num<BF16>::round(dot);
-        L.logits[row] = logit;
-        keep_better(best, {logit, isfinite(logit) ? row : TI_NON_FINITE});
-    });
+    const char* head = L.stack_weight(L.stack.lm_head_offset);
+    const size_t row_bytes = static_cast<size_t>(d) * Num<BF16>::kBytes;
+    gemv<BF16, VPL, 1>([&](int, int row) { return head + static_cast<size_t>(row) * row_bytes; }, begin, end, d, sh.vec,
+                       [&]() { final_normalized(L, step, sh); },
+                       [&](int row, const float* dots) {
+                           const float logit = Num<BF16>::round(dots[0]);
+                           L.logits[row] = logit;
+                           keep_better(best, {logit, isfinite(logit) ? row : TI_NON_FINITE});
+                       });
     // Lanes that emitted hold candidates; reduce the wave, then the block.
     for (int offset = 32; offset > 0; offset >>= 1) {
         ti_candidate other{__shfl_xor(best.value, offset), __shfl_xor(best.id, offset)};
@@ -1085,13 +1009,10 @@ __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, S
             if (step > 0) {
                 uint32_t spins = 0;
                 while ((static_cast<uint32_t>(a >> 32) != epoch || static_cast<uint32_t>(b >> 32) != epoch) && !sh.aborted) {
-                    __builtin_amdgcn_s_sleep(1);
+                    __builtin_amdgcn_s_sleep(2);
                     a = coherent_load64(words);
                     b = coherent_load64(words + 1);
-                    if (++spins > kSpinLimit) {
-                        sh.aborted = 1;
-                        coherent_store64(L.exchange + L.xl.control, 1);
-                    }
+                    stuck(L.exchange, L.xl, ++spins, sh);
                 }
             }
             keep_better(best, {__uint_as_float(static_cast<uint32_t>(a)), static_cast<ti_token_id>(static_cast<uint32_t>(b))});
@@ -1108,7 +1029,7 @@ __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, S
 }
 
 template <bool BF16>
-__device__ __forceinline__ void record_choice(const Launch<BF16>& L, int step, ti_token_id token)
+__device__ void record_choice(const Launch<BF16>& L, int step, ti_token_id token)
 {
     int32_t* status = L.selection.status;
     if (token == TI_NON_FINITE) {
@@ -1123,7 +1044,7 @@ __device__ __forceinline__ void record_choice(const Launch<BF16>& L, int step, t
     }
 }
 
-template <bool BF16>
+template <bool BF16, int VPL>
 __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launch)
 {
     __shared__ Shared sh;
@@ -1134,6 +1055,8 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
         record = launch;
         sh.aborted = 0;
         sh.flag = 0;
+        sh.xsave_tag = 0;
+        sh.rsave_tag = 0;
     }
     __syncthreads();
     const Launch<BF16>& L = record;
@@ -1165,11 +1088,11 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
                 sh.mark_ready = 0;
             }
             switch (task.opcode) {
-            case TI_OP_QKV: op_qkv(L, task, step, token, sh); break;
-            case TI_OP_ATTENTION_SCORES: op_attention<BF16, kMaxGroup>(L, task, step, sh); break;
-            case TI_OP_OUTPUT_PROJECTION: op_output_projection(L, task, step, token, sh); break;
-            case TI_OP_FFN: op_ffn(L, task, step, sh); break;
-            case TI_OP_FFN_REDUCE: op_ffn_reduce(L, task, step, sh); break;
+            case TI_OP_QKV: op_qkv<BF16, VPL>(L, task, step, token, sh); break;
+            case TI_OP_ATTENTION_SCORES: op_attention<BF16>(L, task, step, sh); break;
+            case TI_OP_OUTPUT_PROJECTION: op_output_projection<BF16, VPL>(L, task, step, token, sh); break;
+            case TI_OP_FFN: op_ffn<BF16, VPL>(L, task, step, sh); break;
+            case TI_OP_FFN_REDUCE: op_ffn_reduce<BF16>(L, task, step, sh); break;
             case TI_OP_EMBEDDING: {
                 const int d = L.shape.hidden_size;
                 const void* row = L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) + static_cast<size_t>(token) * d);
@@ -1178,8 +1101,8 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
                 break;
             }
             case TI_OP_FINAL_RMS_NORM: op_final_rms_norm(L, task, step, sh); break;
-            case TI_OP_LOGITS: op_logits(L, task, step, sh); break;
-            default: break;  // attention_values: no work in this worker
+            case TI_OP_LOGITS: op_logits<BF16, VPL>(L, task, step, sh); break;
+            default: break;  // attention_values: merged inside the scores tasks
             }
             __syncthreads();
             if (L.timeline && threadIdx.x == 0) {
@@ -1198,31 +1121,9 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
     }
 }
 
-} // namespace
-
 // ---------------------------------------------------------------- host side of the launch
 
-namespace {
-thread_local char g_message[512];
-void set_message(const char* text)
-{
-    std::strncpy(g_message, text, sizeof g_message - 1);
-    g_message[sizeof g_message - 1] = '\0';
-}
-int fail(int code, const char* text)
-{
-    set_message(text);
-    return code;
-}
-int hip_fail(hipError_t e, const char* what)
-{
-    char buffer[400];
-    std::snprintf(buffer, sizeof buffer, "%s: %s", what, hipGetErrorString(e));
-    set_message(buffer);
-    return TI_ERR_HIP;
-}
-
-template <bool BF16>
+template <bool BF16, int VPL>
 int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_worker_buffers& b, int position,
                  ti_token_input token, ti_selection selection)
 {
@@ -1256,21 +1157,36 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     L.selection_slots = p.selection_slots;
     L.workers = p.workers;
     void* args[] = {&L};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decoder_worker<BF16>), dim3(p.workers),
-                                                    dim3(kThreads), args, 0, stream);
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decoder_worker<BF16, VPL>),
+                                                    dim3(p.workers), dim3(kThreads), args, 0, stream);
     if (e != hipSuccess)
         return hip_fail(e, "cooperative worker launch");
     return TI_OK;
 }
+
+// check_shape admits hidden sizes whose rows give 1, 2, 4 or 8 vectors per lane.
+template <bool BF16>
+int launch_vpl(hipStream_t s, const ti_worker_program_view& p, const ti_worker_buffers& b, int position,
+               ti_token_input token, ti_selection selection)
+{
+    switch (hidden_vectors_per_lane(p.shape.hidden_size, Num<BF16>::kBytes)) {
+    case 1: return launch_typed<BF16, 1>(s, p, b, position, token, selection);
+    case 2: return launch_typed<BF16, 2>(s, p, b, position, token, selection);
+    case 4: return launch_typed<BF16, 4>(s, p, b, position, token, selection);
+    case 8: return launch_typed<BF16, 8>(s, p, b, position, token, selection);
+    default: return fail(TI_ERR_INVALID_ARGUMENT, "hidden size unsupported by the compiled worker's 16-byte row lanes");
+    }
+}
 } // namespace
 
-const char* last_message() { return g_message; }
-void set_last_message(const char* text) { set_message(text); }
-
-template <bool BF16>
-const void* worker_function() { return reinterpret_cast<const void*>(&decoder_worker<BF16>); }
-template const void* worker_function<true>();
-template const void* worker_function<false>();
+std::vector<const void*> worker_functions(bool bf16)
+{
+    if (bf16)
+        return {reinterpret_cast<const void*>(&decoder_worker<true, 1>), reinterpret_cast<const void*>(&decoder_worker<true, 2>),
+                reinterpret_cast<const void*>(&decoder_worker<true, 4>), reinterpret_cast<const void*>(&decoder_worker<true, 8>)};
+    return {reinterpret_cast<const void*>(&decoder_worker<false, 1>), reinterpret_cast<const void*>(&decoder_worker<false, 2>),
+            reinterpret_cast<const void*>(&decoder_worker<false, 4>), reinterpret_cast<const void*>(&decoder_worker<false, 8>)};
+}
 
 } // namespace tiles
 
@@ -1286,284 +1202,6 @@ extern "C" int ti_enqueue_worker(void* stream, const ti_worker_program_view* pro
     if (!problem.empty())
         return fail(TI_ERR_INVALID_ARGUMENT, problem.c_str());
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    return program->weight_dtype == TI_DTYPE_BFLOAT16 ? launch_typed<true>(s, *program, *buffers, position, token, selection)
-                                                      : launch_typed<false>(s, *program, *buffers, position, token, selection);
-}
-
-// ---------------------------------------------------------------- diagnostics kernels (snapshot.cu:8-62)
-
-namespace tiles {
-namespace {
-// Zeroes cache rows at and after `prefix` (or the generation's end) in every layer.
-template <bool BF16>
-__global__ void zero_unused_kv(void* kv, size_t count, int layers, int layer_stride, int width, int capacity,
-                               int key_offset, int value_offset, int prefix, const int32_t* status)
-{
-    const int valid = status ? prefix + status[TI_STATUS_COUNT] : prefix;
-    const size_t per_layer = static_cast<size_t>(capacity) * width;
-    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < 2 * per_layer * layers;
-         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
-        const size_t layer = i / (2 * per_layer);
-        const size_t within = i % (2 * per_layer);
-        const size_t table = within / per_layer;  // 0 = K, 1 = V
-        const size_t element = within % per_layer;
-        if (static_cast<int>(element / width) < valid)
-            continue;
-        const size_t index = layer * layer_stride + (table ? value_offset : key_offset) + element;
-        if (index < count)
-            Num<BF16>::store(kv, index, 0.0f);
-    }
-}
-
-template <bool BF16>
-__global__ void widen(const void* source, size_t count, float* destination)
-{
-    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < count;
-         i += static_cast<size_t>(gridDim.x) * blockDim.x)
-        destination[i] = Num<BF16>::load(source, i);
-}
-} // namespace
-
-std::string check_shape(const ti_model_shape& s, int dtype)
-{
-    const int elem = dtype == TI_DTYPE_BFLOAT16 ? 2 : 4;
-    auto power_of_two = [](long v) { return v > 0 && (v & (v - 1)) == 0; };
-    if (s.hidden_size <= 0 || s.hidden_size > kMaxHidden)
-        return "hidden size exceeds the compiled worker's LDS limit";
-    const long hidden_vectors = static_cast<long>(s.hidden_size) * elem / 16;
-    if (static_cast<long>(s.hidden_size) * elem % 16 != 0 || !(power_of_two(hidden_vectors) || hidden_vectors % 64 == 0) ||
-        hidden_vectors > 8 * 64)
-        return "hidden size unsupported by the compiled worker's 16-byte row lanes";
-    if (s.head_dim > kMaxHeadDim || s.head_dim * elem % 16 != 0 || !power_of_two(s.head_dim * elem / 16))
-        return "head_dim unsupported by the compiled worker";
-    if (s.kv_heads <= 0 || s.query_heads % s.kv_heads != 0)
-        return "invalid GQA grouping";
-    const int group = s.query_heads / s.kv_heads;
-    if (group > kMaxGroup || group * s.head_dim > kMaxGroupTimesHeadDim)
-        return "query group exceeds the compiled worker's limits";
-    if (static_cast<long>(s.attention_chunk_steps) * group * elem > kAttentionSharedBytes ||
-        static_cast<long>(s.attention_chunk_steps) * group > kRegionFloats)
-        return "attention chunk exceeds the compiled worker's LDS";
-    if (s.intermediate_size % 2 != 0)
-        return "odd intermediate size";
-    return {};
-}
-
-std::string check_launch_shape(const ti_worker_program_view& p, const ti_worker_buffers& b, int position, int steps)
-{
-    std::string problem = check_shape(p.shape, p.weight_dtype);
-    if (!problem.empty())
-        return problem;
-    if (!p.instructions || !p.streams || !p.weights || !p.rotary_frequencies)
-        return "incomplete program view";
-    if (!b.input || !b.output || !b.scratch || !b.kv || !b.logits || !b.attention_partials || !b.selection || !b.exchange)
-        return "incomplete worker buffers";
-    if (p.workers <= 0 || p.workers > 4096)
-        return "invalid worker count";
-    if (position < 0 || position + steps > p.shape.max_context)
-        return "sequence context capacity reached";
-    if (p.stack.full_stack && p.selection_slots <= 0)
-        return "stack without selection slots";
-    return {};
-}
-} // namespace tiles
-
-extern "C" const char* ti_error_string(int code)
-{
-    switch (code) {
-    case TI_OK: return "success";
-    case TI_ERR_INVALID_ARGUMENT: return "invalid argument";
-    case TI_ERR_HIP: return "HIP runtime error";
-    case TI_ERR_PLAN: return "invalid decoder package";
-    case TI_ERR_RUNTIME: return "runtime error";
-    case TI_ERR_NO_DEVICE: return "no HIP device";
-    default: return "unknown error";
-    }
-}
-
-extern "C" const char* ti_last_error_message(void) { return tiles::last_message(); }
-extern "C" const char* ti_abi(void) { return tiles::kAbi; }
-extern "C" const char* ti_fingerprint(void) { return tiles::kFingerprint; }
-
-extern "C" size_t ti_exchange_words(const ti_model_shape* shape, int32_t layers, int32_t selection_slots)
-{
-    return shape ? tiles::exchange_layout(*shape, layers, selection_slots).total : 0;
-}
-
-extern "C" uint32_t ti_epochs_per_launch(int32_t layers) { return TI_MAX_LAUNCH_STEPS * tiles::epochs_per_step(layers); }
-
-extern "C" int ti_describe_target(ti_target* out)
-{
-    using namespace tiles;
-    if (!out)
-        return fail(TI_ERR_INVALID_ARGUMENT, "null target");
-    std::memset(out, 0, sizeof *out);
-    int count = 0;
-    if (hipGetDeviceCount(&count) != hipSuccess || count < 1)
-        return fail(TI_ERR_NO_DEVICE, "no HIP device");
-    hipDeviceProp_t props{};
-    hipError_t e = hipGetDeviceProperties(&props, 0);
-    if (e != hipSuccess)
-        return hip_fail(e, "device query");
-    std::strncpy(out->name, props.name, sizeof out->name - 1);
-    std::strncpy(out->arch, props.gcnArchName, sizeof out->arch - 1);
-    out->major = props.major;
-    out->minor = props.minor;
-    out->sm_count = props.multiProcessorCount;
-    out->cooperative_launch = props.cooperativeLaunch ? 1 : 0;
-    out->max_threads_per_sm = props.maxThreadsPerMultiProcessor;
-    out->global_memory_bytes = props.totalGlobalMem;
-    out->threads_per_block = kThreads;
-    out->attention_shared_bytes = kAttentionSharedBytes;
-    (void)hipDriverGetVersion(&out->driver_version);
-    (void)hipRuntimeGetVersion(&out->runtime_version);
-    hipFuncAttributes f32{}, bf16{};
-    if ((e = hipFuncGetAttributes(&f32, worker_function<false>())) != hipSuccess)
-        return hip_fail(e, "FP32 worker attributes");
-    if ((e = hipFuncGetAttributes(&bf16, worker_function<true>())) != hipSuccess)
-        return hip_fail(e, "BF16 worker attributes");
-    int f32_occupancy = 0, bf16_occupancy = 0;
-    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&f32_occupancy, worker_function<false>(), kThreads, 0)) != hipSuccess)
-        return hip_fail(e, "FP32 worker occupancy");
-    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&bf16_occupancy, worker_function<true>(), kThreads, 0)) != hipSuccess)
-        return hip_fail(e, "BF16 worker occupancy");
-    out->f32_registers = f32.numRegs;
-    out->f32_shared_bytes = static_cast<int>(f32.sharedSizeBytes);
-    out->f32_active_blocks = f32_occupancy;
-    out->bf16_registers = bf16.numRegs;
-    out->bf16_shared_bytes = static_cast<int>(bf16.sharedSizeBytes);
-    out->bf16_active_blocks = bf16_occupancy;
-    out->active_blocks_per_sm = f32_occupancy < bf16_occupancy ? f32_occupancy : bf16_occupancy;
-    out->registers_per_thread = f32.numRegs > bf16.numRegs ? f32.numRegs : bf16.numRegs;
-    out->static_shared_bytes = static_cast<int>(f32.sharedSizeBytes > bf16.sharedSizeBytes ? f32.sharedSizeBytes : bf16.sharedSizeBytes);
-    return TI_OK;
-}
-
-extern "C" int ti_enqueue_zero_unused_kv(void* stream, void* kv, int32_t dtype, size_t count, int32_t layers,
-                                         int32_t layer_stride, int32_t width, int32_t capacity, int32_t key_offset,
-                                         int32_t value_offset, int32_t prefix, const int32_t* generated_status)
-{
-    using namespace tiles;
-    if (!kv || layers <= 0 || width <= 0 || capacity <= 0)
-        return fail(TI_ERR_INVALID_ARGUMENT, "invalid K/V zeroing request");
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (dtype == TI_DTYPE_BFLOAT16)
-        hipLaunchKernelGGL(zero_unused_kv<true>, dim3(256), dim3(256), 0, s, kv, count, layers, layer_stride, width, capacity,
-                           key_offset, value_offset, prefix, generated_status);
-    else
-        hipLaunchKernelGGL(zero_unused_kv<false>, dim3(256), dim3(256), 0, s, kv, count, layers, layer_stride, width, capacity,
-                           key_offset, value_offset, prefix, generated_status);
-    const hipError_t e = hipGetLastError();
-    return e == hipSuccess ? TI_OK : hip_fail(e, "K/V zeroing launch");
-}
-
-extern "C" int ti_enqueue_widen(void* stream, const void* source, int32_t dtype, size_t count, float* destination)
-{
-    using namespace tiles;
-    if (!source || !destination)
-        return fail(TI_ERR_INVALID_ARGUMENT, "invalid widen request");
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (dtype == TI_DTYPE_BFLOAT16)
-        hipLaunchKernelGGL(widen<true>, dim3(1024), dim3(256), 0, s, source, count, destination);
-    else
-        hipLaunchKernelGGL(widen<false>, dim3(1024), dim3(256), 0, s, source, count, destination);
-    const hipError_t e = hipGetLastError();
-    return e == hipSuccess ? TI_OK : hip_fail(e, "widen launch");
-}
-
-// ---------------------------------------------------------------- streaming-read roofline
-
-namespace tiles {
-namespace {
-// Reads `n` 16-byte vectors with nontemporal loads, `unroll` independent loads per lane in
-// flight (the reference's stream_vectors probe, bandwidth_probe.cu:509-549, re-written).
-__global__ void stream_read(const u32x4* __restrict__ src, size_t n, int unroll, unsigned* sink)
-{
-    u32x4 acc = {0, 0, 0, 0};
-    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
-    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (unroll >= 8) {
-        for (; i + 7 * stride < n; i += 8 * stride) {
-            u32x4 v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                v[u] = __builtin_nontemporal_load(src + i + u * stride);
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                acc ^= v[u];
-        }
-    } else if (unroll >= 4) {
-        for (; i + 3 * stride < n; i += 4 * stride) {
-            u32x4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                v[u] = __builtin_nontemporal_load(src + i + u * stride);
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                acc ^= v[u];
-        }
-    }
-    for (; i < n; i += stride)
-        acc ^= __builtin_nontemporal_load(src + i);
-    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u)
-        sink[0] = 1;
-}
-} // namespace
-} // namespace tiles
-
-extern "C" int ti_measure_stream_read(size_t bytes, int32_t repeats, double* best_gbps)
-{
-    using namespace tiles;
-    if (!best_gbps || bytes < (1u << 20) || repeats < 1)
-        return fail(TI_ERR_INVALID_ARGUMENT, "invalid stream measurement request");
-    hipDeviceProp_t props{};
-    hipError_t e = hipGetDeviceProperties(&props, 0);
-    if (e != hipSuccess)
-        return hip_fail(e, "device query");
-    void* buffer = nullptr;
-    unsigned* sink = nullptr;
-    if ((e = hipMalloc(&buffer, bytes)) != hipSuccess)
-        return hip_fail(e, "stream buffer");
-    if ((e = hipMalloc(&sink, 64)) != hipSuccess) {
-        (void)hipFree(buffer);
-        return hip_fail(e, "stream sink");
-    }
-    hipEvent_t a = nullptr, b = nullptr;
-    double best = 0.0;
-    const size_t n = bytes / 16;
-    e = hipMemset(buffer, 1, bytes);
-    if (e == hipSuccess)
-        e = hipEventCreate(&a);
-    if (e == hipSuccess)
-        e = hipEventCreate(&b);
-    const int cus = props.multiProcessorCount;
-    const int grids[] = {1, 2, 4, 8, 16, 32};
-    const int blocks[] = {256, 1024};
-    const int unrolls[] = {1, 4, 8};
-    for (int g = 0; e == hipSuccess && g < 6; ++g)
-        for (int bl : blocks)
-            for (int u : unrolls) {
-                const dim3 grid(static_cast<unsigned>(cus * grids[g]));
-                hipLaunchKernelGGL(stream_read, grid, dim3(bl), 0, 0, static_cast<const u32x4*>(buffer), n, u, sink);
-                (void)hipEventRecord(a, 0);
-                for (int r = 0; r < repeats; ++r)
-                    hipLaunchKernelGGL(stream_read, grid, dim3(bl), 0, 0, static_cast<const u32x4*>(buffer), n, u, sink);
-                (void)hipEventRecord(b, 0);
-                if ((e = hipEventSynchronize(b)) != hipSuccess)
-                    break;
-                float ms = 0.0f;
-                (void)hipEventElapsedTime(&ms, a, b);
-                const double gbps = static_cast<double>(bytes) * repeats / (ms * 1e-3) / 1e9;
-                best = gbps > best ? gbps : best;
-            }
-    if (a)
-        (void)hipEventDestroy(a);
-    if (b)
-        (void)hipEventDestroy(b);
-    (void)hipFree(buffer);
-    (void)hipFree(sink);
-    if (e != hipSuccess)
-        return hip_fail(e, "stream measurement");
-    *best_gbps = best;
-    return TI_OK;
+    return program->weight_dtype == TI_DTYPE_BFLOAT16 ? launch_vpl<true>(s, *program, *buffers, position, token, selection)
+                                                      : launch_vpl<false>(s, *program, *buffers, position, token, selection);
 }

@@ -5,6 +5,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "tileinfer_amd.h"
 
@@ -81,6 +82,22 @@ __host__ __device__ inline int qkv_word(int row, const ti_model_shape& s)
         return (row - d) / dh * block + group * dh + (row - d) % dh;
     return (row - d - kvw) / dh * block + (group + 1) * dh + (row - d - kvw) % dh;
 }
+
+// 16-byte vectors a lane holds of a hidden-width row: rows of `hidden` elements of `elem`
+// bytes are split over min(64, vectors) lanes.
+__host__ __device__ inline int hidden_vectors_per_lane(int hidden, int elem)
+{
+    const int vectors = hidden * elem / 16;
+    return vectors > 64 ? vectors / 64 : 1;
+}
+
+// Thread-local message of the last failed call (ti_last_error_message).
+const char* last_message();
+void set_last_message(const char* text);
+int fail(int code, const char* text);        // sets the message, returns `code`
+int hip_fail(int hip_error, const char* what);  // "what: <HIP error string>", returns TI_ERR_HIP
+// Every compiled instantiation of the decode worker for one storage type.
+std::vector<const void*> worker_functions(bool bf16);
 
 // Empty when the compiled worker supports the shape; otherwise the reason.
 std::string check_shape(const ti_model_shape& s, int dtype);
