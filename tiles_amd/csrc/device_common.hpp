@@ -11,6 +11,34 @@ namespace tiles {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
+// Device memory as the global address space.  Kernels reach their buffers through pointers
+// held in a launch record, which the compiler cannot prove global; a generic pointer compiles
+// to flat_* instructions, and a flat access also counts against the LDS wait counter, so every
+// later LDS wait would also wait for all outstanding weight loads.  global_* instructions
+// keep the two counters apart.
+#define TILES_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ inline TILES_GLOBAL T* global(T* p)
+{
+    return (TILES_GLOBAL T*)(p);
+}
+
+// A record of 32-bit fields read from device memory (a struct cannot be copied through a
+// global-address-space reference).
+template <typename T>
+__device__ inline T load_record(const T* p)
+{
+    static_assert(sizeof(T) % 4 == 0, "records are made of 32-bit fields");
+    uint32_t words[sizeof(T) / 4];
+    const TILES_GLOBAL uint32_t* src = global(reinterpret_cast<const uint32_t*>(p));
+#pragma unroll
+    for (unsigned i = 0; i < sizeof(T) / 4; ++i)
+        words[i] = src[i];
+    T out;
+    __builtin_memcpy(&out, words, sizeof(T));
+    return out;
+}
+
 __device__ inline float bf16_bits_to_float(uint32_t bits) { return __uint_as_float(bits << 16); }
 
 __device__ inline uint32_t float_to_bf16_bits(float value)
@@ -37,16 +65,16 @@ struct Num {
     __device__ static float load(const void* base, size_t index)
     {
         if constexpr (BF16)
-            return bf16_bits_to_float(static_cast<const uint16_t*>(base)[index]);
+            return bf16_bits_to_float(global(static_cast<const uint16_t*>(base))[index]);
         else
-            return static_cast<const float*>(base)[index];
+            return global(static_cast<const float*>(base))[index];
     }
     __device__ static void store(void* base, size_t index, float v)
     {
         if constexpr (BF16)
-            static_cast<uint16_t*>(base)[index] = static_cast<uint16_t>(float_to_bf16_bits(v));
+            global(static_cast<uint16_t*>(base))[index] = static_cast<uint16_t>(float_to_bf16_bits(v));
         else
-            static_cast<float*>(base)[index] = v;
+            global(static_cast<float*>(base))[index] = v;
     }
     // Element j of a 16-byte vector, widened to FP32.
     __device__ static float elem(const u32x4& v, int j)
@@ -74,17 +102,36 @@ struct Num {
 };
 
 // Weights stream once per token: nontemporal 16-byte loads (global_load_dwordx4 ... nt).
-__device__ inline u32x4 load_weights(const void* p) { return __builtin_nontemporal_load(static_cast<const u32x4*>(p)); }
+__device__ inline u32x4 load_weights(const void* p) { return __builtin_nontemporal_load(global(static_cast<const u32x4*>(p))); }
 
 // Waits until every earlier memory operation of the wave completed (s_waitcnt vmcnt(0)).
 __device__ inline void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Device-coherent accesses: relaxed agent-scope atomics, global_load/store ... sc1.
-__device__ inline uint64_t coherent_load64(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline void coherent_store64(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline float coherent_loadf(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline void coherent_storef(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline void coherent_store16(uint16_t* p, uint16_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline uint64_t coherent_load64(const uint64_t* p)
+{
+    return __hip_atomic_load(global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void coherent_store64(uint64_t* p, uint64_t v)
+{
+    __hip_atomic_store(global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float coherent_loadf(const float* p)
+{
+    return __hip_atomic_load(global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void coherent_storef(float* p, float v)
+{
+    __hip_atomic_store(global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void coherent_store16(uint16_t* p, uint16_t v)
+{
+    __hip_atomic_store(global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t coherent_fetch_add64(uint64_t* p, uint64_t v)
+{
+    return __hip_atomic_fetch_add(global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // 16-byte device-coherent loads of K/V rows through a buffer resource (sc1).
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
@@ -96,18 +143,103 @@ __device__ inline u32x4 coherent_load128(__amdgpu_buffer_rsrc_t rsrc, uint32_t o
     return __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 16);
 }
 
-// Butterfly sum / max over aligned groups of `width` lanes (a power of two <= 64).
-__device__ inline float wave_sum(float v, int width)
+// ---------------------------------------------------------------- cross-lane reductions
+//
+// DPP lane permutations (GFX9 encodings) run at VALU speed; a __shfl_xor is an LDS-pipe
+// permute with its own latency.  Reductions inside 16-lane rows therefore use DPP only.
+inline constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]: lane i <- i ^ 1
+inline constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]: lane i <- i ^ 2
+inline constexpr int kDppRowHalfMirror = 0x141;  // lane i <- 7 - i within each 8 lanes
+inline constexpr int kDppRowMirror = 0x140;    // lane i <- 15 - i within each row
+inline constexpr int kDppRowRor = 0x120;       // + n: lane i <- (i - n) mod 16 within each row
+inline constexpr int kDppRowBcast15 = 0x142;   // lane 15 of each row -> the whole next row
+inline constexpr int kDppRowBcast31 = 0x143;   // lane 31 -> rows 2 and 3
+
+// v from the lane the permutation selects; lanes of rows outside kRowMask read 0.
+template <int kCtrl, int kRowMask = 0xF>
+__device__ inline float dpp(float v)
 {
-    for (int offset = width >> 1; offset > 0; offset >>= 1)
-        v += __shfl_xor(v, offset);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask, 0xF, false));
+}
+
+// Sum over aligned groups of `width` lanes (a power of two <= 64, the same in every lane).
+// The total lands in the group's last lane, and in every lane of the group when width <= 16.
+__device__ inline float group_sum(float v, int width)
+{
+    if (width >= 2)
+        v += dpp<kDppQuadXor1>(v);
+    if (width >= 4)
+        v += dpp<kDppQuadXor2>(v);
+    if (width >= 8)
+        v += dpp<kDppRowHalfMirror>(v);
+    if (width >= 16)
+        v += dpp<kDppRowMirror>(v);
+    if (width >= 32)
+        v += dpp<kDppRowBcast15, 0xA>(v);  // rows 1, 3 += rows 0, 2
+    if (width >= 64)
+        v += dpp<kDppRowBcast31, 0xC>(v);  // row 3 += row 1
     return v;
 }
-__device__ inline float wave_max(float v, int width)
+
+// Maximum with the same lane layout as group_sum.
+__device__ inline float group_max(float v, int width)
 {
-    for (int offset = width >> 1; offset > 0; offset >>= 1)
-        v = fmaxf(v, __shfl_xor(v, offset));
+    if (width >= 2)
+        v = fmaxf(v, dpp<kDppQuadXor1>(v));
+    if (width >= 4)
+        v = fmaxf(v, dpp<kDppQuadXor2>(v));
+    if (width >= 8)
+        v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+    if (width >= 16)
+        v = fmaxf(v, dpp<kDppRowMirror>(v));
+    if (width >= 32) {
+        const float other = dpp<kDppRowBcast15, 0xA>(v);
+        v = (threadIdx.x & 16) ? fmaxf(v, other) : v;
+    }
+    if (width >= 64) {
+        const float other = dpp<kDppRowBcast31, 0xC>(v);
+        v = (threadIdx.x & 32) ? fmaxf(v, other) : v;
+    }
     return v;
+}
+
+// v of lane `lane` (uniform), in every lane.
+__device__ inline float lane_value(float v, int lane)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// For each of N values: the sum over the lanes that share lane % width (width a power of two
+// <= 64, the same in every lane).  Lanes 0 .. width-1 end with their residue class's total.
+// In-row steps rotate by width, 2 width, ... 8 (DPP); the steps across rows are batched
+// permutes, N independent ones per step.
+template <int N>
+__device__ inline void residue_sum(float (&v)[N], int width)
+{
+    if (width <= 1)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowRor + 1>(v[n]);
+    if (width <= 2)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowRor + 2>(v[n]);
+    if (width <= 4)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowRor + 4>(v[n]);
+    if (width <= 8)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowRor + 8>(v[n]);
+    if (width <= 16)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += __shfl_xor(v[n], 16);
+    if (width <= 32)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += __shfl_xor(v[n], 32);
 }
 
 } // namespace tiles

@@ -269,26 +269,48 @@ __device__ __forceinline__ float attention_output_element(const Launch<BF16>& L,
 
 // ---------------------------------------------------------------- RMSNorm (ops.cuh:145-219)
 
+// A norm's scale elements threadIdx.x + k * kThreads, loaded into registers before the task
+// waits for its input (a load issued after the wait would add a full memory latency).
+struct NormScale {
+    float v[kMaxHidden / kThreads];
+};
+
+template <bool BF16>
+__device__ __forceinline__ NormScale load_scale(const void* scale, int d)
+{
+    NormScale s;
+#pragma unroll
+    for (int k = 0; k < kMaxHidden / kThreads; ++k) {
+        const int i = k * kThreads + static_cast<int>(threadIdx.x);
+        s.v[k] = i < d ? Num<BF16>::load(scale, i) : 0.0f;
+    }
+    return s;
+}
+
 // In place: v[i] = round(round(v[i] * inv_rms) * scale[i]) for bf16, v[i] * inv_rms * scale[i]
 // for fp32 (decoder_reference.py:183-187, decoder_stack.py:126-132).  The statistic is FP32.
 template <bool BF16>
-__device__ __forceinline__ void rms_norm_lds(float* v, int d, const void* scale, float eps, Shared& sh)
+__device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& scale, float eps, Shared& sh)
 {
     float sum = 0.0f;
     for (int i = threadIdx.x; i < d; i += kThreads)
         sum += v[i] * v[i];
-    sum = wave_sum(sum, 64);
+    sum = group_sum(sum, 64);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __syncthreads();
-    if (lane == 0)
+    if (lane == 63)
         sh.small[wave] = sum;
     __syncthreads();
     float total = 0.0f;
     for (int w = 0; w < kWaves; ++w)
         total += sh.small[w];
     const float inv = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
-    for (int i = threadIdx.x; i < d; i += kThreads)
-        v[i] = Num<BF16>::round(Num<BF16>::round(v[i] * inv) * Num<BF16>::load(scale, i));
+#pragma unroll
+    for (int k = 0; k < kMaxHidden / kThreads; ++k) {
+        const int i = k * kThreads + static_cast<int>(threadIdx.x);
+        if (i < d)
+            v[i] = Num<BF16>::round(Num<BF16>::round(v[i] * inv) * scale.v[k]);
+    }
     __syncthreads();
 }
 
@@ -316,8 +338,8 @@ struct RowGeometry {
 // Dot products of rows [r0, r1) of NM matrices of hidden width with the FP32 vector u (LDS).
 // row_ptr(m, row) is the address of a row of matrix m.  D passes of loads are in flight; all
 // D issue before `prepare`, which runs block-wide, waits for the task's inputs and writes u,
-// so weight latency overlaps the wait.  emit(row, dots) runs in each row group's lane 0 with
-// one dot per matrix.
+// so weight latency overlaps the wait.  emit(row, dots) runs in each row group's last lane
+// with one dot per matrix.
 template <bool BF16, int VPL, int NM, typename RowPtr, typename Prepare, typename Emit>
 __device__ __forceinline__ void gemv(RowPtr row_ptr, int r0, int r1, int cols, const float* u, Prepare prepare, Emit emit)
 {
@@ -365,12 +387,12 @@ __device__ __forceinline__ void gemv(RowPtr row_ptr, int r0, int r1, int cols, c
 #pragma unroll
                     for (int j = 0; j < PV; ++j)
                         acc += N::elem(w[s][m * VPL + k], j) * ur[k][j];
-                dots[m] = wave_sum(acc, g.lr);
+                dots[m] = group_sum(acc, g.lr);
             }
             if (active(pass + D))
                 issue(pass + D, w[s]);
             const int row = g.first_row(r0, pass) + g.sub;
-            if (row < r1 && g.col == 0)
+            if (row < r1 && g.col == g.lr - 1)
                 emit(row, dots);
         }
     }
@@ -401,10 +423,11 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
                : row < d + kvw ? wk + static_cast<size_t>(row - d) * row_bytes
                                : wv + static_cast<size_t>(row - d - kvw) * row_bytes;
     };
+    const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.attn_norm), d);
     auto prepare = [&]() {
         load_hidden(L, layer, step, token, sh.vec, sh);
         __syncthreads();
-        rms_norm_lds<BF16>(sh.vec, d, L.layer_weight(layer, L.layout.attn_norm), L.numeric.rms_norm_eps, sh);
+        rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
     };
     float* staged_v = sh.small;  // this task's V rows, published after their cache stores
     gemv<BF16, VPL, 1>(row_ptr, begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
@@ -518,7 +541,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const int half = dh / 2;
     for (int index = threadIdx.x; index < (group + 1) * half; index += kThreads) {
         const int head = index / half, pair = index - head * half;
-        const float angle = static_cast<float>(position) * L.rope[pair];
+        const float angle = static_cast<float>(position) * global(L.rope)[pair];
         rope_pair<BF16>(incoming + head * dh, sh.rotated + head * dh, pair, half, angle);
     }
     for (int index = threadIdx.x; index < dh; index += kThreads)
@@ -572,8 +595,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 #pragma unroll
                 for (int j = 0; j < PV; ++j)
                     dot += (current ? kcur[j] : N::elem(raw[u], j)) * qreg[g][j];
-                dot = wave_sum(dot, LRk);
-                if (g < group && col == 0 && time < end) {
+                dot = group_sum(dot, LRk);
+                if (g < group && col == LRk - 1 && time < end) {
                     const float rounded = N::round(dot);
                     scores[g * span + time - begin] = BF16 ? N::round(rounded * scale) : rounded / divisor;
                 }
@@ -589,12 +612,12 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         float m = -INFINITY;
         for (int i = lane; i < span; i += 64)
             m = fmaxf(m, scores[wave * span + i]);
-        m = wave_max(m, 64);
+        m = lane_value(group_max(m, 64), 63);
         float sum = 0.0f;
         for (int i = lane; i < span; i += 64)
             sum += expf(scores[wave * span + i] - m);
-        sum = wave_sum(sum, 64);
-        if (lane == 0) {
+        sum = group_sum(sum, 64);
+        if (lane == 63) {
             stat_max[wave] = m;
             stat_sum[wave] = sum;
         }
@@ -609,12 +632,10 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     __syncthreads();
 
     // P*V over rows [begin, end): each lane accumulates its slice for every head.
-    float acc[MG][PV];
+    float acc[MG * PV];
 #pragma unroll
-    for (int g = 0; g < MG; ++g)
-#pragma unroll
-        for (int j = 0; j < PV; ++j)
-            acc[g][j] = 0.0f;
+    for (int n = 0; n < MG * PV; ++n)
+        acc[n] = 0.0f;
     for (int first = begin; first < end; first += 2 * block_rows) {
         u32x4 raw[2];
         if (first == begin) {
@@ -634,17 +655,12 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 const float p = g < group ? scores[g * span + time - begin] : 0.0f;
 #pragma unroll
                 for (int j = 0; j < PV; ++j)
-                    acc[g][j] += p * (current ? sh.vcur[col * PV + j] : N::elem(raw[u], j));
+                    acc[g * PV + j] += p * (current ? sh.vcur[col * PV + j] : N::elem(raw[u], j));
             }
         }
     }
     // Reduce over the rows a wave holds (lanes with equal col), then over waves.
-#pragma unroll
-    for (int g = 0; g < MG; ++g)
-#pragma unroll
-        for (int j = 0; j < PV; ++j)
-            for (int offset = LRk; offset < 64; offset <<= 1)
-                acc[g][j] += __shfl_xor(acc[g][j], offset);
+    residue_sum(acc, LRk);
     __syncthreads();  // probabilities are dead
     float* reduction = sh.region;  // [wave][group][dh]
     if (sub == 0)
@@ -653,7 +669,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             if (g < group)
 #pragma unroll
                 for (int j = 0; j < PV; ++j)
-                    reduction[(wave * group + g) * dh + col * PV + j] = acc[g][j];
+                    reduction[(wave * group + g) * dh + col * PV + j] = acc[g * PV + j];
     __syncthreads();
     // group * dh <= kThreads: each thread owns at most one output element.
     const int mine = threadIdx.x;
@@ -686,7 +702,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     __syncthreads();
     uint64_t* counter = L.exchange + L.xl.counters + layer * s.kv_heads + kv_head;
     if (threadIdx.x == 0) {
-        const uint64_t before = __hip_atomic_fetch_add(counter, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t before = coherent_fetch_add64(counter, 1ull);
         sh.flag = before == static_cast<uint64_t>(chunks - 1);
     }
     __syncthreads();
@@ -706,15 +722,15 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             chunk_sum[c * group + wave] = cs;
             m = fmaxf(m, cm);
         }
-        m = wave_max(m, 64);
+        m = lane_value(group_max(m, 64), 63);
         float total = 0.0f;
         for (int c = lane; c < chunks; c += 64) {
             const float e = expf(weight[c * group + wave] - m);
             weight[c * group + wave] = e;
             total += chunk_sum[c * group + wave] * e;
         }
-        total = wave_sum(total, 64);
-        if (lane == 0)
+        total = group_sum(total, 64);
+        if (lane == 63)
             sh.small[2 * kMaxGroup + wave] = total;
     }
     __syncthreads();
@@ -809,6 +825,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     };
     const char* wgate = L.layer_weight(layer, L.layout.Wgate);
     const char* wup = L.layer_weight(layer, L.layout.Wup);
+    const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.ffn_norm), d);
     auto prepare = [&]() {
         issue_down(0);
         poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
@@ -816,7 +833,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
         if (threadIdx.x == 0)
             sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
         __syncthreads();
-        rms_norm_lds<BF16>(sh.vec, d, L.layer_weight(layer, L.layout.ffn_norm), L.numeric.rms_norm_eps, sh);
+        rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
     };
     gemv<BF16, VPL, 2>([&](int m, int row) { return (m == 0 ? wgate : wup) + static_cast<size_t>(row) * row_bytes; }, begin,
                        end, d, sh.vec, prepare, [&](int row, const float* dots) {
@@ -910,17 +927,17 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
             for (int k = 0; k < kPerLane; ++k)
                 total += __uint_as_float(static_cast<uint32_t>(w[k]));  // absent chunks carry +0.0
         }
-        total = wave_sum(total, tpr);
-        if (row_ok && lane == 0) {
+        total = group_sum(total, tpr);
+        if (row_ok && lane == tpr - 1) {
             const float r = attention_output_element(L, layer, step, row, sh);
             const float projected = N::round(total);
             const float y = N::round(projected + r);
             void* hidden = (layer + 1) % 2 == 0 ? L.input : L.output;
             N::store(hidden, row, y);
             if (L.block_trace)
-                L.block_trace[static_cast<size_t>(layer) * d + row] = y;
+                global(L.block_trace)[static_cast<size_t>(layer) * d + row] = y;
             if (L.ffn_trace)
-                L.ffn_trace[row] = projected;
+                global(L.ffn_trace)[row] = projected;
             publish<BF16>(L.exchange + L.xl.hidden((layer + 1) % 2), row, y, L.epoch_of(step, layer, kPhaseY));
         }
     }
@@ -936,20 +953,20 @@ __device__ inline void keep_better(ti_candidate& best, ti_candidate other)
 
 // Final norm of the last layer's output into sh.vec (decoder_stack.py:126-132).
 template <bool BF16>
-__device__ __forceinline__ void final_normalized(const Launch<BF16>& L, int step, Shared& sh)
+__device__ __forceinline__ void final_normalized(const Launch<BF16>& L, int step, const NormScale& scale, Shared& sh)
 {
     const int d = L.shape.hidden_size;
     const int layers = L.stack.layers;
     poll_words(L.exchange + L.xl.hidden(layers % 2), d, row_stride(d, L.workers), L.epoch_of(step, layers - 1, kPhaseY),
                L.exchange, L.xl, sh, [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
     __syncthreads();
-    rms_norm_lds<BF16>(sh.vec, d, L.stack_weight(L.stack.final_norm_offset), L.numeric.rms_norm_eps, sh);
+    rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
 }
 
 template <bool BF16>
 __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
-    final_normalized(L, step, sh);
+    final_normalized(L, step, load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), L.shape.hidden_size), sh);
     void* hidden = (L.stack.layers + 1) % 2 == 0 ? L.input : L.output;
     for (int i = static_cast<int>(t.begin) + threadIdx.x; i < static_cast<int>(t.end); i += kThreads)
         Num<BF16>::store(hidden, i, sh.vec[i]);
@@ -967,11 +984,12 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     ti_candidate best{-INFINITY, 0x7fffffff};
     const char* head = L.stack_weight(L.stack.lm_head_offset);
     const size_t row_bytes = static_cast<size_t>(d) * Num<BF16>::kBytes;
+    const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
     gemv<BF16, VPL, 1>([&](int, int row) { return head + static_cast<size_t>(row) * row_bytes; }, begin, end, d, sh.vec,
-                       [&]() { final_normalized(L, step, sh); },
+                       [&]() { final_normalized(L, step, scale, sh); },
                        [&](int row, const float* dots) {
                            const float logit = Num<BF16>::round(dots[0]);
-                           L.logits[row] = logit;
+                           global(L.logits)[row] = logit;
                            keep_better(best, {logit, isfinite(logit) ? row : TI_NON_FINITE});
                        });
     // Lanes that emitted hold candidates; reduce the wave, then the block.
@@ -986,7 +1004,8 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
         ti_candidate result = sh.candidates[0];
         for (int w = 1; w < kWaves; ++w)
             keep_better(result, sh.candidates[w]);
-        L.selection_out[t.chunk] = result;
+        global(&L.selection_out[t.chunk].value)[0] = result.value;
+        global(&L.selection_out[t.chunk].id)[0] = result.id;
         const uint32_t epoch = L.epoch_of(step, L.stack.layers, kPhaseCandidate);
         uint64_t* slot = L.exchange + L.xl.candidates + 2 * static_cast<size_t>(t.chunk);
         coherent_store64(slot, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(result.value));
@@ -1031,13 +1050,13 @@ __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, S
 template <bool BF16>
 __device__ void record_choice(const Launch<BF16>& L, int step, ti_token_id token)
 {
-    int32_t* status = L.selection.status;
+    TILES_GLOBAL int32_t* status = global(L.selection.status);
     if (token == TI_NON_FINITE) {
         status[TI_STATUS_ERROR] = TI_DEVICE_NON_FINITE;
     } else if (token < 0 || token >= L.stack.vocab_size) {
         status[TI_STATUS_ERROR] = TI_DEVICE_TOKEN_RANGE;
     } else {
-        L.selection.generated[L.selection.first + step] = token;
+        global(L.selection.generated)[L.selection.first + step] = token;
         status[TI_STATUS_COUNT] = L.selection.first + step + 1;
         if (token == L.selection.eos_id)
             status[TI_STATUS_EOS] = 1;
@@ -1061,9 +1080,9 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
     __syncthreads();
     const Launch<BF16>& L = record;
     const bool generating = L.selection.generated != nullptr;
-    if (generating && (L.selection.status[TI_STATUS_EOS] != 0 || L.selection.status[TI_STATUS_ERROR] != 0))
+    if (generating && (global(L.selection.status)[TI_STATUS_EOS] != 0 || global(L.selection.status)[TI_STATUS_ERROR] != 0))
         return;
-    const ti_worker_task_range stream = L.streams[blockIdx.x];
+    const ti_worker_task_range stream = load_record(L.streams + blockIdx.x);
     for (int step = 0; step < L.steps; ++step) {
         ti_token_id token = L.token_id;
         if (generating) {
@@ -1071,19 +1090,19 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
             if (blockIdx.x == 0 && threadIdx.x == 0)
                 record_choice(L, step, token);
         } else if (L.device_tokens != nullptr) {
-            token = L.device_tokens[step];
+            token = global(L.device_tokens)[step];
         }
         if (L.stack.full_stack && (token < 0 || token >= L.stack.vocab_size))
             return;
         for (uint32_t index = stream.begin; index < stream.begin + stream.count; ++index) {
-            const ti_task_record task = L.instructions[index];
+            const ti_task_record task = load_record(L.instructions + index);
             if (task.opcode == TI_OP_BARRIER)
                 continue;  // waves synchronize through the exchange words
             // Optional timeline: 100 MHz device clock (s_memrealtime) at the start of every
             // instruction of the launch's last step, when its first exchange read returned,
             // when its inputs were complete, and at its end (diagnostic_context.cu:257-285).
             if (L.timeline && threadIdx.x == 0) {
-                L.timeline[4 * static_cast<size_t>(index)] = __builtin_amdgcn_s_memrealtime();
+                global(L.timeline)[4 * static_cast<size_t>(index)] = __builtin_amdgcn_s_memrealtime();
                 sh.mark_read = 0;
                 sh.mark_ready = 0;
             }
@@ -1106,14 +1125,14 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
             }
             __syncthreads();
             if (L.timeline && threadIdx.x == 0) {
-                L.timeline[4 * static_cast<size_t>(index) + 1] = sh.mark_read;
-                L.timeline[4 * static_cast<size_t>(index) + 2] = sh.mark_ready;
-                L.timeline[4 * static_cast<size_t>(index) + 3] = __builtin_amdgcn_s_memrealtime();
+                global(L.timeline)[4 * static_cast<size_t>(index) + 1] = sh.mark_read;
+                global(L.timeline)[4 * static_cast<size_t>(index) + 2] = sh.mark_ready;
+                global(L.timeline)[4 * static_cast<size_t>(index) + 3] = __builtin_amdgcn_s_memrealtime();
             }
         }
         if (sh.aborted) {
             if (threadIdx.x == 0 && generating && blockIdx.x == 0)
-                L.selection.status[TI_STATUS_ERROR] = TI_DEVICE_SYNC_TIMEOUT;
+                global(L.selection.status)[TI_STATUS_ERROR] = TI_DEVICE_SYNC_TIMEOUT;
             return;
         }
         if (generating && token == L.selection.eos_id)
