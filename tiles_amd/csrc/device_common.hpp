@@ -101,8 +101,33 @@ struct Num {
     }
 };
 
-// Weights stream once per token: nontemporal 16-byte loads (global_load_dwordx4 ... nt).
-__device__ inline u32x4 load_weights(const void* p) { return __builtin_nontemporal_load(global(static_cast<const u32x4*>(p))); }
+// Two bf16 values in one register, element 0 in the low half.  Exact for values that are
+// already bf16 (rounded FP32 values of a bf16 computation).
+__device__ inline uint32_t pack_bf16(float lo, float hi)
+{
+    return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+}
+
+// c + a.lo * b.lo + a.hi * b.hi for packed bf16 pairs, accumulated in FP32 (v_dot2_f32_bf16).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ inline float dot2_bf16(uint32_t a, uint32_t b, float c)
+{
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// Weights stream once per token: nontemporal 16-byte loads through a buffer resource whose
+// range ends at kBufferOutside.  An offset at or past it reads zeros without a memory access
+// (the hardware range check), so a lane with no row to load issues the same instruction with
+// that offset instead of branching around it.
+inline constexpr uint32_t kBufferOutside = 0x80000000u;
+__device__ inline __amdgpu_buffer_rsrc_t weight_rsrc(const void* base)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, kBufferOutside, 0x00020000);
+}
+__device__ inline u32x4 load_weights(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 2 /* nt */);
+}
 
 // Waits until every earlier memory operation of the wave completed (s_waitcnt vmcnt(0)).
 __device__ inline void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
@@ -181,6 +206,25 @@ __device__ inline float group_sum(float v, int width)
     return v;
 }
 
+// group_sum for a width known at compile time.
+template <int W>
+__device__ inline float group_sum(float v)
+{
+    if constexpr (W >= 2)
+        v += dpp<kDppQuadXor1>(v);
+    if constexpr (W >= 4)
+        v += dpp<kDppQuadXor2>(v);
+    if constexpr (W >= 8)
+        v += dpp<kDppRowHalfMirror>(v);
+    if constexpr (W >= 16)
+        v += dpp<kDppRowMirror>(v);
+    if constexpr (W >= 32)
+        v += dpp<kDppRowBcast15, 0xA>(v);
+    if constexpr (W >= 64)
+        v += dpp<kDppRowBcast31, 0xC>(v);
+    return v;
+}
+
 // Maximum with the same lane layout as group_sum.
 __device__ inline float group_max(float v, int width)
 {
@@ -207,6 +251,36 @@ __device__ inline float group_max(float v, int width)
 __device__ inline float lane_value(float v, int lane)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// residue_sum for a width known at compile time.
+template <int W, int N>
+__device__ inline void residue_sum(float (&v)[N])
+{
+    if constexpr (W <= 1)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowRor + 1>(v[n]);
+    if constexpr (W <= 2)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowRor + 2>(v[n]);
+    if constexpr (W <= 4)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowRor + 4>(v[n]);
+    if constexpr (W <= 8)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowRor + 8>(v[n]);
+    if constexpr (W <= 16)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += __shfl_xor(v[n], 16);
+    if constexpr (W <= 32)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += __shfl_xor(v[n], 32);
 }
 
 // For each of N values: the sum over the lanes that share lane % width (width a power of two

@@ -88,6 +88,8 @@ std::string check_shape(const ti_model_shape& s, int dtype)
         return "hidden size unsupported by the compiled worker's 16-byte row lanes";
     if (s.head_dim > kMaxHeadDim || s.head_dim * elem % 16 != 0 || !power_of_two(s.head_dim * elem / 16))
         return "head_dim unsupported by the compiled worker";
+    if (!worker_compiled(dtype, hidden_vectors_per_lane(s.hidden_size, elem), head_vectors(s.head_dim, elem)))
+        return "no compiled worker for this hidden size and head_dim";
     if (s.kv_heads <= 0 || s.query_heads % s.kv_heads != 0)
         return "invalid GQA grouping";
     const int group = s.query_heads / s.kv_heads;
@@ -118,6 +120,11 @@ std::string check_launch_shape(const ti_worker_program_view& p, const ti_worker_
         return "sequence context capacity reached";
     if (p.stack.full_stack && p.selection_slots <= 0)
         return "stack without selection slots";
+    // Weight loads address one layer's weights, and the LM head, with 32-bit buffer offsets.
+    const uint64_t elem = p.weight_dtype == TI_DTYPE_BFLOAT16 ? 2 : 4;
+    if (static_cast<uint64_t>(p.stack.layer_weight_stride) * elem >= kBufferRange ||
+        static_cast<uint64_t>(p.stack.vocab_size) * p.shape.hidden_size * elem >= kBufferRange)
+        return "weight region exceeds the worker's 2 GiB buffer addressing";
     return {};
 }
 } // namespace tiles
@@ -175,7 +182,7 @@ extern "C" int ti_describe_target(ti_target* out)
     struct Summary { int registers = 0, shared = 0, active = 1 << 30; };
     Summary summary[2];
     for (int bf16 = 0; bf16 < 2; ++bf16)
-        for (const void* f : worker_functions(bf16 != 0)) {
+        for (const void* f : bf16 ? worker_functions_bf16() : worker_functions_f32()) {
             hipFuncAttributes attributes{};
             int active = 0;
             if ((e = hipFuncGetAttributes(&attributes, f)) != hipSuccess)
@@ -328,3 +335,18 @@ extern "C" int ti_measure_stream_read(size_t bytes, int32_t repeats, double* bes
     return TI_OK;
 }
 
+extern "C" int ti_enqueue_worker(void* stream, const ti_worker_program_view* program, const ti_worker_buffers* buffers,
+                                 int32_t position, ti_token_input token, ti_selection selection)
+{
+    using namespace tiles;
+    if (!program || !buffers)
+        return fail(TI_ERR_INVALID_ARGUMENT, "null program or buffers");
+    if (token.steps < 1 || token.steps > TI_MAX_LAUNCH_STEPS)
+        return fail(TI_ERR_INVALID_ARGUMENT, "invalid worker launch step count");
+    const std::string problem = check_launch_shape(*program, *buffers, position, token.steps);
+    if (!problem.empty())
+        return fail(TI_ERR_INVALID_ARGUMENT, problem.c_str());
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    return program->weight_dtype == TI_DTYPE_BFLOAT16 ? launch_worker_bf16(s, *program, *buffers, position, token, selection)
+                                                      : launch_worker_f32(s, *program, *buffers, position, token, selection);
+}

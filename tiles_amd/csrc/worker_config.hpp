@@ -7,6 +7,8 @@
 #include <string>
 #include <vector>
 
+#include <hip/hip_runtime.h>
+
 #include "tileinfer_amd.h"
 
 namespace tiles {
@@ -17,10 +19,12 @@ inline constexpr int kMaxHeadDim = 128;
 inline constexpr int kMaxGroup = 4;                 // query heads per K/V head (registers hold them all)
 inline constexpr int kMaxGroupTimesHeadDim = 512;   // attention P*V reduction in LDS (4 x 128)
 inline constexpr int kMaxTaskRows = 512;            // rows of one GEMV task kept in LDS
+inline constexpr int kMaxStreamRecords = 1536;      // a worker's instruction stream cached in LDS (longer ones are read from memory)
 // Shared bytes for one attention task's scores of all its query heads, in the package's
 // element type (the planner's chunk capacity, plan_core.py:91-97).  Held as FP32 in LDS.
 inline constexpr int kAttentionSharedBytes = 16384;
 inline constexpr int kRegionFloats = 9216;          // >= max(kThreads * 8, attention scores, P*V reduction)
+inline constexpr uint64_t kBufferRange = 1ull << 31;   // bytes a weight buffer resource addresses
 inline constexpr uint32_t kSpinLimit = 1u << 20;    // polls before a wait is declared stuck
 inline constexpr const char* kAbi = "tileinfer-decoder-v10";
 inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-flash-attention-v1-b512";
@@ -91,13 +95,44 @@ __host__ __device__ inline int hidden_vectors_per_lane(int hidden, int elem)
     return vectors > 64 ? vectors / 64 : 1;
 }
 
+// 16-byte vectors in one K/V row (head_dim elements of `elem` bytes): the lanes that hold it.
+__host__ __device__ inline int head_vectors(int head_dim, int elem) { return head_dim * elem / 16; }
+
+// Compiled worker shapes, (hidden_vectors_per_lane, head_vectors) pairs per storage type:
+// every loop bound and reduction width of a kernel is a compile-time constant, and a kernel
+// carries one attention variant (several in one kernel raise register pressure into spills).
+// bf16: hidden 128..512 (1), 1024 (2), 2048 (4), 4096 (8); head_dim 8..128.
+#define TILES_BF16_SHAPES(X) X(1, 1) X(1, 2) X(1, 4) X(1, 8) X(1, 16) X(2, 8) X(2, 16) X(4, 8) X(4, 16) X(8, 16)
+// fp32: hidden 64..256 (1), 512 (2), 1024 (4), 2048 (8); head_dim 8..128.
+#define TILES_F32_SHAPES(X) X(1, 2) X(1, 4) X(1, 8) X(1, 16) X(1, 32) X(2, 16) X(4, 16) X(4, 32) X(8, 16) X(8, 32)
+
+inline bool worker_compiled(int dtype, int vpl, int lrk)
+{
+#define TILES_MATCH(V, K)                                                                                                \
+    if (vpl == V && lrk == K)                                                                                           \
+        return true;
+    if (dtype == TI_DTYPE_BFLOAT16) {
+        TILES_BF16_SHAPES(TILES_MATCH)
+    } else {
+        TILES_F32_SHAPES(TILES_MATCH)
+    }
+#undef TILES_MATCH
+    return false;
+}
+
+// Launch of the compiled worker for the program's shape (TI_ERR_INVALID_ARGUMENT when none).
+int launch_worker_bf16(hipStream_t stream, const ti_worker_program_view& p, const ti_worker_buffers& b, int position,
+                       ti_token_input token, ti_selection selection);
+int launch_worker_f32(hipStream_t stream, const ti_worker_program_view& p, const ti_worker_buffers& b, int position,
+                      ti_token_input token, ti_selection selection);
+std::vector<const void*> worker_functions_bf16();
+std::vector<const void*> worker_functions_f32();
+
 // Thread-local message of the last failed call (ti_last_error_message).
 const char* last_message();
 void set_last_message(const char* text);
 int fail(int code, const char* text);        // sets the message, returns `code`
 int hip_fail(int hip_error, const char* what);  // "what: <HIP error string>", returns TI_ERR_HIP
-// Every compiled instantiation of the decode worker for one storage type.
-std::vector<const void*> worker_functions(bool bf16);
 
 // Empty when the compiled worker supports the shape; otherwise the reason.
 std::string check_shape(const ti_model_shape& s, int dtype);

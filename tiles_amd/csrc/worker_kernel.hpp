@@ -17,10 +17,13 @@
 //
 // Each operation issues its weight loads (nontemporal, 16 bytes per lane, several passes in
 // flight) before it waits for its inputs, so HBM latency overlaps the wait.  The kernel is
-// instantiated per storage type and per number of 16-byte vectors a lane holds of a hidden
-// row (VPL), so each instantiation carries one GEMV shape and stays small in the instruction
-// cache.  Every bf16 rounding point follows the eager-PyTorch contract of the reference
+// instantiated per storage type, per number of 16-byte vectors a lane holds of a hidden row
+// (VPL) and per number of lanes that hold a K/V row (LRK), so that every loop bound and
+// cross-lane reduction width is a compile-time constant; worker_bf16.hip and worker_f32.hip
+// instantiate the shapes listed in worker_config.hpp.  Every bf16 rounding point follows the eager-PyTorch contract of the reference
 // (docs/architecture.md:284-312; ops.cuh sites cited per function).
+#pragma once
+
 #include <string>
 #include <vector>
 
@@ -32,6 +35,10 @@ namespace tiles {
 namespace {
 
 constexpr int kWaves = kThreads / 64;
+
+// This thread's wave, as a value the compiler knows to be uniform across the wave (a scalar),
+// so that branches on it stay scalar branches.
+__device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6); }
 constexpr int kDownBatch = 8;  // Wdown^T rows a thread keeps in flight in an FFN task
 
 // ---------------------------------------------------------------- launch record
@@ -99,7 +106,9 @@ struct Shared {
     float small[kMaxTaskRows];    // reductions over waves, softmax statistics, residual rows
     float rotated[(kMaxGroup + 1) * kMaxHeadDim];
     float vcur[kMaxHeadDim];
+    float rope_cs[kMaxHeadDim];  // the position's RoPE cos (first half) and sin (second half)
     ti_candidate candidates[kWaves];
+    ti_task_record stream[kMaxStreamRecords];  // this worker's instructions, when they fit
     uint32_t xsave_tag;  // epoch_of(step, layer, kPhaseQKV) of xsave's contents, 0 when empty
     uint32_t rsave_tag;  // epoch_of(step, layer, kPhaseR) of rsave's contents
     int flag;
@@ -130,35 +139,55 @@ __device__ inline bool stuck(uint64_t* exchange, const ExchangeLayout& xl, uint3
 // The first read is optimistic (one coherent round trip when the producers are done).  If any
 // word is still missing, only wave 0 keeps polling, one "witness" word every `stride` words
 // (every producer writes a run of at least `stride` words), with a back-off; the block then
-// re-reads what was missing.  Polling the whole vector from every thread of every worker
-// floods the few memory channels that hold it and slows the producers themselves.
+// re-reads.  Polling the whole vector from every thread of every worker floods the few memory
+// channels that hold it and slows the producers themselves.  Every read issues all its loads
+// before it looks at any of them: a use right after a load waits for it, and a loop of such
+// pairs would pay one round trip per word.
 template <typename Sink>
 __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
                                           const ExchangeLayout& xl, Shared& sh, Sink sink)
 {
     constexpr int kBatch = (kMaxHidden + kThreads - 1) / kThreads;
-    const uint64_t done_word = static_cast<uint64_t>(epoch) << 32;
+    constexpr int kWitnessBatch = 8;
     uint64_t w[kBatch];
-    bool ok = true;
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-        const int index = k * kThreads + static_cast<int>(threadIdx.x);
-        w[k] = index < count ? coherent_load64(src + index) : done_word;
-        ok &= static_cast<uint32_t>(w[k] >> 32) == epoch;
-    }
-    const bool all_present = __syncthreads_and(ok);
+    for (int k = 0; k < kBatch; ++k)
+        w[k] = static_cast<uint64_t>(epoch) << 32;
+    auto read = [&]() {
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int index = k * kThreads + static_cast<int>(threadIdx.x);
+            if (k * kThreads < count)  // block-uniform; lanes past count re-read the last word
+                w[k] = coherent_load64(src + (index < count ? index : count - 1));
+        }
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k)
+            ok &= static_cast<uint32_t>(w[k] >> 32) == epoch;
+        return ok;
+    };
+    const bool all_present = __syncthreads_and(read());
     if (threadIdx.x == 0 && sh.mark_read == 0)
         sh.mark_read = __builtin_amdgcn_s_memrealtime();
     if (!all_present) {
         if (threadIdx.x < 64) {
             const int lane = threadIdx.x;
+            const int witnesses = (count + stride - 1) / stride;
             uint32_t spins = 0;
             while (true) {
                 bool mine = true;
-                for (int j = lane; j * stride < count; j += 64)
-                    mine &= static_cast<uint32_t>(coherent_load64(src + j * stride) >> 32) == epoch;
-                if (lane == 0)
-                    mine &= static_cast<uint32_t>(coherent_load64(src + count - 1) >> 32) == epoch;
+                // Witness j is word j * stride; lanes past the last witness check the last word.
+                for (int j0 = 0; j0 <= witnesses; j0 += 64 * kWitnessBatch) {
+                    uint64_t v[kWitnessBatch];
+#pragma unroll
+                    for (int u = 0; u < kWitnessBatch; ++u) {
+                        const int j = j0 + u * 64 + lane;
+                        v[u] = coherent_load64(src + (j < witnesses ? j * stride : count - 1));
+                    }
+#pragma unroll
+                    for (int u = 0; u < kWitnessBatch; ++u)
+                        mine &= static_cast<uint32_t>(v[u] >> 32) == epoch;
+                }
                 if (__all(mine))
                     break;
                 __builtin_amdgcn_s_sleep(2);
@@ -169,17 +198,11 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
             }
         }
         __syncthreads();
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int index = k * kThreads + static_cast<int>(threadIdx.x);
-            uint32_t spins = 0;
-            while (static_cast<uint32_t>(w[k] >> 32) != epoch && !sh.aborted) {
-                w[k] = coherent_load64(src + index);
-                if (static_cast<uint32_t>(w[k] >> 32) == epoch)
-                    break;
-                __builtin_amdgcn_s_sleep(2);
+        uint32_t spins = 0;
+        while (!__syncthreads_and(read()) && !sh.aborted) {
+            __builtin_amdgcn_s_sleep(2);
+            if (threadIdx.x == 0)
                 stuck(exchange, xl, ++spins, sh);
-            }
         }
     }
 #pragma unroll
@@ -231,8 +254,18 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, in
                               ? static_cast<const void*>(L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) +
                                                                         static_cast<size_t>(token) * d))
                               : L.input;
-        for (int i = threadIdx.x; i < d; i += kThreads)
-            dst[i] = sh.xsave[i] = Num<BF16>::load(row, i);
+        float v[kMaxHidden / kThreads];
+#pragma unroll
+        for (int k = 0; k < kMaxHidden / kThreads; ++k) {  // all loads in flight together
+            const int i = k * kThreads + static_cast<int>(threadIdx.x);
+            v[k] = Num<BF16>::load(row, i < d ? i : 0);
+        }
+#pragma unroll
+        for (int k = 0; k < kMaxHidden / kThreads; ++k) {
+            const int i = k * kThreads + static_cast<int>(threadIdx.x);
+            if (i < d)
+                dst[i] = sh.xsave[i] = v[k];
+        }
     } else {
         poll_words(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
                    L.exchange, L.xl, sh, [&](int i, uint32_t p) { dst[i] = sh.xsave[i] = Num<BF16>::from_payload(p); });
@@ -278,11 +311,13 @@ struct NormScale {
 template <bool BF16>
 __device__ __forceinline__ NormScale load_scale(const void* scale, int d)
 {
+    // Unconditional loads (lanes past d re-read element d - 1, never used): a select on a
+    // loaded value would make the load's wait immediate.
     NormScale s;
 #pragma unroll
     for (int k = 0; k < kMaxHidden / kThreads; ++k) {
         const int i = k * kThreads + static_cast<int>(threadIdx.x);
-        s.v[k] = i < d ? Num<BF16>::load(scale, i) : 0.0f;
+        s.v[k] = Num<BF16>::load(scale, i < d ? i : d - 1);
     }
     return s;
 }
@@ -296,7 +331,7 @@ __device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& s
     for (int i = threadIdx.x; i < d; i += kThreads)
         sum += v[i] * v[i];
     sum = group_sum(sum, 64);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     __syncthreads();
     if (lane == 63)
         sh.small[wave] = sum;
@@ -328,7 +363,7 @@ struct RowGeometry {
         rows_per_wave = 64 / lr;
         pass_rows = kWaves * rows_per_wave;
         const int lane = threadIdx.x & 63;
-        wave = threadIdx.x >> 6;
+        wave = wave_id();
         sub = lane / lr;
         col = lane % lr;
     }
@@ -336,12 +371,13 @@ struct RowGeometry {
 };
 
 // Dot products of rows [r0, r1) of NM matrices of hidden width with the FP32 vector u (LDS).
-// row_ptr(m, row) is the address of a row of matrix m.  D passes of loads are in flight; all
+// row_offset(m, row) is the byte offset from `base` of a row of matrix m (below 2 GiB).  D passes of loads are in flight; all
 // D issue before `prepare`, which runs block-wide, waits for the task's inputs and writes u,
 // so weight latency overlaps the wait.  emit(row, dots) runs in each row group's last lane
 // with one dot per matrix.
-template <bool BF16, int VPL, int NM, typename RowPtr, typename Prepare, typename Emit>
-__device__ __forceinline__ void gemv(RowPtr row_ptr, int r0, int r1, int cols, const float* u, Prepare prepare, Emit emit)
+template <bool BF16, int VPL, int NM, typename RowOffset, typename Prepare, typename Emit>
+__device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int r0, int r1, int cols, const float* u,
+                                    Prepare prepare, Emit emit)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
@@ -349,29 +385,62 @@ __device__ __forceinline__ void gemv(RowPtr row_ptr, int r0, int r1, int cols, c
     constexpr int D = K <= 4 ? 4 : (K <= 8 ? 2 : 1);
     const RowGeometry<BF16> g(cols);
     auto active = [&](int pass) { return g.first_row(r0, pass) < r1; };
+    const __amdgpu_buffer_rsrc_t rsrc = weight_rsrc(base);
     auto issue = [&](int pass, u32x4* w) {
         const int row = g.first_row(r0, pass) + g.sub;
-        const int safe = row < r1 ? row : r0;
+        const bool inside = row < r1;
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-            const char* p = row_ptr(m, safe) + static_cast<size_t>(g.col) * 16;
+            const uint32_t start = row_offset(m, inside ? row : r0) + static_cast<uint32_t>(g.col) * 16;
 #pragma unroll
             for (int k = 0; k < VPL; ++k)
-                w[m * VPL + k] = load_weights(p + static_cast<size_t>(k) * g.lr * 16);
+                w[m * VPL + k] = load_weights(rsrc, inside ? start + static_cast<uint32_t>(k * g.lr * 16) : kBufferOutside);
         }
     };
     u32x4 w[D][K];
+    // Every pass issues (rows past the task read zeros from outside the buffer range): a
+    // conditional issue would leave the compiler unsure how many loads are in flight, and its
+    // waits for earlier loads would become waits for all of them.
 #pragma unroll
     for (int s = 0; s < D; ++s)
-        if (active(s))
-            issue(s, w[s]);
+        issue(s, w[s]);
     prepare();
-    float ur[VPL][PV];
+    // The lane's slice of u in registers: packed bf16 pairs for v_dot2_f32_bf16 (u holds
+    // bf16-rounded values there), FP32 otherwise.
+    constexpr int kSlice = BF16 ? VPL * 4 : VPL * PV;
+    uint32_t ur[kSlice];
 #pragma unroll
-    for (int k = 0; k < VPL; ++k)
+    for (int k = 0; k < VPL; ++k) {
+        const float* src = u + (g.col + k * g.lr) * PV;
+        if constexpr (BF16) {
 #pragma unroll
-        for (int j = 0; j < PV; ++j)
-            ur[k][j] = u[(g.col + k * g.lr) * PV + j];
+            for (int q = 0; q < 4; ++q)
+                ur[k * 4 + q] = pack_bf16(src[2 * q], src[2 * q + 1]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < PV; ++j)
+                ur[k * PV + j] = __float_as_uint(src[j]);
+        }
+    }
+    auto dot = [&](const u32x4* wm) {
+        if constexpr (BF16) {
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent chains
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    a[q] = dot2_bf16(wm[k][q], ur[k * 4 + q], a[q]);
+            return (a[0] + a[1]) + (a[2] + a[3]);
+        } else {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int j = 0; j < PV; ++j)
+                    acc += N::elem(wm[k], j) * __uint_as_float(ur[k * PV + j]);
+            return acc;
+        }
+    };
     for (int base = 0; active(base); base += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
@@ -380,17 +449,9 @@ __device__ __forceinline__ void gemv(RowPtr row_ptr, int r0, int r1, int cols, c
                 break;
             float dots[NM];
 #pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < VPL; ++k)
-#pragma unroll
-                    for (int j = 0; j < PV; ++j)
-                        acc += N::elem(w[s][m * VPL + k], j) * ur[k][j];
-                dots[m] = group_sum(acc, g.lr);
-            }
-            if (active(pass + D))
-                issue(pass + D, w[s]);
+            for (int m = 0; m < NM; ++m)
+                dots[m] = VPL > 1 ? group_sum<64>(dot(&w[s][m * VPL])) : group_sum(dot(&w[s][m * VPL]), g.lr);
+            issue(pass + D, w[s]);
             const int row = g.first_row(r0, pass) + g.sub;
             if (row < r1 && g.col == g.lr - 1)
                 emit(row, dots);
@@ -413,15 +474,12 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     const int position = L.position + step;
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseQKV);
-    const char* wq = L.layer_weight(layer, L.layout.Wq);
-    const char* wk = L.layer_weight(layer, L.layout.Wk);
-    const char* wv = L.layer_weight(layer, L.layout.Wv);
-    const size_t row_bytes = static_cast<size_t>(d) * N::kBytes;
     // Rows may span Wq, Wk and Wv, which are separate regions of the layer's weights.
-    auto row_ptr = [&](int, int row) {
-        return row < d         ? wq + static_cast<size_t>(row) * row_bytes
-               : row < d + kvw ? wk + static_cast<size_t>(row - d) * row_bytes
-                               : wv + static_cast<size_t>(row - d - kvw) * row_bytes;
+    auto row_offset = [&](int, int row) {
+        const uint32_t element = row < d         ? L.layout.Wq + static_cast<uint32_t>(row) * d
+                                 : row < d + kvw ? L.layout.Wk + static_cast<uint32_t>(row - d) * d
+                                                 : L.layout.Wv + static_cast<uint32_t>(row - d - kvw) * d;
+        return element * N::kBytes;
     };
     const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.attn_norm), d);
     auto prepare = [&]() {
@@ -430,7 +488,7 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
         rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
     };
     float* staged_v = sh.small;  // this task's V rows, published after their cache stores
-    gemv<BF16, VPL, 1>(row_ptr, begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
+    gemv<BF16, VPL, 1>(L.layer_weight(layer, 0), row_offset, begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
         const float value = N::round(dots[0]);
         if (row < d + kvw)
             publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
@@ -464,31 +522,25 @@ __device__ inline int active_chunks(int position, const ti_model_shape& s)
     return chunks > 2 ? chunks : 2;
 }
 
-// Rotate one split-half pair; cos/sin and products round before the sum (ops.cuh:125-140).
-template <bool BF16>
-__device__ inline void rope_pair(const float* src, float* dst, int pair, int half, float angle)
-{
-    const float c = Num<BF16>::round(cosf(angle));
-    const float s = Num<BF16>::round(sinf(angle));
-    const float a = src[pair], b = src[pair + half];
-    dst[pair] = Num<BF16>::round(Num<BF16>::round(a * c) - Num<BF16>::round(b * s));
-    dst[pair + half] = Num<BF16>::round(Num<BF16>::round(b * c) + Num<BF16>::round(a * s));
-}
-
 // One K/V head and context chunk of decode attention (ops.cuh:574-673, re-designed):
 // RoPE of the group's query heads and current K; chunk 0 stores rotated K into the cache.
 // One active chunk (a prefix of at most attention_fused_steps): scores, exact softmax,
 // probabilities rounded to the storage type, P*V, published as the group's attention output.
 // Several chunks: each chunk keeps (max, sum of exp, unnormalized P*V) in FP32; the chunk
 // that finishes last (an atomic count per head group) merges all of them and publishes.
-// Cached K/V rows never change during a token, so the first block of them is loaded before
-// the task waits for this token's Q/K/V.
-template <bool BF16>
+// LRK lanes hold one K/V row (16 bytes each, head_dim = LRK * elements per vector).  Cached
+// K/V rows never change during a token, so the first block of them, and the position's RoPE
+// angles, are loaded before the task waits for this token's Q/K/V.
+template <bool BF16, int LRK>
 __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
     constexpr int MG = kMaxGroup;
+    constexpr int dh = LRK * PV;
+    constexpr int kRowsPerWave = 64 / LRK;
+    constexpr int kBlockRows = kWaves * kRowsPerWave;
+    constexpr uint32_t kOutside = 0x80000000u;  // past every layer's K/V bytes: the buffer load returns 0
     const ti_model_shape& s = L.shape;
     const int position = L.position + step;
     const int chunks = active_chunks(position, s);
@@ -497,7 +549,6 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         return;
     const int layer = static_cast<int>(t.layer);
     const int kv_head = static_cast<int>(t.kv_head);
-    const int dh = s.head_dim;
     const int group = s.query_heads / s.kv_heads;
     const int first_head = kv_head * group;
     const int kvw = static_cast<int>(L.kv_width());
@@ -506,30 +557,35 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const int end = static_cast<int>(static_cast<int64_t>(length) * (chunk + 1) / chunks);
     const int span = end - begin;
 
-    const int LRk = dh / PV;  // lanes per K/V row (a power of two <= 16)
-    const int rows_per_wave = 64 / LRk;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane / LRk, col = lane % LRk;
-    const int block_rows = kWaves * rows_per_wave;
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int sub = lane / LRK, col = lane % LRK;
     void* key_cache = L.cache(layer, L.layout.key);
     const void* value_cache = L.cache(layer, L.layout.value);
     const uint32_t layer_kv_bytes = static_cast<uint32_t>(static_cast<size_t>(s.max_context) * kvw * N::kBytes);
     const __amdgpu_buffer_rsrc_t krsrc = make_rsrc(key_cache, layer_kv_bytes);
     const __amdgpu_buffer_rsrc_t vrsrc = make_rsrc(value_cache, layer_kv_bytes);
-    auto row_time = [&](int first, int u) { return first + u * block_rows + wave * rows_per_wave + sub; };
+    auto row_time = [&](int first, int u) { return first + u * kBlockRows + wave * kRowsPerWave + sub; };
+    // Rows past the chunk, and the current position (not cached yet), read as zeros.
     auto load_rows = [&](__amdgpu_buffer_rsrc_t rsrc, int first, u32x4* raw) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int time = row_time(first, u);
             const bool cached = time < end && time < position;
-            const uint32_t offset =
-                static_cast<uint32_t>((static_cast<size_t>(cached ? time : 0) * kvw + kv_head * dh + col * PV) * N::kBytes);
-            raw[u] = cached ? coherent_load128(rsrc, offset) : u32x4{0, 0, 0, 0};
+            const uint32_t offset = static_cast<uint32_t>((static_cast<size_t>(time) * kvw + kv_head * dh + col * PV) * N::kBytes);
+            raw[u] = coherent_load128(rsrc, cached ? offset : kOutside);
         }
     };
     u32x4 kfirst[2], vfirst[2];
     load_rows(krsrc, begin, kfirst);
     load_rows(vrsrc, begin, vfirst);
+
+    // cos/sin of the position's RoPE angles, rounded (ops.cuh:125-140).
+    constexpr int half = dh / 2;
+    for (int pair = threadIdx.x; pair < half; pair += kThreads) {
+        const float angle = static_cast<float>(position) * global(L.rope)[pair];
+        sh.rope_cs[pair] = N::round(cosf(angle));
+        sh.rope_cs[half + pair] = N::round(sinf(angle));
+    }
 
     // This token's Q heads, K and V of the head group: one packed exchange block.
     const int block = (group + 2) * dh;
@@ -538,11 +594,12 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                row_stride(s.hidden_size + 2 * kvw, L.workers), L.epoch_of(step, layer, kPhaseQKV), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { incoming[i] = N::from_payload(p); });
     __syncthreads();
-    const int half = dh / 2;
     for (int index = threadIdx.x; index < (group + 1) * half; index += kThreads) {
         const int head = index / half, pair = index - head * half;
-        const float angle = static_cast<float>(position) * global(L.rope)[pair];
-        rope_pair<BF16>(incoming + head * dh, sh.rotated + head * dh, pair, half, angle);
+        const float c = sh.rope_cs[pair], sn = sh.rope_cs[half + pair];
+        const float a = incoming[head * dh + pair], b = incoming[head * dh + pair + half];
+        sh.rotated[head * dh + pair] = N::round(N::round(a * c) - N::round(b * sn));
+        sh.rotated[head * dh + pair + half] = N::round(N::round(b * c) + N::round(a * sn));
     }
     for (int index = threadIdx.x; index < dh; index += kThreads)
         sh.vcur[index] = incoming[(group + 1) * dh + index];
@@ -562,22 +619,24 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         }
     }
 
-    // Scores of rows [begin, end): LRk lanes hold one 16-byte slice of a K row each.
+    // Scores of rows [begin, end).  Every lane holds its slice of all MG query heads (heads
+    // past the group compute values that are never stored) and of the current K row.
     const float scale = 1.0f / sqrtf(static_cast<float>(dh));
     const float divisor = sqrtf(static_cast<float>(dh));
     float* scores = sh.region;  // [group][span] (the incoming block is consumed)
-    float qreg[MG][PV];
+    constexpr int kWords = BF16 ? 4 : PV;  // registers per 16-byte slice
+    uint32_t qreg[MG][kWords];
+    uint32_t kcur[kWords];
 #pragma unroll
-    for (int g = 0; g < MG; ++g)
+    for (int g = 0; g <= MG; ++g) {
+        const float* src = sh.rotated + (g < MG ? g : group) * dh + col * PV;
+        uint32_t* dst = g < MG ? qreg[g] : kcur;
 #pragma unroll
-        for (int j = 0; j < PV; ++j)
-            qreg[g][j] = g < group ? sh.rotated[g * dh + col * PV + j] : 0.0f;
-    float kcur[PV];
-#pragma unroll
-    for (int j = 0; j < PV; ++j)
-        kcur[j] = sh.rotated[group * dh + col * PV + j];
+        for (int q = 0; q < kWords; ++q)
+            dst[q] = BF16 ? pack_bf16(src[2 * q], src[2 * q + 1]) : __float_as_uint(src[q]);
+    }
     __syncthreads();  // incoming is dead; scores may overwrite the region
-    for (int first = begin; first < end; first += 2 * block_rows) {
+    for (int first = begin; first < end; first += 2 * kBlockRows) {
         u32x4 raw[2];
         if (first == begin) {
             raw[0] = kfirst[0];
@@ -589,14 +648,28 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         for (int u = 0; u < 2; ++u) {
             const int time = row_time(first, u);
             const bool current = time == position;
+            uint32_t kw[kWords];
+#pragma unroll
+            for (int q = 0; q < kWords; ++q)
+                kw[q] = current ? kcur[q] : raw[u][q];
 #pragma unroll
             for (int g = 0; g < MG; ++g) {
                 float dot = 0.0f;
+                if constexpr (BF16) {
+                    float a = 0.0f, b = 0.0f;
 #pragma unroll
-                for (int j = 0; j < PV; ++j)
-                    dot += (current ? kcur[j] : N::elem(raw[u], j)) * qreg[g][j];
-                dot = group_sum(dot, LRk);
-                if (g < group && col == LRk - 1 && time < end) {
+                    for (int q = 0; q < 4; q += 2) {
+                        a = dot2_bf16(kw[q], qreg[g][q], a);
+                        b = dot2_bf16(kw[q + 1], qreg[g][q + 1], b);
+                    }
+                    dot = a + b;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < PV; ++j)
+                        dot += __uint_as_float(kw[j]) * __uint_as_float(qreg[g][j]);
+                }
+                dot = group_sum<LRK>(dot);
+                if (g < group && col == LRK - 1 && time < end) {
                     const float rounded = N::round(dot);
                     scores[g * span + time - begin] = BF16 ? N::round(rounded * scale) : rounded / divisor;
                 }
@@ -616,7 +689,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         float sum = 0.0f;
         for (int i = lane; i < span; i += 64)
             sum += expf(scores[wave * span + i] - m);
-        sum = group_sum(sum, 64);
+        sum = group_sum<64>(sum);
         if (lane == 63) {
             stat_max[wave] = m;
             stat_sum[wave] = sum;
@@ -632,11 +705,15 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     __syncthreads();
 
     // P*V over rows [begin, end): each lane accumulates its slice for every head.
+    float vnow[PV];
+#pragma unroll
+    for (int j = 0; j < PV; ++j)
+        vnow[j] = sh.vcur[col * PV + j];
     float acc[MG * PV];
 #pragma unroll
     for (int n = 0; n < MG * PV; ++n)
         acc[n] = 0.0f;
-    for (int first = begin; first < end; first += 2 * block_rows) {
+    for (int first = begin; first < end; first += 2 * kBlockRows) {
         u32x4 raw[2];
         if (first == begin) {
             raw[0] = vfirst[0];
@@ -647,20 +724,25 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int time = row_time(first, u);
-            if (time >= end)
-                continue;
+            const bool inside = time < end;
             const bool current = time == position;
+            float v[PV];
+#pragma unroll
+            for (int j = 0; j < PV; ++j)
+                v[j] = current ? vnow[j] : N::elem(raw[u], j);
 #pragma unroll
             for (int g = 0; g < MG; ++g) {
-                const float p = g < group ? scores[g * span + time - begin] : 0.0f;
+                // Rows past the chunk, and heads past the group, read in-bounds LDS and weigh 0.
+                const float read = scores[g * span + time - begin];
+                const float p = inside && g < group ? read : 0.0f;
 #pragma unroll
                 for (int j = 0; j < PV; ++j)
-                    acc[g * PV + j] += p * (current ? sh.vcur[col * PV + j] : N::elem(raw[u], j));
+                    acc[g * PV + j] += p * v[j];
             }
         }
     }
     // Reduce over the rows a wave holds (lanes with equal col), then over waves.
-    residue_sum(acc, LRk);
+    residue_sum<LRK>(acc);
     __syncthreads();  // probabilities are dead
     float* reduction = sh.region;  // [wave][group][dh]
     if (sub == 0)
@@ -710,8 +792,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         return;
     // The last chunk of this head group merges every chunk.  Wave g gathers head g's chunk
     // statistics (one load per lane and chunk, all in flight together) into LDS:
-    // M = max_c max_c', S = sum_c sum_c exp(max_c - M), weight_c = exp(max_c - M).
-    float* weight = sh.region;                   // [chunks][group]
+    // M = max_c max_c, S = sum_c sum_c exp(max_c - M), weight_c = exp(max_c - M).
+    float* weight = sh.region;                      // [chunks][group]
     float* chunk_sum = sh.region + chunks * group;  // [chunks][group]
     if (wave < group) {
         float m = -INFINITY;
@@ -729,7 +811,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             weight[c * group + wave] = e;
             total += chunk_sum[c * group + wave] * e;
         }
-        total = group_sum(total, 64);
+        total = group_sum<64>(total);
         if (lane == 63)
             sh.small[2 * kMaxGroup + wave] = total;
     }
@@ -772,8 +854,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseR);
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     float* residual = sh.small;  // rows [begin, end)
-    const char* wo = L.layer_weight(layer, L.layout.Wo);
-    const size_t row_bytes = static_cast<size_t>(d) * N::kBytes;
+    const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
     auto prepare = [&]() {
         for (int i = begin + static_cast<int>(threadIdx.x); i < end; i += kThreads)
             residual[i - begin] = input_element(L, layer, step, token, i, sh);
@@ -785,8 +866,8 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
             for (int i = threadIdx.x; i < d; i += kThreads)
                 N::store(L.scratch, L.layout.attention + i, sh.vec[i]);
     };
-    gemv<BF16, VPL, 1>([&](int, int row) { return wo + static_cast<size_t>(row) * row_bytes; }, begin, end, d, sh.vec,
-                       prepare, [&](int row, const float* dots) {
+    gemv<BF16, VPL, 1>(L.layer_weight(layer, L.layout.Wo), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
+                       begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
                            const float r = N::round(N::round(dots[0]) + residual[row - begin]);
                            N::store(L.scratch, L.layout.r + row, r);
                            publish<BF16>(L.exchange + L.xl.r, row, r, epoch);
@@ -813,21 +894,20 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     const int nvec = d / PV;
     const int groups = kThreads / nvec;  // >= 1 and exact: the loader bounds hidden_size to powers of two
     const int col = threadIdx.x % nvec, grp = threadIdx.x / nvec;
-    const size_t row_bytes = static_cast<size_t>(d) * N::kBytes;
-    const char* wdown = L.layer_weight(layer, L.layout.Wdown) + static_cast<size_t>(col) * 16;
+    const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
+    const __amdgpu_buffer_rsrc_t down_rsrc = weight_rsrc(L.layer_weight(layer, L.layout.Wdown));
     u32x4 dw[kDownBatch];
-    auto issue_down = [&](int first_k) {
+    auto issue_down = [&](int first_k, u32x4* out) {
 #pragma unroll
         for (int k = 0; k < kDownBatch; ++k) {
             const int i = grp + (first_k + k) * groups;
-            dw[k] = i < rows ? load_weights(wdown + static_cast<size_t>(begin + i) * row_bytes) : u32x4{0, 0, 0, 0};
+            const uint32_t offset = static_cast<uint32_t>(begin + i) * row_bytes + static_cast<uint32_t>(col) * 16;
+            out[k] = load_weights(down_rsrc, i < rows ? offset : kBufferOutside);
         }
     };
-    const char* wgate = L.layer_weight(layer, L.layout.Wgate);
-    const char* wup = L.layer_weight(layer, L.layout.Wup);
     const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.ffn_norm), d);
     auto prepare = [&]() {
-        issue_down(0);
+        issue_down(0, dw);
         poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
                    [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
         if (threadIdx.x == 0)
@@ -835,8 +915,11 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
         __syncthreads();
         rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
     };
-    gemv<BF16, VPL, 2>([&](int m, int row) { return (m == 0 ? wgate : wup) + static_cast<size_t>(row) * row_bytes; }, begin,
-                       end, d, sh.vec, prepare, [&](int row, const float* dots) {
+    gemv<BF16, VPL, 2>(L.layer_weight(layer, 0),
+                       [&](int m, int row) {
+                           return ((m == 0 ? L.layout.Wgate : L.layout.Wup) + static_cast<uint32_t>(row) * d) * N::kBytes;
+                       },
+                       begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
                            gate[row - begin] = N::round(dots[0]);
                            up[row - begin] = N::round(dots[1]);
                        });
@@ -853,10 +936,12 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
 #pragma unroll
     for (int j = 0; j < PV; ++j)
         acc[j] = 0.0f;
+    // Double-buffered: the next batch of rows is in flight while this one is consumed (rows
+    // past the chunk read zeros from outside the buffer range).
     const int per_thread = (rows + groups - 1) / groups;
     for (int first_k = 0; first_k < per_thread; first_k += kDownBatch) {
-        if (first_k > 0)
-            issue_down(first_k);
+        u32x4 next[kDownBatch];
+        issue_down(first_k + kDownBatch, next);
 #pragma unroll
         for (int k = 0; k < kDownBatch; ++k) {
             const int i = grp + (first_k + k) * groups;
@@ -865,6 +950,9 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
             for (int j = 0; j < PV; ++j)
                 acc[j] += N::elem(dw[k], j) * p;
         }
+#pragma unroll
+        for (int k = 0; k < kDownBatch; ++k)
+            dw[k] = next[k];
     }
     __syncthreads();  // product is dead
     float* reduction = sh.region;  // [groups][d]
@@ -908,20 +996,30 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
         const bool row_ok = first + slot < rows;
         float total = 0.0f;
         for (int c0 = 0; c0 < s.ffn_chunks; c0 += kPerLane * tpr) {
+            // Every load issues before any result is used; slots past the row's chunks
+            // re-read a real word and are replaced by +0.0 afterwards.
             uint64_t w[kPerLane];
-            bool ok = true;
+            auto read = [&]() {
 #pragma unroll
-            for (int k = 0; k < kPerLane; ++k) {
-                const int c = c0 + lane + k * tpr;
-                w[k] = row_ok && c < s.ffn_chunks ? coherent_load64(base + static_cast<size_t>(c) * d + row) : present;
-                ok &= static_cast<uint32_t>(w[k] >> 32) == in_epoch;
-            }
-            if (!ok) {
+                for (int k = 0; k < kPerLane; ++k) {
+                    const int c = c0 + lane + k * tpr;
+                    const bool real = row_ok && c < s.ffn_chunks;
+                    w[k] = coherent_load64(base + static_cast<size_t>(real ? c : 0) * d + (row_ok ? row : begin));
+                }
+                bool ok = true;
 #pragma unroll
-                for (int k = 0; k < kPerLane; ++k)
-                    if (static_cast<uint32_t>(w[k] >> 32) != in_epoch)
-                        w[k] = present | poll_one(base + static_cast<size_t>(c0 + lane + k * tpr) * d + row, in_epoch,
-                                                  L.exchange, L.xl, sh);
+                for (int k = 0; k < kPerLane; ++k) {
+                    const int c = c0 + lane + k * tpr;
+                    if (!(row_ok && c < s.ffn_chunks))
+                        w[k] = present;
+                    ok &= static_cast<uint32_t>(w[k] >> 32) == in_epoch;
+                }
+                return ok;
+            };
+            uint32_t spins = 0;
+            for (bool ok = read(); !ok && !sh.aborted; ok = read()) {
+                __builtin_amdgcn_s_sleep(2);
+                stuck(L.exchange, L.xl, ++spins, sh);
             }
 #pragma unroll
             for (int k = 0; k < kPerLane; ++k)
@@ -980,12 +1078,12 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
 {
     const int d = L.shape.hidden_size;
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     ti_candidate best{-INFINITY, 0x7fffffff};
-    const char* head = L.stack_weight(L.stack.lm_head_offset);
-    const size_t row_bytes = static_cast<size_t>(d) * Num<BF16>::kBytes;
+    const uint32_t row_bytes = static_cast<uint32_t>(d) * Num<BF16>::kBytes;
     const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
-    gemv<BF16, VPL, 1>([&](int, int row) { return head + static_cast<size_t>(row) * row_bytes; }, begin, end, d, sh.vec,
+    gemv<BF16, VPL, 1>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
+                       begin, end, d, sh.vec,
                        [&]() { final_normalized(L, step, scale, sh); },
                        [&](int row, const float* dots) {
                            const float logit = Num<BF16>::round(dots[0]);
@@ -1014,34 +1112,43 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
 }
 
 // Greedy selection over every logits task's candidate (ops.cuh:895-911).  Step 0 of a launch
-// reads the candidates a previous launch left (complete at the kernel boundary).
+// reads the candidates a previous launch left (complete at the kernel boundary).  Every thread
+// reads its slots at once; a late slot is waited for alone.
 template <bool BF16>
 __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, Shared& sh)
 {
     const int slots = L.selection_slots;
-    if (threadIdx.x < 64) {
-        ti_candidate best{-INFINITY, 0x7fffffff};
-        const uint32_t epoch = step > 0 ? L.epoch_of(step - 1, L.stack.layers, kPhaseCandidate) : 0u;
-        for (int slot = threadIdx.x; slot < slots; slot += 64) {
-            const uint64_t* words = L.exchange + L.xl.candidates + 2 * static_cast<size_t>(slot);
-            uint64_t a = coherent_load64(words), b = coherent_load64(words + 1);
-            if (step > 0) {
-                uint32_t spins = 0;
-                while ((static_cast<uint32_t>(a >> 32) != epoch || static_cast<uint32_t>(b >> 32) != epoch) && !sh.aborted) {
-                    __builtin_amdgcn_s_sleep(2);
-                    a = coherent_load64(words);
-                    b = coherent_load64(words + 1);
-                    stuck(L.exchange, L.xl, ++spins, sh);
-                }
+    const uint32_t epoch = step > 0 ? L.epoch_of(step - 1, L.stack.layers, kPhaseCandidate) : 0u;
+    ti_candidate best{-INFINITY, 0x7fffffff};
+    for (int base = 0; base < slots; base += kThreads) {
+        const int slot = base + static_cast<int>(threadIdx.x);
+        const bool real = slot < slots;
+        const uint64_t* words = L.exchange + L.xl.candidates + 2 * static_cast<size_t>(real ? slot : 0);
+        uint64_t a = coherent_load64(words), b = coherent_load64(words + 1);
+        if (real && step > 0) {
+            uint32_t spins = 0;
+            while ((static_cast<uint32_t>(a >> 32) != epoch || static_cast<uint32_t>(b >> 32) != epoch) && !sh.aborted) {
+                __builtin_amdgcn_s_sleep(2);
+                a = coherent_load64(words);
+                b = coherent_load64(words + 1);
+                stuck(L.exchange, L.xl, ++spins, sh);
             }
+        }
+        if (real)
             keep_better(best, {__uint_as_float(static_cast<uint32_t>(a)), static_cast<ti_token_id>(static_cast<uint32_t>(b))});
-        }
-        for (int offset = 32; offset > 0; offset >>= 1) {
-            ti_candidate other{__shfl_xor(best.value, offset), __shfl_xor(best.id, offset)};
-            keep_better(best, other);
-        }
-        if (threadIdx.x == 0)
-            sh.token = best.id;
+    }
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        ti_candidate other{__shfl_xor(best.value, offset), __shfl_xor(best.id, offset)};
+        keep_better(best, other);
+    }
+    if ((threadIdx.x & 63) == 0)
+        sh.candidates[wave_id()] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        ti_candidate result = sh.candidates[0];
+        for (int w = 1; w < kWaves; ++w)
+            keep_better(result, sh.candidates[w]);
+        sh.token = result.id;
     }
     __syncthreads();
     return sh.token;
@@ -1063,7 +1170,7 @@ __device__ void record_choice(const Launch<BF16>& L, int step, ti_token_id token
     }
 }
 
-template <bool BF16, int VPL>
+template <bool BF16, int VPL, int LRK>
 __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launch)
 {
     __shared__ Shared sh;
@@ -1083,6 +1190,13 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
     if (generating && (global(L.selection.status)[TI_STATUS_EOS] != 0 || global(L.selection.status)[TI_STATUS_ERROR] != 0))
         return;
     const ti_worker_task_range stream = load_record(L.streams + blockIdx.x);
+    // The worker's instruction records move to LDS once: read from memory as each task
+    // starts, every record would cost a dependent memory round trip between two tasks.
+    const bool cached = stream.count <= static_cast<uint32_t>(kMaxStreamRecords);
+    if (cached)
+        for (uint32_t i = threadIdx.x; i < stream.count; i += kThreads)
+            sh.stream[i] = load_record(L.instructions + stream.begin + i);
+    __syncthreads();
     for (int step = 0; step < L.steps; ++step) {
         ti_token_id token = L.token_id;
         if (generating) {
@@ -1095,7 +1209,7 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
         if (L.stack.full_stack && (token < 0 || token >= L.stack.vocab_size))
             return;
         for (uint32_t index = stream.begin; index < stream.begin + stream.count; ++index) {
-            const ti_task_record task = load_record(L.instructions + index);
+            const ti_task_record task = cached ? sh.stream[index - stream.begin] : load_record(L.instructions + index);
             if (task.opcode == TI_OP_BARRIER)
                 continue;  // waves synchronize through the exchange words
             // Optional timeline: 100 MHz device clock (s_memrealtime) at the start of every
@@ -1108,7 +1222,7 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
             }
             switch (task.opcode) {
             case TI_OP_QKV: op_qkv<BF16, VPL>(L, task, step, token, sh); break;
-            case TI_OP_ATTENTION_SCORES: op_attention<BF16>(L, task, step, sh); break;
+            case TI_OP_ATTENTION_SCORES: op_attention<BF16, LRK>(L, task, step, sh); break;
             case TI_OP_OUTPUT_PROJECTION: op_output_projection<BF16, VPL>(L, task, step, token, sh); break;
             case TI_OP_FFN: op_ffn<BF16, VPL>(L, task, step, sh); break;
             case TI_OP_FFN_REDUCE: op_ffn_reduce<BF16>(L, task, step, sh); break;
@@ -1142,7 +1256,7 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
 
 // ---------------------------------------------------------------- host side of the launch
 
-template <bool BF16, int VPL>
+template <bool BF16, int VPL, int LRK>
 int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_worker_buffers& b, int position,
                  ti_token_input token, ti_selection selection)
 {
@@ -1176,51 +1290,11 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     L.selection_slots = p.selection_slots;
     L.workers = p.workers;
     void* args[] = {&L};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decoder_worker<BF16, VPL>),
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decoder_worker<BF16, VPL, LRK>),
                                                     dim3(p.workers), dim3(kThreads), args, 0, stream);
     if (e != hipSuccess)
         return hip_fail(e, "cooperative worker launch");
     return TI_OK;
 }
-
-// check_shape admits hidden sizes whose rows give 1, 2, 4 or 8 vectors per lane.
-template <bool BF16>
-int launch_vpl(hipStream_t s, const ti_worker_program_view& p, const ti_worker_buffers& b, int position,
-               ti_token_input token, ti_selection selection)
-{
-    switch (hidden_vectors_per_lane(p.shape.hidden_size, Num<BF16>::kBytes)) {
-    case 1: return launch_typed<BF16, 1>(s, p, b, position, token, selection);
-    case 2: return launch_typed<BF16, 2>(s, p, b, position, token, selection);
-    case 4: return launch_typed<BF16, 4>(s, p, b, position, token, selection);
-    case 8: return launch_typed<BF16, 8>(s, p, b, position, token, selection);
-    default: return fail(TI_ERR_INVALID_ARGUMENT, "hidden size unsupported by the compiled worker's 16-byte row lanes");
-    }
-}
 } // namespace
-
-std::vector<const void*> worker_functions(bool bf16)
-{
-    if (bf16)
-        return {reinterpret_cast<const void*>(&decoder_worker<true, 1>), reinterpret_cast<const void*>(&decoder_worker<true, 2>),
-                reinterpret_cast<const void*>(&decoder_worker<true, 4>), reinterpret_cast<const void*>(&decoder_worker<true, 8>)};
-    return {reinterpret_cast<const void*>(&decoder_worker<false, 1>), reinterpret_cast<const void*>(&decoder_worker<false, 2>),
-            reinterpret_cast<const void*>(&decoder_worker<false, 4>), reinterpret_cast<const void*>(&decoder_worker<false, 8>)};
-}
-
 } // namespace tiles
-
-extern "C" int ti_enqueue_worker(void* stream, const ti_worker_program_view* program, const ti_worker_buffers* buffers,
-                                 int32_t position, ti_token_input token, ti_selection selection)
-{
-    using namespace tiles;
-    if (!program || !buffers)
-        return fail(TI_ERR_INVALID_ARGUMENT, "null program or buffers");
-    if (token.steps < 1 || token.steps > TI_MAX_LAUNCH_STEPS)
-        return fail(TI_ERR_INVALID_ARGUMENT, "invalid worker launch step count");
-    const std::string problem = check_launch_shape(*program, *buffers, position, token.steps);
-    if (!problem.empty())
-        return fail(TI_ERR_INVALID_ARGUMENT, problem.c_str());
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    return program->weight_dtype == TI_DTYPE_BFLOAT16 ? launch_vpl<true>(s, *program, *buffers, position, token, selection)
-                                                      : launch_vpl<false>(s, *program, *buffers, position, token, selection);
-}
