@@ -1,10 +1,10 @@
 """Benchmark: bf16 batch-1 greedy decode of a random-init Llama-3.2-1B on one MI355X.
 
-Prints ONE JSON line (the driver's contract).  The workload named by BASELINE.json's metric:
+Prints ONE JSON line.  The workload of the headline metric (ms/token of batch-1 bf16 decode):
 
-* ctx 1 (config 3, the headline ``value``): 1-token prompt, 256 new tokens, 64 per launch;
-* ctx 4096 (config 4): 4096 seeded uniform prompt tokens prefilled, then 64 new tokens in one
-  launch (reported under ``ctx4096``).
+* ctx 1 (the headline ``value``): 1-token prompt, 256 new tokens, 64 per launch;
+* ctx 4096: 4096 seeded uniform prompt tokens prefilled, then 64 new tokens in one launch
+  (reported under ``ctx4096``).
 
 A "step" is one token of decode (one pass of the hot path); ``ms_per_step`` = ``value``
 = ms/token of the generate launches, timed with HIP events on the context stream (prefill,
@@ -28,9 +28,12 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-WEIGHT_BYTES = 2_471_628_800          # bf16 weights streamed per token
+WEIGHT_BYTES = 2_471_628_800          # bf16 weights streamed per token: 1,235,814,400 parameters x 2 bytes
 KV_BYTES_PER_POSITION = 32_768        # 16 layers x (K + V) x 8 heads x 64 x 2 bytes
 PEAK_HBM_GBPS = 8000.0                # MI355X published HBM3E bandwidth
+# HBM bytes a ctx-1 generate token moves, measured with rocprofv3 FETCH_SIZE and WRITE_SIZE
+# (calibrated against a known-size read and fill), profiles/decoder_worker_llama1b_bf16_ctx1_hbm_counters.md.
+MEASURED_TRAFFIC_BYTES_PER_TOKEN = 2_691_095_082
 
 
 def log(*args) -> None:
@@ -77,6 +80,9 @@ def main() -> int:
     parser.add_argument("--no-ctx4096", action="store_true")
     parser.add_argument("--cpu-tokens", type=int, default=24)
     parser.add_argument("--chunk-steps", type=int, default=128)
+    parser.add_argument("--write-package", type=Path, default=None,
+                        help="only write the benchmark's package to this directory and its ctx-1 prompt to "
+                             "DIR.ctx1.json (for `tiles_amd/tile_runtime bench` under a profiler), then exit")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the decode worker is single-GPU); --gpus {args.gpus} is not supported",
@@ -89,6 +95,11 @@ def main() -> int:
     from tiles_amd.tileplan import probe
 
     target = probe.probe_library()
+    if args.write_package is not None:
+        S.llama_package(args.write_package, 4096 + 64, "bfloat16", seed=0, chunk_steps=args.chunk_steps, target=target)
+        Path(f"{args.write_package}.ctx1.json").write_text(json.dumps({"tokens": [S.BOS]}) + "\n")
+        log(f"wrote {args.write_package} and {args.write_package}.ctx1.json")
+        return 0
     stream_gbps = R.measure_stream_read(2 << 30, 3)
     log(f"measured stream read {stream_gbps:.1f} GB/s")
     work = S.scratch_dir()
@@ -162,7 +173,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (random-init N(0,0.02) weights, norm weights 1.0, seed 0)",
         "config": {"workload": "Llama-3.2-1B bf16 batch-1 greedy decode, ctx 1: 1-token prompt, 256 new tokens, "
-                               "64 per persistent launch (BASELINE config 3); ctx 4096 under ctx4096 (config 4)",
+                               "64 per persistent launch; ctx 4096 (4096-token prompt, 64 new tokens) under ctx4096",
                    "global_batch": 1, "seq_len": len(prompt) + new_tokens, "parallelism": "none",
                    "attention_chunk_steps": args.chunk_steps, "workers": target["launch"]["worker_count"]},
         "tokens_per_second": 1e3 / ms_per_token,
@@ -170,7 +181,8 @@ def main() -> int:
         "floor_ms_per_token": floor_ms,
         "fraction_of_floor": floor_ms / ms_per_token,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBPS, "traffic": None,
+                     "frac": achieved / PEAK_HBM_GBPS,
+                     "traffic": MEASURED_TRAFFIC_BYTES_PER_TOKEN * min(new_tokens, 64),
                      "kernel": "decoder_worker", "launches": launches * steps,
                      "bytes_per_launch": total_bytes / launches, "avg_launch_us": mean_us / launches},
         "ctx4096": ctx4096,

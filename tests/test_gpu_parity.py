@@ -8,8 +8,9 @@ kernel_regression.py:111-297, decoder_regression.py:41-220):
 * a small stack with a long context and 16-step attention chunks: the split-context merge
   path (several chunks per head) vs the oracle, fp32 within 1e-4 relative.
 * random-init Llama-3.2-1B: fp32 per-step logits within 1e-4 relative (the north-star fp32
-  bar); bf16 within the measured noise floor of two valid eager orderings,
-  greedy tokens equal wherever the oracle's top-2 gap exceeds that floor.
+  bar); bf16 within the measured noise floor of two valid eager orderings of the same bf16
+  computation (0.078 absolute at most on these logits), greedy tokens equal wherever the
+  oracle's top-2 gap exceeds that floor.
 * generation semantics: multi-launch, EOS, capacity, vocabulary and non-finite-logit errors.
 """
 

@@ -72,7 +72,7 @@ std::vector<ti_token_id> read_prompt(const std::string& path)
     return out;
 }
 
-enum class Mode { help, target, inspect, check, generate, bench };
+enum class Mode { help, target, inspect, check, generate, bench, stream };
 
 struct Command {
     Mode mode = Mode::help;
@@ -92,6 +92,14 @@ Command parse(int argc, char** argv)
         return c;
     if (argc == 2 && mode == "--describe-target-json") {
         c.mode = Mode::target;
+        return c;
+    }
+    if ((argc == 3 || argc == 4) && mode == "--measure-stream-read") {
+        c.mode = Mode::stream;
+        c.count = parse_int(argv[2]);  // MiB read per dispatch
+        c.rounds = argc == 4 ? parse_int(argv[3]) : 3;
+        if (c.count <= 0 || c.rounds <= 0)
+            throw std::runtime_error("invalid stream measurement arguments");
         return c;
     }
     if (argc == 3 && mode == "--inspect-plan") {
@@ -328,13 +336,25 @@ int main(int argc, char** argv)
                          "tile_runtime bench PACKAGE INPUTS.json --new-tokens N --warmup W --rounds R\n"
                          "tile_runtime check PACKAGE INPUTS.json [--trace-blocks]\n"
                          "tile_runtime --describe-target-json\n"
-                         "tile_runtime --inspect-plan PACKAGE\n";
+                         "tile_runtime --inspect-plan PACKAGE\n"
+                         "tile_runtime --measure-stream-read MIB [REPEATS]\n";
             return 0;
         }
         ti_target target{};
         ok(ti_describe_target(&target));
         if (c.mode == Mode::target) {
-            std::cout << tiles::target_json(target).dump(2) << '\n';
+            std::cout << tiles::target_json(target).dump(2) << std::endl;
+            return 0;
+        }
+        if (c.mode == Mode::stream) {
+            // Streaming-read roofline probe: one fill of the buffer, then nontemporal read
+            // dispatches of exactly MIB MiB each (also a known-size reference for counters).
+            double gbps = 0.0;
+            ok(ti_measure_stream_read(static_cast<size_t>(c.count) << 20, c.rounds, &gbps));
+            Json out = Json::object();
+            out.set("bytes_per_dispatch", Json::integer(static_cast<int64_t>(c.count) << 20));
+            out.set("best_GBps", Json::real(gbps));
+            std::cout << out.dump() << std::endl;
             return 0;
         }
         ti_plan* handle = nullptr;
@@ -351,7 +371,7 @@ int main(int argc, char** argv)
         }
         for (const auto& [k, v] : tiles::precision_json(plan).fields())
             result.set(k, v);
-        std::cout << result.dump() << '\n';
+        std::cout << result.dump() << std::endl;
         return 0;
     } catch (const std::exception& e) {
         std::cerr << "tile_runtime: " << e.what() << '\n';
