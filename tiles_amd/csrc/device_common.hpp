@@ -129,6 +129,12 @@ __device__ inline u32x4 load_weights(__amdgpu_buffer_rsrc_t rsrc, uint32_t offse
     return __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 2 /* nt */);
 }
 
+// Keeps memory operations issued before it from being moved after it (and the reverse) by
+// the compiler; emits no instruction.  Loads issued before a task waits for its inputs would
+// otherwise be sunk next to their first use, after the wait, and their latency would no
+// longer overlap it.
+__device__ inline void issue_fence() { asm volatile("" ::: "memory"); }
+
 // Waits until every earlier memory operation of the wave completed (s_waitcnt vmcnt(0)).
 __device__ inline void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
 

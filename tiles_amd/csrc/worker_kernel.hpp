@@ -100,6 +100,10 @@ struct Launch {
 
 struct Shared {
     float vec[kMaxHidden];        // a task's input vector, FP32 values of the storage type
+    // The same vector as bf16 bits (bf16 storage): the GEMV reads each lane's slice as one
+    // 16-byte vector at consecutive addresses.  Reading it from `vec` (32 bytes per lane, lanes
+    // 32 bytes apart) put 16 lanes on each LDS bank.
+    uint16_t vbits[kMaxHidden];
     float region[kRegionFloats];  // scores/probabilities, reductions, FFN gate/up/product
     float xsave[kMaxHidden];      // the layer input this worker last read, before the norm
     float rsave[kMaxHidden];      // the attention block output this worker last read
@@ -323,7 +327,8 @@ __device__ __forceinline__ NormScale load_scale(const void* scale, int d)
 }
 
 // In place: v[i] = round(round(v[i] * inv_rms) * scale[i]) for bf16, v[i] * inv_rms * scale[i]
-// for fp32 (decoder_reference.py:183-187, decoder_stack.py:126-132).  The statistic is FP32.
+// for fp32 (decoder_reference.py:183-187, decoder_stack.py:126-132), with the bf16 bits in
+// sh.vbits (v is sh.vec).  The statistic is FP32.
 template <bool BF16>
 __device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& scale, float eps, Shared& sh)
 {
@@ -343,8 +348,11 @@ __device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& s
 #pragma unroll
     for (int k = 0; k < kMaxHidden / kThreads; ++k) {
         const int i = k * kThreads + static_cast<int>(threadIdx.x);
-        if (i < d)
+        if (i < d) {
             v[i] = Num<BF16>::round(Num<BF16>::round(v[i] * inv) * scale.v[k]);
+            if constexpr (BF16)
+                sh.vbits[i] = static_cast<uint16_t>(float_to_bf16_bits(v[i]));
+        }
     }
     __syncthreads();
 }
@@ -370,13 +378,14 @@ struct RowGeometry {
     __device__ int first_row(int r0, int pass) const { return r0 + pass * pass_rows + wave * rows_per_wave; }
 };
 
-// Dot products of rows [r0, r1) of NM matrices of hidden width with the FP32 vector u (LDS).
+// Dot products of rows [r0, r1) of NM matrices of hidden width with the vector u in LDS
+// (sh.vbits for bf16 storage, sh.vec for fp32: see gemv_input).
 // row_offset(m, row) is the byte offset from `base` of a row of matrix m (below 2 GiB).  D passes of loads are in flight; all
 // D issue before `prepare`, which runs block-wide, waits for the task's inputs and writes u,
 // so weight latency overlaps the wait.  emit(row, dots) runs in each row group's last lane
 // with one dot per matrix.
 template <bool BF16, int VPL, int NM, typename RowOffset, typename Prepare, typename Emit>
-__device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int r0, int r1, int cols, const float* u,
+__device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int r0, int r1, int cols, const void* u,
                                     Prepare prepare, Emit emit)
 {
     using N = Num<BF16>;
@@ -404,23 +413,17 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
 #pragma unroll
     for (int s = 0; s < D; ++s)
         issue(s, w[s]);
+    issue_fence();
     prepare();
-    // The lane's slice of u in registers: packed bf16 pairs for v_dot2_f32_bf16 (u holds
-    // bf16-rounded values there), FP32 otherwise.
-    constexpr int kSlice = BF16 ? VPL * 4 : VPL * PV;
-    uint32_t ur[kSlice];
+    // The lane's slice of u in registers, one 16-byte LDS vector per k: packed bf16 pairs
+    // for v_dot2_f32_bf16, or four FP32 values.
+    uint32_t ur[VPL * 4];
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
-        const float* src = u + (g.col + k * g.lr) * PV;
-        if constexpr (BF16) {
+        const u32x4 v = static_cast<const u32x4*>(u)[g.col + k * g.lr];
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                ur[k * 4 + q] = pack_bf16(src[2 * q], src[2 * q + 1]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < PV; ++j)
-                ur[k * PV + j] = __float_as_uint(src[j]);
-        }
+        for (int q = 0; q < 4; ++q)
+            ur[k * 4 + q] = v[q];
     }
     auto dot = [&](const u32x4* wm) {
         if constexpr (BF16) {
@@ -437,7 +440,7 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
             for (int k = 0; k < VPL; ++k)
 #pragma unroll
                 for (int j = 0; j < PV; ++j)
-                    acc += N::elem(wm[k], j) * __uint_as_float(ur[k * PV + j]);
+                    acc += N::elem(wm[k], j) * __uint_as_float(ur[k * 4 + j]);
             return acc;
         }
     };
@@ -460,6 +463,12 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
 }
 
 // ---------------------------------------------------------------- operations
+
+template <bool BF16>
+__device__ inline const void* gemv_input(const Shared& sh)
+{
+    return BF16 ? static_cast<const void*>(sh.vbits) : static_cast<const void*>(sh.vec);
+}
 
 // [Q; K; V] rows of the normalized layer input (ops.cuh:266-289): Q and K round to the storage
 // type and are published unrotated; V rows also go to the cache row of the current position,
@@ -488,7 +497,8 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
         rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
     };
     float* staged_v = sh.small;  // this task's V rows, published after their cache stores
-    gemv<BF16, VPL, 1>(L.layer_weight(layer, 0), row_offset, begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
+    gemv<BF16, VPL, 1>(L.layer_weight(layer, 0), row_offset, begin, end, d, gemv_input<BF16>(sh), prepare,
+                       [&](int row, const float* dots) {
         const float value = N::round(dots[0]);
         if (row < d + kvw)
             publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
@@ -578,6 +588,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     u32x4 kfirst[2], vfirst[2];
     load_rows(krsrc, begin, kfirst);
     load_rows(vrsrc, begin, vfirst);
+    issue_fence();
 
     // cos/sin of the position's RoPE angles, rounded (ops.cuh:125-140).
     constexpr int half = dh / 2;
@@ -860,14 +871,17 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
             residual[i - begin] = input_element(L, layer, step, token, i, sh);
         poll_words(L.exchange + L.xl.attn, d, (L.shape.query_heads / L.shape.kv_heads) * L.shape.head_dim,
                    L.epoch_of(step, layer, kPhaseAttn), L.exchange, L.xl, sh,
-                   [&](int i, uint32_t p) { sh.vec[i] = N::from_payload(p); });
+                   [&](int i, uint32_t p) {
+                       sh.vec[i] = N::from_payload(p);
+                       sh.vbits[i] = static_cast<uint16_t>(p);
+                   });
         __syncthreads();
         if (begin == 0)
             for (int i = threadIdx.x; i < d; i += kThreads)
                 N::store(L.scratch, L.layout.attention + i, sh.vec[i]);
     };
     gemv<BF16, VPL, 1>(L.layer_weight(layer, L.layout.Wo), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
-                       begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
+                       begin, end, d, gemv_input<BF16>(sh), prepare, [&](int row, const float* dots) {
                            const float r = N::round(N::round(dots[0]) + residual[row - begin]);
                            N::store(L.scratch, L.layout.r + row, r);
                            publish<BF16>(L.exchange + L.xl.r, row, r, epoch);
@@ -908,6 +922,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.ffn_norm), d);
     auto prepare = [&]() {
         issue_down(0, dw);
+        issue_fence();
         poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
                    [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
         if (threadIdx.x == 0)
@@ -919,7 +934,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
                        [&](int m, int row) {
                            return ((m == 0 ? L.layout.Wgate : L.layout.Wup) + static_cast<uint32_t>(row) * d) * N::kBytes;
                        },
-                       begin, end, d, sh.vec, prepare, [&](int row, const float* dots) {
+                       begin, end, d, gemv_input<BF16>(sh), prepare, [&](int row, const float* dots) {
                            gate[row - begin] = N::round(dots[0]);
                            up[row - begin] = N::round(dots[1]);
                        });
@@ -1083,7 +1098,7 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     const uint32_t row_bytes = static_cast<uint32_t>(d) * Num<BF16>::kBytes;
     const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
     gemv<BF16, VPL, 1>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
-                       begin, end, d, sh.vec,
+                       begin, end, d, gemv_input<BF16>(sh),
                        [&]() { final_normalized(L, step, scale, sh); },
                        [&](int row, const float* dots) {
                            const float logit = Num<BF16>::round(dots[0]);
