@@ -104,7 +104,7 @@ struct Shared {
     // 16-byte vector at consecutive addresses.  Reading it from `vec` (32 bytes per lane, lanes
     // 32 bytes apart) put 16 lanes on each LDS bank.
     uint16_t vbits[kMaxHidden];
-    float region[kRegionFloats];  // scores/probabilities, reductions, FFN gate/up/product
+    alignas(16) float region[kRegionFloats];  // scores/probabilities, reductions, FFN gate/up/product
     float xsave[kMaxHidden];      // the layer input this worker last read, before the norm
     float rsave[kMaxHidden];      // the attention block output this worker last read
     float small[kMaxTaskRows];    // reductions over waves, softmax statistics, residual rows
@@ -970,10 +970,15 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
             dw[k] = next[k];
     }
     __syncthreads();  // product is dead
-    float* reduction = sh.region;  // [groups][d]
+    // Sum over the row groups through LDS ([group][d]: a lane writes its PV outputs as 16-byte
+    // vectors), then publish with consecutive threads on consecutive words, so that the
+    // device-coherent stores coalesce.
+    float* reduction = sh.region;
 #pragma unroll
-    for (int j = 0; j < PV; ++j)
-        reduction[grp * d + col * PV + j] = acc[j];
+    for (int h = 0; h < PV / 4; ++h)
+        reinterpret_cast<u32x4*>(reduction + grp * d + col * PV)[h] =
+            u32x4{__float_as_uint(acc[4 * h]), __float_as_uint(acc[4 * h + 1]), __float_as_uint(acc[4 * h + 2]),
+                  __float_as_uint(acc[4 * h + 3])};
     __syncthreads();
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseFfn);
     uint64_t* partials = L.exchange + L.xl.ffn + static_cast<size_t>(t.chunk) * d;
