@@ -39,7 +39,6 @@ constexpr int kWaves = kThreads / 64;
 // This thread's wave, as a value the compiler knows to be uniform across the wave (a scalar),
 // so that branches on it stay scalar branches.
 __device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6); }
-constexpr int kDownBatch = 8;  // Wdown^T rows a thread keeps in flight in an FFN task
 
 // ---------------------------------------------------------------- launch record
 
@@ -233,6 +232,44 @@ __device__ inline uint32_t poll_one(const uint64_t* src, uint32_t epoch, uint64_
     return static_cast<uint32_t>(w);
 }
 
+// Wave 0 waits until each witness word witness(j), j < n, carries `epoch` (8 loads in flight per
+// lane, a back-off between rounds); the block then meets at a barrier.  Used after an optimistic
+// read came up short: one wave polling one word per producer instead of every thread polling
+// every word keeps the waiting workers from flooding the memory system that the others are
+// still streaming weights through.  Block-wide: every thread must call it.
+template <typename Witness>
+__device__ __forceinline__ void wait_witnesses(int n, Witness witness, uint32_t epoch, uint64_t* exchange,
+                                              const ExchangeLayout& xl, Shared& sh)
+{
+    constexpr int kBatch = 8;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        uint32_t spins = 0;
+        while (true) {
+            bool mine = true;
+            for (int j0 = 0; j0 < n; j0 += 64 * kBatch) {
+                uint64_t v[kBatch];
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    const int j = j0 + u * 64 + lane;
+                    v[u] = coherent_load64(witness(j < n ? j : n - 1));
+                }
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u)
+                    mine &= static_cast<uint32_t>(v[u] >> 32) == epoch;
+            }
+            if (__all(mine))
+                break;
+            __builtin_amdgcn_s_sleep(2);
+            if (lane == 0)
+                stuck(exchange, xl, ++spins, sh);
+            if (__any(sh.aborted))
+                break;
+        }
+    }
+    __syncthreads();
+}
+
 template <bool BF16>
 __device__ inline void publish(uint64_t* dst, int index, float rounded, uint32_t epoch)
 {
@@ -332,10 +369,15 @@ __device__ __forceinline__ NormScale load_scale(const void* scale, int d)
 template <bool BF16>
 __device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& scale, float eps, Shared& sh)
 {
+    float x[kMaxHidden / kThreads];  // all reads first (v holds kMaxHidden floats)
+#pragma unroll
+    for (int k = 0; k < kMaxHidden / kThreads; ++k)
+        x[k] = v[k * kThreads + threadIdx.x];
     float sum = 0.0f;
-    for (int i = threadIdx.x; i < d; i += kThreads)
-        sum += v[i] * v[i];
-    sum = group_sum(sum, 64);
+#pragma unroll
+    for (int k = 0; k < kMaxHidden / kThreads; ++k)
+        sum += k * kThreads + static_cast<int>(threadIdx.x) < d ? x[k] * x[k] : 0.0f;
+    sum = group_sum<64>(sum);
     const int lane = threadIdx.x & 63, wave = wave_id();
     __syncthreads();
     if (lane == 63)
@@ -384,32 +426,33 @@ struct RowGeometry {
 // D issue before `prepare`, which runs block-wide, waits for the task's inputs and writes u,
 // so weight latency overlaps the wait.  emit(row, dots) runs in each row group's last lane
 // with one dot per matrix.
-template <bool BF16, int VPL, int NM, typename RowOffset, typename Prepare, typename Emit>
+template <bool BF16, int VPL, int NM, int DEPTH = 0, typename RowOffset, typename Prepare, typename Emit>
 __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int r0, int r1, int cols, const void* u,
                                     Prepare prepare, Emit emit)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
     constexpr int K = VPL * NM;
-    constexpr int D = K <= 4 ? 4 : (K <= 8 ? 2 : 1);
+    constexpr int D = DEPTH > 0 ? DEPTH : (K <= 4 ? 4 : (K <= 8 ? 2 : 1));
     const RowGeometry<BF16> g(cols);
     auto active = [&](int pass) { return g.first_row(r0, pass) < r1; };
-    const __amdgpu_buffer_rsrc_t rsrc = weight_rsrc(base);
     auto issue = [&](int pass, u32x4* w) {
         const int row = g.first_row(r0, pass) + g.sub;
         const bool inside = row < r1;
+        const char* at = static_cast<const char*>(base) + (inside ? g.col * 16 : 0);
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-            const uint32_t start = row_offset(m, inside ? row : r0) + static_cast<uint32_t>(g.col) * 16;
+            const char* p = at + row_offset(m, inside ? row : r0);
 #pragma unroll
             for (int k = 0; k < VPL; ++k)
-                w[m * VPL + k] = load_weights(rsrc, inside ? start + static_cast<uint32_t>(k * g.lr * 16) : kBufferOutside);
+                w[m * VPL + k] = load_weights(p + (inside ? k * g.lr * 16 : 0));
         }
     };
     u32x4 w[D][K];
-    // Every pass issues (rows past the task read zeros from outside the buffer range): a
-    // conditional issue would leave the compiler unsure how many loads are in flight, and its
-    // waits for earlier loads would become waits for all of them.
+    // Every pass issues; lanes past the task all read the first 16 bytes of the task's first
+    // row (one cached request per instruction).  A conditional issue would leave the compiler
+    // unsure how many loads are in flight, and its waits for earlier loads would become waits
+    // for all of them.
 #pragma unroll
     for (int s = 0; s < D; ++s)
         issue(s, w[s]);
@@ -890,109 +933,158 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
 
 // One FFN product chunk (ops.cuh:739-813): z = RMSNorm(r); p = round(round(silu(round(gate)))
 // * round(up)) for rows [begin, end); then the chunk's FP32 down partial over every output,
-// published for the reduce wave.  Wdown is stored transposed, [intermediate, hidden]: a thread
-// owns one 16-byte column slice and a residue class of the chunk's rows, and issues the loads
-// of its first kDownBatch rows before the task waits for r.
+// published for the reduce wave.  Wdown is stored transposed, [intermediate, hidden].
+//
+// Rows stream whole: a lane group takes row i's gate and up slices and the same slice of
+// Wdown^T row i in one pass, so p_i multiplies the down row as soon as the group has it, and
+// every pass loads the same amount (3 x VPL 16-byte vectors per lane).  A lane owns the output
+// columns that match its input slice; waves then sum their partials through LDS.  D passes are
+// in flight, all issued before the task waits for r.
 template <bool BF16, int VPL>
 __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
+    constexpr int NV = 3 * VPL;                      // vectors per lane and row: gate, up, down
+    constexpr int D = VPL >= 8 ? 1 : (VPL >= 4 ? 2 : 4);
+    constexpr int kOut = VPL * PV;                   // outputs a lane owns
     const int d = L.shape.hidden_size;
     const int layer = static_cast<int>(t.layer);
-    const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
-    const int rows = end - begin;
-    float* product = sh.region;        // [rows]
-    float* gate = sh.region + rows;    // [rows]
-    float* up = sh.region + 2 * rows;  // [rows]
-    const int nvec = d / PV;
-    const int groups = kThreads / nvec;  // >= 1 and exact: the loader bounds hidden_size to powers of two
-    const int col = threadIdx.x % nvec, grp = threadIdx.x / nvec;
+    const int r0 = static_cast<int>(t.begin), r1 = static_cast<int>(t.end);
+    const RowGeometry<BF16> g(d);
     const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
-    const __amdgpu_buffer_rsrc_t down_rsrc = weight_rsrc(L.layer_weight(layer, L.layout.Wdown));
-    u32x4 dw[kDownBatch];
-    auto issue_down = [&](int first_k, u32x4* out) {
-#pragma unroll
-        for (int k = 0; k < kDownBatch; ++k) {
-            const int i = grp + (first_k + k) * groups;
-            const uint32_t offset = static_cast<uint32_t>(begin + i) * row_bytes + static_cast<uint32_t>(col) * 16;
-            out[k] = load_weights(down_rsrc, i < rows ? offset : kBufferOutside);
-        }
-    };
+    const char* gate = L.layer_weight(layer, L.layout.Wgate) + g.col * 16;
+    const char* up = L.layer_weight(layer, L.layout.Wup) + g.col * 16;
+    const char* down = L.layer_weight(layer, L.layout.Wdown) + g.col * 16;
     const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.ffn_norm), d);
-    auto prepare = [&]() {
-        issue_down(0, dw);
-        issue_fence();
-        poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
-                   [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
-        if (threadIdx.x == 0)
-            sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
-        __syncthreads();
-        rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
-    };
-    gemv<BF16, VPL, 2>(L.layer_weight(layer, 0),
-                       [&](int m, int row) {
-                           return ((m == 0 ? L.layout.Wgate : L.layout.Wup) + static_cast<uint32_t>(row) * d) * N::kBytes;
-                       },
-                       begin, end, d, gemv_input<BF16>(sh), prepare, [&](int row, const float* dots) {
-                           gate[row - begin] = N::round(dots[0]);
-                           up[row - begin] = N::round(dots[1]);
-                       });
-    __syncthreads();
-    for (int i = threadIdx.x; i < rows; i += kThreads) {
-        const float g = gate[i];
-        const float silu = N::round(g / (1.0f + expf(-g)));
-        const float p = N::round(silu * up[i]);
-        product[i] = p;
-        N::store(L.scratch, L.layout.product + begin + i, p);
-    }
-    __syncthreads();
-    float acc[PV];
+    auto row_of = [&](int pass) { return g.first_row(r0, pass) + g.sub; };
+    // Lanes past the chunk all read the first 16 bytes of its first row (one cached request
+    // per instruction); their product is zero.
+    auto issue = [&](int pass, u32x4* w) {
+        const int row = row_of(pass);
+        const bool inside = row < r1;
+        const size_t at = static_cast<size_t>(inside ? row : r0) * row_bytes - (inside ? 0 : g.col * 16);
 #pragma unroll
-    for (int j = 0; j < PV; ++j)
-        acc[j] = 0.0f;
-    // Double-buffered: the next batch of rows is in flight while this one is consumed (rows
-    // past the chunk read zeros from outside the buffer range).
-    const int per_thread = (rows + groups - 1) / groups;
-    for (int first_k = 0; first_k < per_thread; first_k += kDownBatch) {
-        u32x4 next[kDownBatch];
-        issue_down(first_k + kDownBatch, next);
-#pragma unroll
-        for (int k = 0; k < kDownBatch; ++k) {
-            const int i = grp + (first_k + k) * groups;
-            const float p = i < rows ? product[i] : 0.0f;
-#pragma unroll
-            for (int j = 0; j < PV; ++j)
-                acc[j] += N::elem(dw[k], j) * p;
+        for (int k = 0; k < VPL; ++k) {
+            const size_t o = at + (inside ? static_cast<size_t>(k) * g.lr * 16 : 0);
+            w[k] = load_weights(gate + o);
+            w[VPL + k] = load_weights(up + o);
+            w[2 * VPL + k] = load_weights(down + o);
         }
+    };
+    u32x4 w[D][NV];
 #pragma unroll
-        for (int k = 0; k < kDownBatch; ++k)
-            dw[k] = next[k];
-    }
-    __syncthreads();  // product is dead
-    // Sum over the row groups through LDS ([group][d]: a lane writes its PV outputs as 16-byte
-    // vectors), then publish with consecutive threads on consecutive words, so that the
-    // device-coherent stores coalesce.
-    float* reduction = sh.region;
-#pragma unroll
-    for (int h = 0; h < PV / 4; ++h)
-        reinterpret_cast<u32x4*>(reduction + grp * d + col * PV)[h] =
-            u32x4{__float_as_uint(acc[4 * h]), __float_as_uint(acc[4 * h + 1]), __float_as_uint(acc[4 * h + 2]),
-                  __float_as_uint(acc[4 * h + 3])};
+    for (int s = 0; s < D; ++s)
+        issue(s, w[s]);
+    issue_fence();
+
+    poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
+               [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
+    if (threadIdx.x == 0)
+        sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
     __syncthreads();
+    rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
+    uint32_t ur[VPL * 4];
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const u32x4 v = static_cast<const u32x4*>(gemv_input<BF16>(sh))[g.col + k * g.lr];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            ur[k * 4 + q] = v[q];
+    }
+    auto dot = [&](const u32x4* wm) {
+        if constexpr (BF16) {
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    a[q] = dot2_bf16(wm[k][q], ur[k * 4 + q], a[q]);
+            return (a[0] + a[1]) + (a[2] + a[3]);
+        } else {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int j = 0; j < PV; ++j)
+                    acc += N::elem(wm[k], j) * __uint_as_float(ur[k * 4 + j]);
+            return acc;
+        }
+    };
+    float acc[kOut];
+#pragma unroll
+    for (int n = 0; n < kOut; ++n)
+        acc[n] = 0.0f;
+    const int lane = threadIdx.x & 63;
+    for (int base = 0; g.first_row(r0, base) < r1; base += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int pass = base + s;
+            if (g.first_row(r0, pass) >= r1)
+                break;
+            float gate = VPL > 1 ? group_sum<64>(dot(&w[s][0])) : group_sum(dot(&w[s][0]), g.lr);
+            float up = VPL > 1 ? group_sum<64>(dot(&w[s][VPL])) : group_sum(dot(&w[s][VPL]), g.lr);
+            // The group's sums sit in its last lane (in every lane when the group has <= 16).
+            if (g.lr == 64) {
+                gate = lane_value(gate, 63);
+                up = lane_value(up, 63);
+            } else if (g.lr == 32) {
+                gate = __shfl(gate, (lane & 32) | 31);
+                up = __shfl(up, (lane & 32) | 31);
+            }
+            const int row = row_of(pass);
+            const float gr = N::round(gate);
+            const float silu = N::round(gr / (1.0f + expf(-gr)));
+            const float p = row < r1 ? N::round(silu * N::round(up)) : 0.0f;
+            if (row < r1 && g.col == g.lr - 1)
+                N::store(L.scratch, L.layout.product + row, p);
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int j = 0; j < PV; ++j)
+                    acc[k * PV + j] += N::elem(w[s][2 * VPL + k], j) * p;
+            issue(pass + D, w[s]);
+        }
+    }
+    // Lanes of one wave that hold the same columns (several rows per pass) add up first.
+    if (g.lr < 64)
+        residue_sum(acc, g.lr);
+    // Then the waves, KS slices of VPL at a time through LDS ([slice][wave][lr * PV] floats,
+    // as many slices as fit the work region), each round published with consecutive threads on
+    // consecutive words.
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseFfn);
     uint64_t* partials = L.exchange + L.xl.ffn + static_cast<size_t>(t.chunk) * d;
-    for (int i = threadIdx.x; i < d; i += kThreads) {
-        float total = 0.0f;
-        for (int g = 0; g < groups; ++g)
-            total += reduction[g * d + i];
-        coherent_store64(partials + i, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(total));
+    float* reduction = sh.region;
+    const int slice = g.lr * PV;
+    constexpr int KS = VPL >= 2 ? 2 : 1;
+    static_assert(kWaves * 64 * PV * KS <= kRegionFloats, "FFN reduction rounds exceed the work region");
+#pragma unroll
+    for (int k0 = 0; k0 < VPL; k0 += KS) {
+        __syncthreads();
+        if (g.sub == 0)
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+                for (int h = 0; h < PV / 4; ++h) {
+                    const int k = k0 + kk;
+                    reinterpret_cast<u32x4*>(reduction + (kk * kWaves + g.wave) * slice + g.col * PV)[h] =
+                        u32x4{__float_as_uint(acc[k * PV + 4 * h]), __float_as_uint(acc[k * PV + 4 * h + 1]),
+                              __float_as_uint(acc[k * PV + 4 * h + 2]), __float_as_uint(acc[k * PV + 4 * h + 3])};
+                }
+        __syncthreads();
+        for (int o = threadIdx.x; o < KS * slice; o += kThreads) {
+            const int kk = o / slice, c = o - kk * slice;
+            float total = 0.0f;
+            for (int wv = 0; wv < kWaves; ++wv)
+                total += reduction[(kk * kWaves + wv) * slice + c];
+            coherent_store64(partials + k0 * slice + o, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(total));
+        }
     }
 }
 
 // y rows: the chunks' FP32 down partials summed, rounded before the residual (ops.cuh:820-838).
 // TPR lanes (a power of two <= 64) sum one row; each lane issues up to kPerLane chunk reads
-// at once and only falls back to waiting when some chunk has not arrived.
+// at once and re-reads them until all have arrived.
 template <bool BF16>
 __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
@@ -1036,6 +1128,8 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
                 }
                 return ok;
             };
+            // Missing chunks are re-read by their own lanes: waiting on witnesses first would add
+            // two round trips to the layer's critical path.
             uint32_t spins = 0;
             for (bool ok = read(); !ok && !sh.aborted; ok = read()) {
                 __builtin_amdgcn_s_sleep(2);
@@ -1133,25 +1227,33 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
 
 // Greedy selection over every logits task's candidate (ops.cuh:895-911).  Step 0 of a launch
 // reads the candidates a previous launch left (complete at the kernel boundary).  Every thread
-// reads its slots at once; a late slot is waited for alone.
+// reads its slots at once; if some are late, wave 0 waits on their ID words.
 template <bool BF16>
 __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, Shared& sh)
 {
     const int slots = L.selection_slots;
     const uint32_t epoch = step > 0 ? L.epoch_of(step - 1, L.stack.layers, kPhaseCandidate) : 0u;
     ti_candidate best{-INFINITY, 0x7fffffff};
-    for (int base = 0; base < slots; base += kThreads) {
+    const uint64_t* candidates = L.exchange + L.xl.candidates;
+    for (int base = 0; base < slots; base += kThreads) {  // block-uniform
         const int slot = base + static_cast<int>(threadIdx.x);
         const bool real = slot < slots;
-        const uint64_t* words = L.exchange + L.xl.candidates + 2 * static_cast<size_t>(real ? slot : 0);
-        uint64_t a = coherent_load64(words), b = coherent_load64(words + 1);
-        if (real && step > 0) {
+        const uint64_t* words = candidates + 2 * static_cast<size_t>(real ? slot : 0);
+        uint64_t a, b;
+        auto read = [&]() {
+            a = coherent_load64(words);
+            b = coherent_load64(words + 1);
+            return step == 0 || (static_cast<uint32_t>(a >> 32) == epoch && static_cast<uint32_t>(b >> 32) == epoch);
+        };
+        if (!__syncthreads_and(read())) {
+            const int n = slots - base < kThreads ? slots - base : kThreads;
+            wait_witnesses(n, [&](int j) { return candidates + 2 * static_cast<size_t>(base + j) + 1; }, epoch, L.exchange,
+                           L.xl, sh);
             uint32_t spins = 0;
-            while ((static_cast<uint32_t>(a >> 32) != epoch || static_cast<uint32_t>(b >> 32) != epoch) && !sh.aborted) {
+            while (!__syncthreads_and(read()) && !sh.aborted) {
                 __builtin_amdgcn_s_sleep(2);
-                a = coherent_load64(words);
-                b = coherent_load64(words + 1);
-                stuck(L.exchange, L.xl, ++spins, sh);
+                if (threadIdx.x == 0)
+                    stuck(L.exchange, L.xl, ++spins, sh);
             }
         }
         if (real)
