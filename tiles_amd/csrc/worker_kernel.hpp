@@ -214,6 +214,10 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
         if (index < count)
             sink(index, static_cast<uint32_t>(w[k]));
     }
+    // This worker's earlier stores (K/V cache rows written after their exchange words) complete
+    // before anything it publishes from here on, which is what every later reader of those rows
+    // follows.  The loads above already returned, so this waits only for stores.
+    wait_stores();
     if (threadIdx.x == 0)
         sh.mark_ready = __builtin_amdgcn_s_memrealtime();
 }
@@ -513,9 +517,10 @@ __device__ inline const void* gemv_input(const Shared& sh)
     return BF16 ? static_cast<const void*>(sh.vbits) : static_cast<const void*>(sh.vec);
 }
 
-// [Q; K; V] rows of the normalized layer input (ops.cuh:266-289): Q and K round to the storage
-// type and are published unrotated; V rows also go to the cache row of the current position,
-// and their words are published once those stores completed.
+// [Q; K; V] rows of the normalized layer input (ops.cuh:266-289), rounded to the storage type
+// and published unrotated.  V rows also go to the cache row of the current position; this
+// token's attention takes V from the exchange words, and the worker's next input poll waits for
+// the cache stores before it publishes anything else, so later tokens find the row complete.
 template <bool BF16, int VPL>
 __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_record& t, int step, ti_token_id token, Shared& sh)
 {
@@ -539,13 +544,12 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
         __syncthreads();
         rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
     };
-    float* staged_v = sh.small;  // this task's V rows, published after their cache stores
-    gemv<BF16, VPL, 1>(L.layer_weight(layer, 0), row_offset, begin, end, d, gemv_input<BF16>(sh), prepare,
+    float* staged_v = sh.small;  // this task's V rows, for the cache stores after the GEMV
+    gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, 0), row_offset, begin, end, d, gemv_input<BF16>(sh), prepare,
                        [&](int row, const float* dots) {
         const float value = N::round(dots[0]);
-        if (row < d + kvw)
-            publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
-        else
+        publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
+        if (row >= d + kvw)
             staged_v[row - begin] = value;
     });
     const int first_v = begin > d + kvw ? begin : d + kvw;
@@ -561,9 +565,6 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
         else
             coherent_storef(static_cast<float*>(cache) + index, staged_v[row - begin]);
     }
-    wait_stores();
-    for (int row = first_v + static_cast<int>(threadIdx.x); row < end; row += kThreads)
-        publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), staged_v[row - begin], epoch);
 }
 
 __device__ inline int active_chunks(int position, const ti_model_shape& s)
@@ -923,7 +924,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
             for (int i = threadIdx.x; i < d; i += kThreads)
                 N::store(L.scratch, L.layout.attention + i, sh.vec[i]);
     };
-    gemv<BF16, VPL, 1>(L.layer_weight(layer, L.layout.Wo), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
+    gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, L.layout.Wo), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
                        begin, end, d, gemv_input<BF16>(sh), prepare, [&](int row, const float* dots) {
                            const float r = N::round(N::round(dots[0]) + residual[row - begin]);
                            N::store(L.scratch, L.layout.r + row, r);
@@ -1196,7 +1197,7 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     ti_candidate best{-INFINITY, 0x7fffffff};
     const uint32_t row_bytes = static_cast<uint32_t>(d) * Num<BF16>::kBytes;
     const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
-    gemv<BF16, VPL, 1>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
+    gemv<BF16, VPL, 1, 4>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
                        begin, end, d, gemv_input<BF16>(sh),
                        [&]() { final_normalized(L, step, scale, sh); },
                        [&](int row, const float* dots) {
@@ -1320,6 +1321,8 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
             sh.stream[i] = load_record(L.instructions + stream.begin + i);
     __syncthreads();
     for (int step = 0; step < L.steps; ++step) {
+        // The previous step's K/V cache stores complete before this step publishes anything.
+        wait_stores();
         ti_token_id token = L.token_id;
         if (generating) {
             token = greedy(L, step, sh);
