@@ -440,23 +440,26 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
     constexpr int D = DEPTH > 0 ? DEPTH : (K <= 4 ? 4 : (K <= 8 ? 2 : 1));
     const RowGeometry<BF16> g(cols);
     auto active = [&](int pass) { return g.first_row(r0, pass) < r1; };
+    // Lanes past the task read the task's first row from its start, 16 bytes apart per k: one
+    // cached request per instruction.  Their addresses differ per k on purpose: equal ones let
+    // the compiler load once for those lanes and copy, behind a wait for that load.
     auto issue = [&](int pass, u32x4* w) {
         const int row = g.first_row(r0, pass) + g.sub;
         const bool inside = row < r1;
-        const char* at = static_cast<const char*>(base) + (inside ? g.col * 16 : 0);
+        const uint32_t col = inside ? static_cast<uint32_t>(g.col) * 16u : 0u;
+        const uint32_t stride = inside ? static_cast<uint32_t>(g.lr) * 16u : 16u;
+        const char* at = static_cast<const char*>(base) + col;
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
             const char* p = at + row_offset(m, inside ? row : r0);
 #pragma unroll
             for (int k = 0; k < VPL; ++k)
-                w[m * VPL + k] = load_weights(p + (inside ? k * g.lr * 16 : 0));
+                w[m * VPL + k] = load_weights(p + k * stride);
         }
     };
     u32x4 w[D][K];
-    // Every pass issues; lanes past the task all read the first 16 bytes of the task's first
-    // row (one cached request per instruction).  A conditional issue would leave the compiler
-    // unsure how many loads are in flight, and its waits for earlier loads would become waits
-    // for all of them.
+    // Every pass issues.  A conditional issue would leave the compiler unsure how many loads are
+    // in flight, and its waits for earlier loads would become waits for all of them.
 #pragma unroll
     for (int s = 0; s < D; ++s)
         issue(s, w[s]);
@@ -531,12 +534,15 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     const int position = L.position + step;
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseQKV);
-    // Rows may span Wq, Wk and Wv, which are separate regions of the layer's weights.
-    auto row_offset = [&](int, int row) {
-        const uint32_t element = row < d         ? L.layout.Wq + static_cast<uint32_t>(row) * d
-                                 : row < d + kvw ? L.layout.Wk + static_cast<uint32_t>(row - d) * d
-                                                 : L.layout.Wv + static_cast<uint32_t>(row - d - kvw) * d;
-        return element * N::kBytes;
+    // Rows may span Wq, Wk and Wv, which are separate regions of the layer's weights.  The
+    // region is a select of values read once (a select of the fields themselves became branches
+    // around their loads).
+    const uint32_t wq = L.layout.Wq, wk = L.layout.Wk, wv = L.layout.Wv;
+    auto row_offset = [=](int, int row) {
+        const bool q = row < d, k = row < d + kvw;
+        const uint32_t region = q ? wq : (k ? wk : wv);
+        const uint32_t first = q ? 0u : static_cast<uint32_t>(k ? d : d + kvw);
+        return (region + (static_cast<uint32_t>(row) - first) * static_cast<uint32_t>(d)) * N::kBytes;
     };
     const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.attn_norm), d);
     auto prepare = [&]() {
