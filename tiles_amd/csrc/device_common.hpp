@@ -113,6 +113,16 @@ __device__ inline float dot2_bf16(uint32_t a, uint32_t b, float c)
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
+// D = A B + C on 16x16 FP32 tiles with K = 32 bf16 (v_mfma_f32_16x16x32_bf16): lane l holds
+// row l % 16 of A and column l % 16 of B, elements 8 (l / 16) .. 8 (l / 16) + 7 of each as four
+// packed pairs, and rows 4 (l / 16) .. 4 (l / 16) + 3 of column l % 16 of C and D.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ inline f32x4 mfma_16x16x32_bf16(const u32x4& a, const u32x4& b, const f32x4& c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
 // Weights stream once per token: nontemporal 16-byte global loads (global_load_dwordx4 ... nt).
 // Measured on the FFN's access pattern, these stream at about 7.0 TB/s and buffer-resource loads
 // at 5.2-6.0 TB/s, so a lane with no row to load re-reads a row of its task (a cache hit) rather

@@ -97,12 +97,22 @@ struct Launch {
     }
 };
 
+// bf16 elements of the attention's V^T block: head_dim rows of (block positions + 8), with 128
+// positions per block up to 64 dims and 64 beyond.
+constexpr int kVtElements = kMaxHeadDim * (64 + 8);
+static_assert(64 * (128 + 8) <= kVtElements, "V^T block of a 64-dim head");
+
 struct Shared {
-    float vec[kMaxHidden];        // a task's input vector, FP32 values of the storage type
-    // The same vector as bf16 bits (bf16 storage): the GEMV reads each lane's slice as one
-    // 16-byte vector at consecutive addresses.  Reading it from `vec` (32 bytes per lane, lanes
-    // 32 bytes apart) put 16 lanes on each LDS bank.
-    uint16_t vbits[kMaxHidden];
+    union {
+        struct {
+            float vec[kMaxHidden];  // a task's input vector, FP32 values of the storage type
+            // The same vector as bf16 bits (bf16 storage): the GEMV reads each lane's slice as
+            // one 16-byte vector at consecutive addresses.  Reading it from `vec` (32 bytes per
+            // lane, lanes 32 bytes apart) put 16 lanes on each LDS bank.
+            uint16_t vbits[kMaxHidden];
+        };
+        alignas(16) uint16_t vt[kVtElements];  // attention: V^T of a block of positions (no input vector)
+    };
     alignas(16) float region[kRegionFloats];  // scores/probabilities, reductions, FFN gate/up/product
     float xsave[kMaxHidden];      // the layer input this worker last read, before the norm
     float rsave[kMaxHidden];      // the attention block output this worker last read
@@ -588,9 +598,17 @@ __device__ inline int active_chunks(int position, const ti_model_shape& s)
 // probabilities rounded to the storage type, P*V, published as the group's attention output.
 // Several chunks: each chunk keeps (max, sum of exp, unnormalized P*V) in FP32; the chunk
 // that finishes last (an atomic count per head group) merges all of them and publishes.
-// LRK lanes hold one K/V row (16 bytes each, head_dim = LRK * elements per vector).  Cached
-// K/V rows never change during a token, so the first block of them, and the position's RoPE
-// angles, are loaded before the task waits for this token's Q/K/V.
+//
+// bf16 heads of 32, 64 or 128 dims compute Q K^T and P V on the matrix cores
+// (v_mfma_f32_16x16x32_bf16): a wave takes 16 positions at a time, lane l holding position
+// l % 16 and dims 8 (l / 16) .. + 7 of every 32 (one 16-byte load per 32 dims), against the
+// group's query heads padded to 16 rows.  V is transposed through LDS a block of positions at
+// a time, so P V runs the positions as the reduced dimension; waves split the head's dims 16
+// at a time.  Unnormalized FP32 probabilities of split chunks enter as the exact sum of three
+// bf16 parts.  Other shapes use the vector path: LRK lanes hold one K/V row (16 bytes each),
+// rows spread over lanes and waves, partial P V sums reduced across them.
+// Cached K/V rows never change during a token, so the first rows of the chunk, and the
+// position's RoPE angles, are loaded before the task waits for this token's Q/K/V.
 template <bool BF16, int LRK>
 __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
@@ -598,6 +616,13 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     constexpr int PV = N::kPerVec;
     constexpr int MG = kMaxGroup;
     constexpr int dh = LRK * PV;
+    constexpr bool kMfma = BF16 && dh % 32 == 0;
+    constexpr int KS = dh / 32;                      // 32-dim slices of a head (matrix path)
+    constexpr int kTile = 16;                        // positions per matrix tile
+    constexpr int PB = dh > 64 ? 64 : 128;           // positions per V^T block in LDS
+    constexpr int kVtStride = PB + 8;                // bf16 elements per V^T row
+    static_assert(!kMfma || dh * kVtStride <= kVtElements, "V^T block exceeds its LDS area");
+    static_assert(!kMfma || dh / 16 <= kWaves, "a wave per 16 output dims");
     constexpr int kRowsPerWave = 64 / LRK;
     constexpr int kBlockRows = kWaves * kRowsPerWave;
     constexpr uint32_t kOutside = 0x80000000u;  // past every layer's K/V bytes: the buffer load returns 0
@@ -618,26 +643,45 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const int span = end - begin;
 
     const int lane = threadIdx.x & 63, wave = wave_id();
-    const int sub = lane / LRK, col = lane % LRK;
+    const int sub = lane / LRK, col = lane % LRK;    // vector path: row and 16-byte slice
+    const int tr = lane % kTile, tk = lane / kTile;  // matrix path: tile row and 8-element slice
     void* key_cache = L.cache(layer, L.layout.key);
     const void* value_cache = L.cache(layer, L.layout.value);
     const uint32_t layer_kv_bytes = static_cast<uint32_t>(static_cast<size_t>(s.max_context) * kvw * N::kBytes);
     const __amdgpu_buffer_rsrc_t krsrc = make_rsrc(key_cache, layer_kv_bytes);
     const __amdgpu_buffer_rsrc_t vrsrc = make_rsrc(value_cache, layer_kv_bytes);
+    // Rows past the chunk, and the current position (not cached yet), read as zeros.  Their
+    // offsets differ per load: equal ones let the compiler merge the loads behind a wait.
     auto row_time = [&](int first, int u) { return first + u * kBlockRows + wave * kRowsPerWave + sub; };
-    // Rows past the chunk, and the current position (not cached yet), read as zeros.
     auto load_rows = [&](__amdgpu_buffer_rsrc_t rsrc, int first, u32x4* raw) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int time = row_time(first, u);
             const bool cached = time < end && time < position;
             const uint32_t offset = static_cast<uint32_t>((static_cast<size_t>(time) * kvw + kv_head * dh + col * PV) * N::kBytes);
-            raw[u] = coherent_load128(rsrc, cached ? offset : kOutside);
+            raw[u] = coherent_load128(rsrc, cached ? offset : kOutside + 16u * u);
         }
     };
-    u32x4 kfirst[2], vfirst[2];
-    load_rows(krsrc, begin, kfirst);
-    load_rows(vrsrc, begin, vfirst);
+    // Matrix path: tile `tile` of the chunk, lane l at position begin + 16 tile + l % 16.
+    auto load_tile = [&](__amdgpu_buffer_rsrc_t rsrc, int tile, u32x4* raw) {
+        const int time = begin + tile * kTile + tr;
+        const bool cached = time < end && time < position;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const uint32_t offset =
+                static_cast<uint32_t>((static_cast<size_t>(time) * kvw + kv_head * dh + 32 * k + 8 * tk) * N::kBytes);
+            raw[k] = coherent_load128(rsrc, cached ? offset : kOutside + 16u * k);
+        }
+    };
+    constexpr int kFirst = kMfma ? KS : 2;
+    u32x4 kfirst[kFirst], vfirst[kFirst];
+    if constexpr (kMfma) {
+        load_tile(krsrc, wave, kfirst);
+        load_tile(vrsrc, wave, vfirst);
+    } else {
+        load_rows(krsrc, begin, kfirst);
+        load_rows(vrsrc, begin, vfirst);
+    }
     issue_fence();
 
     // cos/sin of the position's RoPE angles, rounded (ops.cuh:125-140).
@@ -664,7 +708,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     }
     for (int index = threadIdx.x; index < dh; index += kThreads)
         sh.vcur[index] = incoming[(group + 1) * dh + index];
-    __syncthreads();
+    __syncthreads();  // incoming is dead: the scores may overwrite the region
     if (chunk == 0) {
         for (int index = threadIdx.x; index < (group + 1) * dh; index += kThreads) {
             const float value = sh.rotated[index];
@@ -680,147 +724,266 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         }
     }
 
-    // Scores of rows [begin, end).  Every lane holds its slice of all MG query heads (heads
-    // past the group compute values that are never stored) and of the current K row.
     const float scale = 1.0f / sqrtf(static_cast<float>(dh));
     const float divisor = sqrtf(static_cast<float>(dh));
-    float* scores = sh.region;  // [group][span] (the incoming block is consumed)
-    constexpr int kWords = BF16 ? 4 : PV;  // registers per 16-byte slice
-    uint32_t qreg[MG][kWords];
-    uint32_t kcur[kWords];
+    float* scores = sh.region;  // [group][span]
+    auto score_of = [&](float dot) {
+        const float rounded = N::round(dot);
+        return BF16 ? N::round(rounded * scale) : rounded / divisor;
+    };
+    // Matrix path: eight bf16 values of `src` as four packed pairs.
+    auto pack8 = [](const float* src) {
+        u32x4 v;
 #pragma unroll
-    for (int g = 0; g <= MG; ++g) {
-        const float* src = sh.rotated + (g < MG ? g : group) * dh + col * PV;
-        uint32_t* dst = g < MG ? qreg[g] : kcur;
+        for (int q = 0; q < 4; ++q)
+            v[q] = pack_bf16(src[2 * q], src[2 * q + 1]);
+        return v;
+    };
+    // Matrix path: V^T of positions [block * PB, block * PB + PB) of the chunk, one column per
+    // position, written by the waves that hold those tiles (vb: the wave's tile rows).
+    uint16_t* vt = sh.vt;
+    auto write_vt = [&](int first_tile, const u32x4* vb) {
+        const int column = wave * kTile + tr;
+        const bool current = begin + (first_tile + wave) * kTile + tr == position;
 #pragma unroll
-        for (int q = 0; q < kWords; ++q)
-            dst[q] = BF16 ? pack_bf16(src[2 * q], src[2 * q + 1]) : __float_as_uint(src[q]);
-    }
-    __syncthreads();  // incoming is dead; scores may overwrite the region
-    for (int first = begin; first < end; first += 2 * kBlockRows) {
-        u32x4 raw[2];
-        if (first == begin) {
-            raw[0] = kfirst[0];
-            raw[1] = kfirst[1];
-        } else {
-            load_rows(krsrc, first, raw);
+        for (int k = 0; k < KS; ++k) {
+            const u32x4 now = pack8(sh.vcur + 32 * k + 8 * tk);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t pair = current ? now[q] : vb[k][q];
+                const int dim = 32 * k + 8 * tk + 2 * q;
+                vt[dim * kVtStride + column] = static_cast<uint16_t>(pair);
+                vt[(dim + 1) * kVtStride + column] = static_cast<uint16_t>(pair >> 16);
+            }
         }
+    };
+
+    if constexpr (kMfma) {
+        // A: query head tr (zero past the group); the current K row stands in for the
+        // position's own tile row.
+        u32x4 qa[KS], kc[KS];
+        const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int time = row_time(first, u);
-            const bool current = time == position;
-            uint32_t kw[kWords];
+        for (int k = 0; k < KS; ++k) {
+            qa[k] = tr < group ? pack8(sh.rotated + tr * dh + 32 * k + 8 * tk) : zero;
+            kc[k] = pack8(sh.rotated + group * dh + 32 * k + 8 * tk);
+        }
+        auto tile_scores = [&](int tile, const u32x4* kb) {
+            const int time = begin + tile * kTile + tr;
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                acc = mfma_16x16x32_bf16(qa[k], time == position ? kc[k] : kb[k], acc);
+            // Lanes 0-15 hold heads 0-3 of their position.
+            if (tk == 0 && time < end)
+#pragma unroll
+                for (int g = 0; g < MG; ++g)
+                    if (g < group)
+                        scores[g * span + time - begin] = score_of(acc[g]);
+        };
+        if (wave * kTile < span)
+            tile_scores(wave, kfirst);
+        for (int tile = wave + kWaves; tile * kTile < span; tile += kWaves) {
+            u32x4 kb[KS];
+            load_tile(krsrc, tile, kb);
+            tile_scores(tile, kb);
+        }
+        if (wave < PB / kTile)
+            write_vt(0, vfirst);
+    } else {
+        // Scores of rows [begin, end).  Every lane holds its slice of all MG query heads (heads
+        // past the group compute values that are never stored) and of the current K row.
+        constexpr int kWords = BF16 ? 4 : PV;  // registers per 16-byte slice
+        uint32_t qreg[MG][kWords];
+        uint32_t kcur[kWords];
+#pragma unroll
+        for (int g = 0; g <= MG; ++g) {
+            const float* src = sh.rotated + (g < MG ? g : group) * dh + col * PV;
+            uint32_t* dst = g < MG ? qreg[g] : kcur;
 #pragma unroll
             for (int q = 0; q < kWords; ++q)
-                kw[q] = current ? kcur[q] : raw[u][q];
+                dst[q] = BF16 ? pack_bf16(src[2 * q], src[2 * q + 1]) : __float_as_uint(src[q]);
+        }
+        for (int first = begin; first < end; first += 2 * kBlockRows) {
+            u32x4 raw[2];
+            if (first == begin) {
+                raw[0] = kfirst[0];
+                raw[1] = kfirst[1];
+            } else {
+                load_rows(krsrc, first, raw);
+            }
 #pragma unroll
-            for (int g = 0; g < MG; ++g) {
-                float dot = 0.0f;
-                if constexpr (BF16) {
-                    float a = 0.0f, b = 0.0f;
+            for (int u = 0; u < 2; ++u) {
+                const int time = row_time(first, u);
+                const bool current = time == position;
+                uint32_t kw[kWords];
 #pragma unroll
-                    for (int q = 0; q < 4; q += 2) {
-                        a = dot2_bf16(kw[q], qreg[g][q], a);
-                        b = dot2_bf16(kw[q + 1], qreg[g][q + 1], b);
+                for (int q = 0; q < kWords; ++q)
+                    kw[q] = current ? kcur[q] : raw[u][q];
+#pragma unroll
+                for (int g = 0; g < MG; ++g) {
+                    float dot = 0.0f;
+                    if constexpr (BF16) {
+                        float a = 0.0f, b = 0.0f;
+#pragma unroll
+                        for (int q = 0; q < 4; q += 2) {
+                            a = dot2_bf16(kw[q], qreg[g][q], a);
+                            b = dot2_bf16(kw[q + 1], qreg[g][q + 1], b);
+                        }
+                        dot = a + b;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < PV; ++j)
+                            dot += __uint_as_float(kw[j]) * __uint_as_float(qreg[g][j]);
                     }
-                    dot = a + b;
-                } else {
-#pragma unroll
-                    for (int j = 0; j < PV; ++j)
-                        dot += __uint_as_float(kw[j]) * __uint_as_float(qreg[g][j]);
-                }
-                dot = group_sum<LRK>(dot);
-                if (g < group && col == LRK - 1 && time < end) {
-                    const float rounded = N::round(dot);
-                    scores[g * span + time - begin] = BF16 ? N::round(rounded * scale) : rounded / divisor;
+                    dot = group_sum<LRK>(dot);
+                    if (g < group && col == LRK - 1 && time < end)
+                        scores[g * span + time - begin] = score_of(dot);
                 }
             }
         }
     }
     __syncthreads();
 
-    // Softmax statistics per head: one wave per head.
+    // Softmax per head, one wave each: the maximum, exp(score - max) in place and its sum;
+    // one active chunk then rounds the probabilities exp / sum to the storage type.
     float* stat_max = sh.small;
     float* stat_sum = sh.small + kMaxGroup;
+    const bool fused = chunks == 1;
     if (wave < group) {
+        float* row = scores + wave * span;
         float m = -INFINITY;
         for (int i = lane; i < span; i += 64)
-            m = fmaxf(m, scores[wave * span + i]);
+            m = fmaxf(m, row[i]);
         m = lane_value(group_max(m, 64), 63);
         float sum = 0.0f;
-        for (int i = lane; i < span; i += 64)
-            sum += expf(scores[wave * span + i] - m);
-        sum = group_sum<64>(sum);
+        for (int i = lane; i < span; i += 64) {
+            const float e = expf(row[i] - m);
+            row[i] = e;
+            sum += e;
+        }
+        sum = lane_value(group_sum<64>(sum), 63);
+        if (fused)
+            for (int i = lane; i < span; i += 64)
+                row[i] = N::round(row[i] / sum);
         if (lane == 63) {
             stat_max[wave] = m;
             stat_sum[wave] = sum;
         }
     }
     __syncthreads();
-    const bool fused = chunks == 1;
-    for (int index = threadIdx.x; index < group * span; index += kThreads) {
-        const int g = index / span;
-        const float e = expf(scores[index] - stat_max[g]);
-        scores[index] = fused ? N::round(e / stat_sum[g]) : e;
-    }
-    __syncthreads();
 
-    // P*V over rows [begin, end): each lane accumulates its slice for every head.
-    float vnow[PV];
-#pragma unroll
-    for (int j = 0; j < PV; ++j)
-        vnow[j] = sh.vcur[col * PV + j];
-    float acc[MG * PV];
-#pragma unroll
-    for (int n = 0; n < MG * PV; ++n)
-        acc[n] = 0.0f;
-    for (int first = begin; first < end; first += 2 * kBlockRows) {
-        u32x4 raw[2];
-        if (first == begin) {
-            raw[0] = vfirst[0];
-            raw[1] = vfirst[1];
-        } else {
-            load_rows(vrsrc, first, raw);
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int time = row_time(first, u);
-            const bool inside = time < end;
-            const bool current = time == position;
-            float v[PV];
-#pragma unroll
-            for (int j = 0; j < PV; ++j)
-                v[j] = current ? vnow[j] : N::elem(raw[u], j);
-#pragma unroll
-            for (int g = 0; g < MG; ++g) {
-                // Rows past the chunk, and heads past the group, read in-bounds LDS and weigh 0.
-                const float read = scores[g * span + time - begin];
-                const float p = inside && g < group ? read : 0.0f;
-#pragma unroll
-                for (int j = 0; j < PV; ++j)
-                    acc[g * PV + j] += p * v[j];
-            }
-        }
-    }
-    // Reduce over the rows a wave holds (lanes with equal col), then over waves.
-    residue_sum<LRK>(acc);
-    __syncthreads();  // probabilities are dead
-    float* reduction = sh.region;  // [wave][group][dh]
-    if (sub == 0)
-#pragma unroll
-        for (int g = 0; g < MG; ++g)
-            if (g < group)
-#pragma unroll
-                for (int j = 0; j < PV; ++j)
-                    reduction[(wave * group + g) * dh + col * PV + j] = acc[g * PV + j];
-    __syncthreads();
     // group * dh <= kThreads: each thread owns at most one output element.
     const int mine = threadIdx.x;
     const bool owner = mine < group * dh;
     float out = 0.0f;
-    if (owner)
-        for (int w = 0; w < kWaves; ++w)
-            out += reduction[w * group * dh + mine];
+    if constexpr (kMfma) {
+        // Wave n < dh / 16 accumulates output dims 16 n .. 16 n + 15 of every head over the
+        // chunk's positions, PB at a time: A = probabilities of head tr at 8 consecutive
+        // positions (zero past the group or the span), B = the same positions of V^T row 16 n + tr.
+        f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int n = wave;
+        for (int first = 0; first < span; first += PB) {
+            if (first > 0) {
+                __syncthreads();  // the previous block's V^T has been read
+                if (wave < PB / kTile) {
+                    u32x4 vb[KS];
+                    load_tile(vrsrc, first / kTile + wave, vb);
+                    write_vt(first / kTile, vb);
+                }
+                __syncthreads();
+            }
+            if (n < dh / 16) {
+#pragma unroll
+                for (int q = 0; q < PB / 32; ++q) {
+                    const int t0 = first + 32 * q + 8 * tk;
+                    const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + (16 * n + tr) * kVtStride + 32 * q + 8 * tk);
+                    float p[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        p[e] = tr < group && t0 + e < span ? scores[tr * span + t0 + e] : 0.0f;
+                    if (fused) {
+                        o = mfma_16x16x32_bf16(pack8(p), vb, o);
+                    } else {
+                        // p = hi + mid + lo exactly: each part keeps the next 8 significant bits.
+                        float hi[8], mid[8], lo[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            hi[e] = __uint_as_float(__float_as_uint(p[e]) & 0xffff0000u);
+                            const float rest = p[e] - hi[e];
+                            mid[e] = __uint_as_float(__float_as_uint(rest) & 0xffff0000u);
+                            lo[e] = rest - mid[e];
+                        }
+                        o = mfma_16x16x32_bf16(pack8(hi), vb, o);
+                        o = mfma_16x16x32_bf16(pack8(mid), vb, o);
+                        o = mfma_16x16x32_bf16(pack8(lo), vb, o);
+                    }
+                }
+            }
+        }
+        float* results = sh.rotated;  // [group][dh]: the rotated heads are dead
+        if (n < dh / 16 && tk == 0)
+#pragma unroll
+            for (int g = 0; g < MG; ++g)
+                if (g < group)
+                    results[g * dh + 16 * n + tr] = o[g];
+        __syncthreads();
+        if (owner)
+            out = results[mine];
+    } else {
+        // P*V over rows [begin, end): each lane accumulates its slice for every head.
+        float vnow[PV];
+#pragma unroll
+        for (int j = 0; j < PV; ++j)
+            vnow[j] = sh.vcur[col * PV + j];
+        float acc[MG * PV];
+#pragma unroll
+        for (int n = 0; n < MG * PV; ++n)
+            acc[n] = 0.0f;
+        for (int first = begin; first < end; first += 2 * kBlockRows) {
+            u32x4 raw[2];
+            if (first == begin) {
+                raw[0] = vfirst[0];
+                raw[1] = vfirst[1];
+            } else {
+                load_rows(vrsrc, first, raw);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int time = row_time(first, u);
+                const bool inside = time < end;
+                const bool current = time == position;
+                float v[PV];
+#pragma unroll
+                for (int j = 0; j < PV; ++j)
+                    v[j] = current ? vnow[j] : N::elem(raw[u], j);
+#pragma unroll
+                for (int g = 0; g < MG; ++g) {
+                    // Rows past the chunk, and heads past the group, read in-bounds LDS and weigh 0.
+                    const float read = scores[g * span + time - begin];
+                    const float p = inside && g < group ? read : 0.0f;
+#pragma unroll
+                    for (int j = 0; j < PV; ++j)
+                        acc[g * PV + j] += p * v[j];
+                }
+            }
+        }
+        // Reduce over the rows a wave holds (lanes with equal col), then over waves.
+        residue_sum<LRK>(acc);
+        __syncthreads();  // probabilities are dead
+        float* reduction = sh.region;  // [wave][group][dh]
+        if (sub == 0)
+#pragma unroll
+            for (int g = 0; g < MG; ++g)
+                if (g < group)
+#pragma unroll
+                    for (int j = 0; j < PV; ++j)
+                        reduction[(wave * group + g) * dh + col * PV + j] = acc[g * PV + j];
+        __syncthreads();
+        if (owner)
+            for (int w = 0; w < kWaves; ++w)
+                out += reduction[w * group * dh + mine];
+    }
 
     const uint32_t out_epoch = L.epoch_of(step, layer, kPhaseAttn);
     uint64_t* attn = L.exchange + L.xl.attn + first_head * dh;
