@@ -79,7 +79,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-ctx4096", action="store_true")
     parser.add_argument("--cpu-tokens", type=int, default=24)
-    parser.add_argument("--chunk-steps", type=int, default=128)
+    # 130-step chunks: the 4160-position context splits into 32 chunks per K/V head, 256
+    # attention tasks for 256 workers (128 would give 33 chunks and two tasks to 8 workers).
+    parser.add_argument("--chunk-steps", type=int, default=130)
     parser.add_argument("--write-package", type=Path, default=None,
                         help="only write the benchmark's package to this directory and its ctx-1 prompt to "
                              "DIR.ctx1.json (for `tiles_amd/tile_runtime bench` under a profiler), then exit")

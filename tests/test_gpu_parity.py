@@ -151,8 +151,10 @@ def test_split_context_attention_merge(target, tmp, dtype):
 @pytest.mark.parametrize("head_dim,chunk_steps,fused_steps,context", [
     (64, 128, 128, 101),   # one fused chunk inside one V^T block
     (64, 128, 128, 300),   # three chunks of 100 positions: unnormalized probabilities, merged
-    (64, 256, 256, 250),   # one fused chunk over two V^T blocks and two rounds of score tiles
-    (32, 128, 128, 128),   # one slice per head; a fused chunk ending on a block boundary
+    (64, 130, 130, 130),   # a second tile for waves 0 and 1 (ten tiles in one block)
+    (64, 160, 160, 300),   # two chunks of 150 positions
+    (64, 256, 256, 250),   # one fused chunk over two V^T blocks and three rounds of score tiles
+    (32, 160, 160, 160),   # one slice per head; a fused chunk ending on a block boundary
     (128, 128, 128, 120),  # 64-position V^T blocks: two in one chunk
     (128, 64, 64, 200),    # 128 dims over four 50-position chunks
 ])

@@ -97,10 +97,10 @@ struct Launch {
     }
 };
 
-// bf16 elements of the attention's V^T block: head_dim rows of (block positions + 8), with 128
-// positions per block up to 64 dims and 64 beyond.
-constexpr int kVtElements = kMaxHeadDim * (64 + 8);
-static_assert(64 * (128 + 8) <= kVtElements, "V^T block of a 64-dim head");
+// bf16 elements of the attention's V^T block: head_dim rows of (block positions + 8), with 160
+// positions per block up to 64 dims and 64 beyond.  It shares LDS with the input vector.
+constexpr int kVtElements = kMaxHidden * 3;
+static_assert(64 * (160 + 8) <= kVtElements && kMaxHeadDim * (64 + 8) <= kVtElements, "V^T blocks");
 
 struct Shared {
     union {
@@ -619,8 +619,10 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     constexpr bool kMfma = BF16 && dh % 32 == 0;
     constexpr int KS = dh / 32;                      // 32-dim slices of a head (matrix path)
     constexpr int kTile = 16;                        // positions per matrix tile
-    constexpr int PB = dh > 64 ? 64 : 128;           // positions per V^T block in LDS
+    constexpr int PB = dh > 64 ? 64 : 160;           // positions per V^T block in LDS
     constexpr int kVtStride = PB + 8;                // bf16 elements per V^T row
+    constexpr int kBlockTiles = PB / kTile;
+    constexpr int TW = (kBlockTiles + kWaves - 1) / kWaves;  // tiles per wave in a block
     static_assert(!kMfma || dh * kVtStride <= kVtElements, "V^T block exceeds its LDS area");
     static_assert(!kMfma || dh / 16 <= kWaves, "a wave per 16 output dims");
     constexpr int kRowsPerWave = 64 / LRK;
@@ -673,14 +675,19 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             raw[k] = coherent_load128(rsrc, cached ? offset : kOutside + 16u * k);
         }
     };
+    // Matrix path: tiles wave, wave + 8, ... of the first block; vector path: two rows.
     constexpr int kFirst = kMfma ? KS : 2;
-    u32x4 kfirst[kFirst], vfirst[kFirst];
+    constexpr int kFirstTiles = kMfma ? TW : 1;
+    u32x4 kfirst[kFirstTiles][kFirst], vfirst[kFirstTiles][kFirst];
     if constexpr (kMfma) {
-        load_tile(krsrc, wave, kfirst);
-        load_tile(vrsrc, wave, vfirst);
+#pragma unroll
+        for (int j = 0; j < TW; ++j) {
+            load_tile(krsrc, wave + j * kWaves, kfirst[j]);
+            load_tile(vrsrc, wave + j * kWaves, vfirst[j]);
+        }
     } else {
-        load_rows(krsrc, begin, kfirst);
-        load_rows(vrsrc, begin, vfirst);
+        load_rows(krsrc, begin, kfirst[0]);
+        load_rows(vrsrc, begin, vfirst[0]);
     }
     issue_fence();
 
@@ -739,12 +746,13 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             v[q] = pack_bf16(src[2 * q], src[2 * q + 1]);
         return v;
     };
-    // Matrix path: V^T of positions [block * PB, block * PB + PB) of the chunk, one column per
-    // position, written by the waves that hold those tiles (vb: the wave's tile rows).
+    // Matrix path: V^T of the PB positions from tile first_tile of the chunk, one column per
+    // position; the wave writes its tile wave + 8 j of the block (vb: that tile's rows).
     uint16_t* vt = sh.vt;
-    auto write_vt = [&](int first_tile, const u32x4* vb) {
-        const int column = wave * kTile + tr;
-        const bool current = begin + (first_tile + wave) * kTile + tr == position;
+    auto write_vt = [&](int first_tile, int j, const u32x4* vb) {
+        const int tile = wave + j * kWaves;
+        const int column = tile * kTile + tr;
+        const bool current = begin + (first_tile + tile) * kTile + tr == position;
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
             const u32x4 now = pack8(sh.vcur + 32 * k + 8 * tk);
@@ -781,15 +789,19 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                     if (g < group)
                         scores[g * span + time - begin] = score_of(acc[g]);
         };
-        if (wave * kTile < span)
-            tile_scores(wave, kfirst);
-        for (int tile = wave + kWaves; tile * kTile < span; tile += kWaves) {
+#pragma unroll
+        for (int j = 0; j < TW; ++j)
+            if ((wave + j * kWaves) * kTile < span)
+                tile_scores(wave + j * kWaves, kfirst[j]);
+        for (int tile = wave + TW * kWaves; tile * kTile < span; tile += kWaves) {
             u32x4 kb[KS];
             load_tile(krsrc, tile, kb);
             tile_scores(tile, kb);
         }
-        if (wave < PB / kTile)
-            write_vt(0, vfirst);
+#pragma unroll
+        for (int j = 0; j < TW; ++j)
+            if (wave + j * kWaves < kBlockTiles)
+                write_vt(0, j, vfirst[j]);
     } else {
         // Scores of rows [begin, end).  Every lane holds its slice of all MG query heads (heads
         // past the group compute values that are never stored) and of the current K row.
@@ -807,8 +819,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         for (int first = begin; first < end; first += 2 * kBlockRows) {
             u32x4 raw[2];
             if (first == begin) {
-                raw[0] = kfirst[0];
-                raw[1] = kfirst[1];
+                raw[0] = kfirst[0][0];
+                raw[1] = kfirst[0][1];
             } else {
                 load_rows(krsrc, first, raw);
             }
@@ -886,10 +898,13 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         for (int first = 0; first < span; first += PB) {
             if (first > 0) {
                 __syncthreads();  // the previous block's V^T has been read
-                if (wave < PB / kTile) {
-                    u32x4 vb[KS];
-                    load_tile(vrsrc, first / kTile + wave, vb);
-                    write_vt(first / kTile, vb);
+#pragma unroll
+                for (int j = 0; j < TW; ++j) {
+                    if (wave + j * kWaves < kBlockTiles) {
+                        u32x4 vb[KS];
+                        load_tile(vrsrc, first / kTile + wave + j * kWaves, vb);
+                        write_vt(first / kTile, j, vb);
+                    }
                 }
                 __syncthreads();
             }
@@ -943,8 +958,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         for (int first = begin; first < end; first += 2 * kBlockRows) {
             u32x4 raw[2];
             if (first == begin) {
-                raw[0] = vfirst[0];
-                raw[1] = vfirst[1];
+                raw[0] = vfirst[0][0];
+                raw[1] = vfirst[0][1];
             } else {
                 load_rows(vrsrc, first, raw);
             }
@@ -1014,9 +1029,28 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     __syncthreads();
     if (!sh.flag)
         return;
-    // The last chunk of this head group merges every chunk.  Wave g gathers head g's chunk
-    // statistics (one load per lane and chunk, all in flight together) into LDS:
-    // M = max_c max_c, S = sum_c sum_c exp(max_c - M), weight_c = exp(max_c - M).
+    // The last chunk of this head group merges every chunk: out = sum_c w_c P_c / S with
+    // w_c = exp(max_c - M), M = max_c max_c and S = sum_c w_c sum_c.  Every load of the merge
+    // goes out before any is used: the chunk partials first (threads split an output's chunks
+    // `slices` ways, kBatch chunks each), then wave g's lanes load head g's chunk statistics
+    // (one chunk per lane) into LDS.
+    const int outputs = group * dh;
+    const int slices = kThreads / outputs;
+    const int o = static_cast<int>(threadIdx.x) % outputs, slice = static_cast<int>(threadIdx.x) / outputs;
+    const float* column = partials + static_cast<size_t>(first_head) * dh + o;
+    const size_t chunk_stride = static_cast<size_t>(s.query_heads) * dh;
+    constexpr int kBatch = 32;
+    float part[kBatch];
+    // Unconditional loads (past the last chunk they re-read it): a load whose use is a select
+    // would wait for it before the next one issues.
+    auto load_part = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int c = min(c0 + slice + k * slices, chunks - 1);
+            part[k] = coherent_loadf(column + static_cast<size_t>(c) * chunk_stride);
+        }
+    };
+    load_part(0);
     float* weight = sh.region;                      // [chunks][group]
     float* chunk_sum = sh.region + chunks * group;  // [chunks][group]
     if (wave < group) {
@@ -1040,24 +1074,30 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             sh.small[2 * kMaxGroup + wave] = total;
     }
     __syncthreads();
-    if (owner) {
-        const int g = mine / dh;
-        const float* column = partials + static_cast<size_t>(first_head) * dh + mine;
-        const size_t chunk_stride = static_cast<size_t>(s.query_heads) * dh;
-        float total = 0.0f;
-        int c = 0;
-        for (; c + 4 <= chunks; c += 4) {
-            float v[4];
+    const int g = o / dh;
+    float acc = 0.0f;
+    for (int c0 = 0;;) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                v[k] = coherent_loadf(column + (c + k) * chunk_stride);
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                total += v[k] * weight[(c + k) * group + g];
+        for (int k = 0; k < kBatch; ++k) {
+            const int c = c0 + slice + k * slices;
+            if (c < chunks)
+                acc += part[k] * weight[c * group + g];
         }
-        for (; c < chunks; ++c)
-            total += coherent_loadf(column + c * chunk_stride) * weight[c * group + g];
-        out = total / sh.small[2 * kMaxGroup + g];
+        c0 += kBatch * slices;
+        if (c0 >= chunks)
+            break;
+        load_part(c0);
+    }
+    static_assert(kThreads <= (kMaxGroup + 1) * kMaxHeadDim, "merge sums exceed their LDS area");
+    float* sums = sh.rotated;  // [slices][outputs] (slices * outputs <= kThreads)
+    if (slice < slices)
+        sums[slice * outputs + o] = acc;
+    __syncthreads();
+    if (owner) {
+        float total = 0.0f;
+        for (int j = 0; j < slices; ++j)
+            total += sums[j * outputs + mine];
+        out = total / sh.small[2 * kMaxGroup + mine / dh];
     }
     if (threadIdx.x == 0)
         coherent_store64(counter, 0);
