@@ -4,6 +4,7 @@
 // bandwidth_probe.cu:509-549).
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -181,19 +182,26 @@ extern "C" int ti_describe_target(ti_target* out)
     // Every instantiation of each storage type: the largest registers and LDS, the lowest residency.
     struct Summary { int registers = 0, shared = 0, active = 1 << 30; };
     Summary summary[2];
-    for (int bf16 = 0; bf16 < 2; ++bf16)
-        for (const void* f : bf16 ? worker_functions_bf16() : worker_functions_f32()) {
+    for (int bf16 = 0; bf16 < 2; ++bf16) {
+        std::vector<std::pair<const void*, int>> functions;
+        for (const void* f : bf16 ? worker_functions_bf16() : worker_functions_f32())
+            functions.emplace_back(f, kThreads);
+        if (bf16)
+            for (const void* f : worker_functions_ring())
+                functions.emplace_back(f, kRingThreads);
+        for (const auto& [f, threads] : functions) {
             hipFuncAttributes attributes{};
             int active = 0;
             if ((e = hipFuncGetAttributes(&attributes, f)) != hipSuccess)
                 return hip_fail(e, "worker attributes");
-            if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&active, f, kThreads, 0)) != hipSuccess)
+            if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&active, f, threads, 0)) != hipSuccess)
                 return hip_fail(e, "worker occupancy");
             Summary& t = summary[bf16];
             t.registers = std::max(t.registers, attributes.numRegs);
             t.shared = std::max(t.shared, static_cast<int>(attributes.sharedSizeBytes));
             t.active = std::min(t.active, active);
         }
+    }
     out->f32_registers = summary[0].registers;
     out->f32_shared_bytes = summary[0].shared;
     out->f32_active_blocks = summary[0].active;
@@ -347,6 +355,13 @@ extern "C" int ti_enqueue_worker(void* stream, const ti_worker_program_view* pro
     if (!problem.empty())
         return fail(TI_ERR_INVALID_ARGUMENT, problem.c_str());
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    return program->weight_dtype == TI_DTYPE_BFLOAT16 ? launch_worker_bf16(s, *program, *buffers, position, token, selection)
-                                                      : launch_worker_f32(s, *program, *buffers, position, token, selection);
+    if (program->weight_dtype != TI_DTYPE_BFLOAT16)
+        return launch_worker_f32(s, *program, *buffers, position, token, selection);
+    // TILES_AMD_WORKER selects the worker where a streaming worker exists: "stream" or
+    // "exchange" (read at every launch).  The exchange worker is the default.
+    const char* choice = std::getenv("TILES_AMD_WORKER");
+    const bool stream_worker = choice != nullptr && std::strcmp(choice, "stream") == 0;
+    if (stream_worker && ring_worker_compiled(program->shape, program->weight_dtype))
+        return launch_worker_ring(s, *program, *buffers, position, token, selection);
+    return launch_worker_bf16(s, *program, *buffers, position, token, selection);
 }

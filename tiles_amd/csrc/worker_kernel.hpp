@@ -31,10 +31,36 @@
 #include "tileinfer_amd.h"
 #include "worker_config.hpp"
 
+// Two builds of this source.  The exchange worker (TILES_RING 0): 8 waves run every task and
+// each task streams its own weights.  The streaming worker (TILES_RING 1, bf16 with hidden
+// size 2048): 8 compute waves run the tasks and 4 streamer waves copy every weight row the
+// worker will consume, in consumption order, into a ring of LDS row slots.  The streamers run
+// ahead across tasks, layers and tokens, so HBM keeps streaming while the compute waves wait
+// for their inputs.  The compute waves' own loads (exchange polls, K/V rows) never sit behind
+// bulk weight loads either: a wave's vector loads return in issue order.
+#ifndef TILES_RING
+#define TILES_RING 0
+#endif
+
 namespace tiles {
 namespace {
 
-constexpr int kWaves = kThreads / 64;
+constexpr bool kRing = TILES_RING != 0;
+constexpr int kWaves = kThreads / 64;  // compute waves
+#if TILES_RING
+constexpr int kStreamWaves = 4;
+constexpr int kBlockThreads = kThreads + 64 * kStreamWaves;
+constexpr int kLdsHidden = kRingHidden;
+constexpr int kLdsRegionFloats = kRingRegionFloats;
+constexpr int kLdsStreamRecords = kRingStreamRecords;
+constexpr int kRingRowVectors = kRingHidden * 2 / 16;  // 16-byte vectors of one bf16 weight row
+constexpr int kStageRows = 7;                          // rows in flight per streamer wave
+#else
+constexpr int kBlockThreads = kThreads;
+constexpr int kLdsHidden = kMaxHidden;
+constexpr int kLdsRegionFloats = kRegionFloats;
+constexpr int kLdsStreamRecords = kMaxStreamRecords;
+#endif
 
 // This thread's wave, as a value the compiler knows to be uniform across the wave (a scalar),
 // so that branches on it stay scalar branches.
@@ -97,31 +123,39 @@ struct Launch {
     }
 };
 
-// bf16 elements of the attention's V^T block: head_dim rows of (block positions + 8), with 160
-// positions per block up to 64 dims and 64 beyond.  It shares LDS with the input vector.
-constexpr int kVtElements = kMaxHidden * 3;
-static_assert(64 * (160 + 8) <= kVtElements && kMaxHeadDim * (64 + 8) <= kVtElements, "V^T blocks");
+// bf16 elements of the attention's V^T block: head_dim rows of (block positions + 8).  It
+// shares LDS with the input vector.  A block holds the most positions (a multiple of 32, at most
+// 160) whose rows fit.
+constexpr int kVtElements = kLdsHidden * 3;
+constexpr int vt_block_positions(int dh)
+{
+    int positions = 160;
+    while (positions > 32 && dh * (positions + 8) > kVtElements)
+        positions -= 32;
+    return positions;
+}
+static_assert(kMaxHeadDim * (vt_block_positions(kMaxHeadDim) + 8) <= kVtElements, "V^T blocks");
 
 struct Shared {
     union {
         struct {
-            float vec[kMaxHidden];  // a task's input vector, FP32 values of the storage type
+            float vec[kLdsHidden];  // a task's input vector, FP32 values of the storage type
             // The same vector as bf16 bits (bf16 storage): the GEMV reads each lane's slice as
             // one 16-byte vector at consecutive addresses.  Reading it from `vec` (32 bytes per
             // lane, lanes 32 bytes apart) put 16 lanes on each LDS bank.
-            uint16_t vbits[kMaxHidden];
+            uint16_t vbits[kLdsHidden];
         };
         alignas(16) uint16_t vt[kVtElements];  // attention: V^T of a block of positions (no input vector)
     };
-    alignas(16) float region[kRegionFloats];  // scores/probabilities, reductions, FFN gate/up/product
-    float xsave[kMaxHidden];      // the layer input this worker last read, before the norm
-    float rsave[kMaxHidden];      // the attention block output this worker last read
+    alignas(16) float region[kLdsRegionFloats];  // scores/probabilities, reductions, FFN gate/up/product
+    float xsave[kLdsHidden];      // the layer input this worker last read, before the norm
+    float rsave[kLdsHidden];      // the attention block output this worker last read
     float small[kMaxTaskRows];    // reductions over waves, softmax statistics, residual rows
     float rotated[(kMaxGroup + 1) * kMaxHeadDim];
     float vcur[kMaxHeadDim];
     float rope_cs[kMaxHeadDim];  // the position's RoPE cos (first half) and sin (second half)
     ti_candidate candidates[kWaves];
-    ti_task_record stream[kMaxStreamRecords];  // this worker's instructions, when they fit
+    ti_task_record stream[kLdsStreamRecords];  // this worker's instructions, when they fit
     uint32_t xsave_tag;  // epoch_of(step, layer, kPhaseQKV) of xsave's contents, 0 when empty
     uint32_t rsave_tag;  // epoch_of(step, layer, kPhaseR) of rsave's contents
     int flag;
@@ -129,7 +163,140 @@ struct Shared {
     int token;
     uint64_t mark_read;   // timeline: when the instruction's first exchange read returned
     uint64_t mark_ready;  // timeline: when its last exchange wait ended
+#if TILES_RING
+    // Weight rows in consumption order: slot s of the launch lives in ring[s % kRingSlots].
+    alignas(16) u32x4 ring[kRingSlots * kRingRowVectors];
+    alignas(16) int arrive[kWaves];       // barriers each compute wave has reached
+    alignas(16) int released[kWaves];     // per compute wave: the lowest slot it may still read
+    alignas(16) int landed[kStreamWaves]; // streamer wave q writes slots q, q + 4, ...: 1 + its last one
+    int failed[2];                        // block_sync_and: last barrier a wave failed, by parity
+    int stop;                             // the compute waves left the launch
+#endif
 };
+
+// ---------------------------------------------------------------- block synchronization
+
+// LDS words shared between waves, read and written without caching in registers.
+__device__ inline int lds_read(const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+__device__ inline void lds_write(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+// Waits until this wave's LDS accesses completed (s_waitcnt lgkmcnt(0)), leaving vector memory
+// operations in flight; also a compiler barrier for memory accesses.
+__device__ inline void lds_complete() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+#if TILES_RING
+constexpr uint32_t kRingSpinLimit = 1u << 24;  // polls of an LDS word before a wait is declared stuck
+
+// Minimum of the first N (4 or 8) LDS counters at p (16-byte aligned), read 16 bytes at a
+// time.
+template <int N>
+__device__ inline int lds_min(const int* p)
+{
+    static_assert(N == 4 || N == 8, "whole 16-byte groups");
+    // Through an LDS-address-space pointer: a generic volatile access compiles to a flat load,
+    // which also counts against the vector-memory counter and waits for every load in flight.
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    typedef const volatile __attribute__((address_space(3))) i32x4 lds_i32x4;
+    lds_i32x4* q = (lds_i32x4*)(p);
+    i32x4 a = q[0];
+    int m = min(min(a[0], a[1]), min(a[2], a[3]));
+    if constexpr (N == 8) {
+        a = q[1];
+        m = min(m, min(min(a[0], a[1]), min(a[2], a[3])));
+    }
+    return __builtin_amdgcn_readfirstlane(m);
+}
+
+// Barrier of the compute waves (the streamer waves never take part, so s_barrier cannot be
+// used): each wave counts its arrivals in LDS and waits until every compute wave has arrived
+// as often.  Returns the barrier's number.
+__device__ inline int compute_barrier(Shared& sh)
+{
+    const int w = wave_id();
+    lds_complete();  // this wave's LDS writes land before its arrival does
+    const int generation = __builtin_amdgcn_readfirstlane(lds_read(&sh.arrive[w])) + 1;
+    lds_write(&sh.arrive[w], generation);
+    uint32_t spins = 0;
+    while (lds_min<kWaves>(sh.arrive) < generation) {
+        __builtin_amdgcn_s_sleep(1);
+        // A wave that left the launch never arrives (never expected; no wait is endless), and
+        // once a wait gave up, the launch only drains.
+        if (++spins > kRingSpinLimit || sh.aborted) {
+            sh.aborted = 1;
+            break;
+        }
+    }
+    asm volatile("" ::: "memory");
+    return generation;
+}
+#endif
+
+// Barrier of the waves that run tasks.
+__device__ inline void block_sync(Shared& sh)
+{
+#if TILES_RING
+    compute_barrier(sh);
+#else
+    (void)sh;
+    __syncthreads();
+#endif
+}
+
+// Barrier that also returns whether `pred` held in every task thread.
+__device__ inline bool block_sync_and(Shared& sh, bool pred)
+{
+#if TILES_RING
+    // A failing wave marks the barrier's number in the slot of its parity: a wave that passed
+    // the next barrier cannot overwrite that slot before every wave has read it.
+    const int next = __builtin_amdgcn_readfirstlane(lds_read(&sh.arrive[wave_id()])) + 1;
+    if (!__all(pred))
+        lds_write(&sh.failed[next & 1], next);
+    const int generation = compute_barrier(sh);
+    return lds_read(&sh.failed[generation & 1]) != generation;
+#else
+    (void)sh;
+    return __syncthreads_and(pred);
+#endif
+}
+
+#if TILES_RING
+// ---------------------------------------------------------------- weight ring (compute side)
+
+// Waits until ring slot `slot` holds its row; `have` caches a bound below which every slot
+// has landed.  Streamer wave q writes the slots s = q (mod 4) in order and then sets
+// landed[q] = s + 1 (q - 3 before its first), so every slot below min(landed) + 3 is there.
+__device__ inline void ring_wait(Shared& sh, uint32_t slot, int& have)
+{
+    uint32_t spins = 0;
+    while (static_cast<int>(slot) >= have) {
+        have = lds_min<kStreamWaves>(sh.landed) + kStreamWaves - 1;
+        if (static_cast<int>(slot) < have)
+            break;
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > kRingSpinLimit || sh.aborted) {
+            sh.aborted = 1;
+            have = 0x7fffffff;  // read whatever the slot holds; the launch reports the timeout
+            break;
+        }
+    }
+    asm volatile("" ::: "memory");
+}
+
+__device__ inline const u32x4* ring_row(const Shared& sh, uint32_t slot)
+{
+    return sh.ring + (slot % kRingSlots) * kRingRowVectors;
+}
+
+// This wave reads no ring slot below `slot` any more.  Its reads of those slots precede this
+// write in program order, and one wave's LDS accesses execute in order.  Progress: a wave
+// releases everything below the first slot it needs before it waits, and the slots it waits
+// for lie within kRingSlots of that first slot, so the wave holding the lowest release can
+// always be served.
+__device__ inline void ring_release(Shared& sh, uint32_t slot)
+{
+    asm volatile("" ::: "memory");
+    lds_write(&sh.released[wave_id()], static_cast<int>(slot));
+}
+#endif
 
 // ---------------------------------------------------------------- exchange polling
 
@@ -147,7 +314,7 @@ __device__ inline bool stuck(uint64_t* exchange, const ExchangeLayout& xl, uint3
     return false;
 }
 
-// Reads `count` (at most kMaxHidden) exchange words from `src` until each carries `epoch`
+// Reads `count` (at most kLdsHidden) exchange words from `src` until each carries `epoch`
 // and hands each payload to `sink(index, payload)`.  Block-wide: every thread must call it.
 // The first read is optimistic (one coherent round trip when the producers are done).  If any
 // word is still missing, only wave 0 keeps polling, one "witness" word every `stride` words
@@ -160,7 +327,7 @@ template <typename Sink>
 __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
                                           const ExchangeLayout& xl, Shared& sh, Sink sink)
 {
-    constexpr int kBatch = (kMaxHidden + kThreads - 1) / kThreads;
+    constexpr int kBatch = (kLdsHidden + kThreads - 1) / kThreads;
     constexpr int kWitnessBatch = 8;
     uint64_t w[kBatch];
 #pragma unroll
@@ -179,7 +346,7 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
             ok &= static_cast<uint32_t>(w[k] >> 32) == epoch;
         return ok;
     };
-    const bool all_present = __syncthreads_and(read());
+    const bool all_present = block_sync_and(sh, read());
     if (threadIdx.x == 0 && sh.mark_read == 0)
         sh.mark_read = __builtin_amdgcn_s_memrealtime();
     if (!all_present) {
@@ -210,9 +377,9 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
                     break;
             }
         }
-        __syncthreads();
+        block_sync(sh);
         uint32_t spins = 0;
-        while (!__syncthreads_and(read()) && !sh.aborted) {
+        while (!block_sync_and(sh, read()) && !sh.aborted) {
             __builtin_amdgcn_s_sleep(2);
             if (threadIdx.x == 0)
                 stuck(exchange, xl, ++spins, sh);
@@ -281,7 +448,7 @@ __device__ __forceinline__ void wait_witnesses(int n, Witness witness, uint32_t 
                 break;
         }
     }
-    __syncthreads();
+    block_sync(sh);
 }
 
 template <bool BF16>
@@ -309,14 +476,14 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, in
                               ? static_cast<const void*>(L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) +
                                                                         static_cast<size_t>(token) * d))
                               : L.input;
-        float v[kMaxHidden / kThreads];
+        float v[kLdsHidden / kThreads];
 #pragma unroll
-        for (int k = 0; k < kMaxHidden / kThreads; ++k) {  // all loads in flight together
+        for (int k = 0; k < kLdsHidden / kThreads; ++k) {  // all loads in flight together
             const int i = k * kThreads + static_cast<int>(threadIdx.x);
             v[k] = Num<BF16>::load(row, i < d ? i : 0);
         }
 #pragma unroll
-        for (int k = 0; k < kMaxHidden / kThreads; ++k) {
+        for (int k = 0; k < kLdsHidden / kThreads; ++k) {
             const int i = k * kThreads + static_cast<int>(threadIdx.x);
             if (i < d)
                 dst[i] = sh.xsave[i] = v[k];
@@ -360,7 +527,7 @@ __device__ __forceinline__ float attention_output_element(const Launch<BF16>& L,
 // A norm's scale elements threadIdx.x + k * kThreads, loaded into registers before the task
 // waits for its input (a load issued after the wait would add a full memory latency).
 struct NormScale {
-    float v[kMaxHidden / kThreads];
+    float v[kLdsHidden / kThreads];
 };
 
 template <bool BF16>
@@ -370,7 +537,7 @@ __device__ __forceinline__ NormScale load_scale(const void* scale, int d)
     // loaded value would make the load's wait immediate.
     NormScale s;
 #pragma unroll
-    for (int k = 0; k < kMaxHidden / kThreads; ++k) {
+    for (int k = 0; k < kLdsHidden / kThreads; ++k) {
         const int i = k * kThreads + static_cast<int>(threadIdx.x);
         s.v[k] = Num<BF16>::load(scale, i < d ? i : d - 1);
     }
@@ -383,26 +550,26 @@ __device__ __forceinline__ NormScale load_scale(const void* scale, int d)
 template <bool BF16>
 __device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& scale, float eps, Shared& sh)
 {
-    float x[kMaxHidden / kThreads];  // all reads first (v holds kMaxHidden floats)
+    float x[kLdsHidden / kThreads];  // all reads first (v holds kLdsHidden floats)
 #pragma unroll
-    for (int k = 0; k < kMaxHidden / kThreads; ++k)
+    for (int k = 0; k < kLdsHidden / kThreads; ++k)
         x[k] = v[k * kThreads + threadIdx.x];
     float sum = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMaxHidden / kThreads; ++k)
+    for (int k = 0; k < kLdsHidden / kThreads; ++k)
         sum += k * kThreads + static_cast<int>(threadIdx.x) < d ? x[k] * x[k] : 0.0f;
     sum = group_sum<64>(sum);
     const int lane = threadIdx.x & 63, wave = wave_id();
-    __syncthreads();
+    block_sync(sh);
     if (lane == 63)
         sh.small[wave] = sum;
-    __syncthreads();
+    block_sync(sh);
     float total = 0.0f;
     for (int w = 0; w < kWaves; ++w)
         total += sh.small[w];
     const float inv = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
 #pragma unroll
-    for (int k = 0; k < kMaxHidden / kThreads; ++k) {
+    for (int k = 0; k < kLdsHidden / kThreads; ++k) {
         const int i = k * kThreads + static_cast<int>(threadIdx.x);
         if (i < d) {
             v[i] = Num<BF16>::round(Num<BF16>::round(v[i] * inv) * scale.v[k]);
@@ -410,7 +577,7 @@ __device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& s
                 sh.vbits[i] = static_cast<uint16_t>(float_to_bf16_bits(v[i]));
         }
     }
-    __syncthreads();
+    block_sync(sh);
 }
 
 // ---------------------------------------------------------------- GEMV over rows
@@ -434,21 +601,89 @@ struct RowGeometry {
     __device__ int first_row(int r0, int pass) const { return r0 + pass * pass_rows + wave * rows_per_wave; }
 };
 
+// The lane's slice of a hidden-width vector u in LDS, one 16-byte vector per k: packed bf16
+// pairs for v_dot2_f32_bf16, or four FP32 values.
+template <int VPL>
+struct InputSlice {
+    uint32_t r[VPL * 4];
+    __device__ InputSlice(const void* u, int col, int lr)
+    {
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+            const u32x4 v = static_cast<const u32x4*>(u)[col + k * lr];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                r[k * 4 + q] = v[q];
+        }
+    }
+    // The lane's part of one row's dot product (VPL 16-byte vectors of the row).
+    template <bool BF16>
+    __device__ float dot(const u32x4* wm) const
+    {
+        using N = Num<BF16>;
+        if constexpr (BF16) {
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent chains
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    a[q] = dot2_bf16(wm[k][q], r[k * 4 + q], a[q]);
+            return (a[0] + a[1]) + (a[2] + a[3]);
+        } else {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int j = 0; j < N::kPerVec; ++j)
+                    acc += N::elem(wm[k], j) * __uint_as_float(r[k * 4 + j]);
+            return acc;
+        }
+    }
+};
+
 // Dot products of rows [r0, r1) of NM matrices of hidden width with the vector u in LDS
-// (sh.vbits for bf16 storage, sh.vec for fp32: see gemv_input).
-// row_offset(m, row) is the byte offset from `base` of a row of matrix m (below 2 GiB).  D passes of loads are in flight; all
-// D issue before `prepare`, which runs block-wide, waits for the task's inputs and writes u,
-// so weight latency overlaps the wait.  emit(row, dots) runs in each row group's last lane
-// with one dot per matrix.
+// (sh.vbits for bf16 storage, sh.vec for fp32: see gemv_input).  emit(row, dots) runs in each
+// row group's last lane with one dot per matrix.
+//
+// Exchange worker: row_offset(m, row) is the byte offset from `base` of a row of matrix m
+// (below 2 GiB).  D passes of loads are in flight; all D issue before `prepare`, which runs
+// block-wide, waits for the task's inputs and writes u, so weight latency overlaps the wait.
+// Streaming worker: row r0 + j is ring slot slot0 + j (NM == 1); wave w takes rows j = w,
+// w + 8, ... as in the exchange worker's passes, so both compute the same sums.
 template <bool BF16, int VPL, int NM, int DEPTH = 0, typename RowOffset, typename Prepare, typename Emit>
 __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int r0, int r1, int cols, const void* u,
-                                    Prepare prepare, Emit emit)
+                                    uint32_t slot0, Shared& sh, Prepare prepare, Emit emit)
 {
     using N = Num<BF16>;
-    constexpr int PV = N::kPerVec;
     constexpr int K = VPL * NM;
     constexpr int D = DEPTH > 0 ? DEPTH : (K <= 4 ? 4 : (K <= 8 ? 2 : 1));
     const RowGeometry<BF16> g(cols);
+#if TILES_RING
+    static_assert(BF16 && NM == 1 && VPL * 64 == kRingRowVectors, "ring rows are whole bf16 hidden rows");
+    (void)base;
+    (void)row_offset;
+    (void)D;
+    prepare();
+    const InputSlice<VPL> in(u, g.col, g.lr);
+    const int rows = r1 - r0;
+    int have = 0;
+    for (int j = g.wave; j < rows; j += kWaves) {
+        const uint32_t slot = slot0 + static_cast<uint32_t>(j);
+        ring_wait(sh, slot, have);
+        const u32x4* ring = ring_row(sh, slot);
+        u32x4 w[VPL];
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+            w[k] = ring[k * 64 + g.col];
+        float dots[1] = {group_sum<64>(in.template dot<BF16>(w))};
+        ring_release(sh, slot0 + static_cast<uint32_t>(min(j + kWaves, rows)));
+        if (g.col == 63)
+            emit(r0 + j, dots);
+    }
+    ring_release(sh, slot0 + static_cast<uint32_t>(rows));
+#else
+    (void)slot0;
+    (void)sh;
     auto active = [&](int pass) { return g.first_row(r0, pass) < r1; };
     // Lanes past the task read the task's first row from its start, 16 bytes apart per k: one
     // cached request per instruction.  Their addresses differ per k on purpose: equal ones let
@@ -475,51 +710,27 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
         issue(s, w[s]);
     issue_fence();
     prepare();
-    // The lane's slice of u in registers, one 16-byte LDS vector per k: packed bf16 pairs
-    // for v_dot2_f32_bf16, or four FP32 values.
-    uint32_t ur[VPL * 4];
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-        const u32x4 v = static_cast<const u32x4*>(u)[g.col + k * g.lr];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            ur[k * 4 + q] = v[q];
-    }
-    auto dot = [&](const u32x4* wm) {
-        if constexpr (BF16) {
-            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent chains
-#pragma unroll
-            for (int k = 0; k < VPL; ++k)
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    a[q] = dot2_bf16(wm[k][q], ur[k * 4 + q], a[q]);
-            return (a[0] + a[1]) + (a[2] + a[3]);
-        } else {
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < VPL; ++k)
-#pragma unroll
-                for (int j = 0; j < PV; ++j)
-                    acc += N::elem(wm[k], j) * __uint_as_float(ur[k * 4 + j]);
-            return acc;
-        }
-    };
-    for (int base = 0; active(base); base += D) {
+    const InputSlice<VPL> in(u, g.col, g.lr);
+    for (int pass0 = 0; active(pass0); pass0 += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
-            const int pass = base + s;
+            const int pass = pass0 + s;
             if (!active(pass))
                 break;
             float dots[NM];
 #pragma unroll
-            for (int m = 0; m < NM; ++m)
-                dots[m] = VPL > 1 ? group_sum<64>(dot(&w[s][m * VPL])) : group_sum(dot(&w[s][m * VPL]), g.lr);
+            for (int m = 0; m < NM; ++m) {
+                const float part = in.template dot<BF16>(&w[s][m * VPL]);
+                dots[m] = VPL > 1 ? group_sum<64>(part) : group_sum(part, g.lr);
+            }
             issue(pass + D, w[s]);
             const int row = g.first_row(r0, pass) + g.sub;
             if (row < r1 && g.col == g.lr - 1)
                 emit(row, dots);
         }
     }
+    (void)N::kBytes;
+#endif
 }
 
 // ---------------------------------------------------------------- operations
@@ -535,7 +746,8 @@ __device__ inline const void* gemv_input(const Shared& sh)
 // token's attention takes V from the exchange words, and the worker's next input poll waits for
 // the cache stores before it publishes anything else, so later tokens find the row complete.
 template <bool BF16, int VPL>
-__device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_record& t, int step, ti_token_id token, Shared& sh)
+__device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_record& t, int step, ti_token_id token, uint32_t slot0,
+                                       Shared& sh)
 {
     using N = Num<BF16>;
     const int d = L.shape.hidden_size;
@@ -557,11 +769,11 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.attn_norm), d);
     auto prepare = [&]() {
         load_hidden(L, layer, step, token, sh.vec, sh);
-        __syncthreads();
+        block_sync(sh);
         rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
     };
     float* staged_v = sh.small;  // this task's V rows, for the cache stores after the GEMV
-    gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, 0), row_offset, begin, end, d, gemv_input<BF16>(sh), prepare,
+    gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, 0), row_offset, begin, end, d, gemv_input<BF16>(sh), slot0, sh, prepare,
                        [&](int row, const float* dots) {
         const float value = N::round(dots[0]);
         publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
@@ -571,7 +783,7 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     const int first_v = begin > d + kvw ? begin : d + kvw;
     if (end <= first_v)
         return;
-    __syncthreads();
+    block_sync(sh);
     void* cache = L.cache(layer, L.layout.value);
     for (int row = first_v + static_cast<int>(threadIdx.x); row < end; row += kThreads) {
         const size_t index = static_cast<size_t>(position) * kvw + (row - d - kvw);
@@ -619,7 +831,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     constexpr bool kMfma = BF16 && dh % 32 == 0;
     constexpr int KS = dh / 32;                      // 32-dim slices of a head (matrix path)
     constexpr int kTile = 16;                        // positions per matrix tile
-    constexpr int PB = dh > 64 ? 64 : 160;           // positions per V^T block in LDS
+    constexpr int PB = vt_block_positions(dh);       // positions per V^T block in LDS
     constexpr int kVtStride = PB + 8;                // bf16 elements per V^T row
     constexpr int kBlockTiles = PB / kTile;
     constexpr int TW = (kBlockTiles + kWaves - 1) / kWaves;  // tiles per wave in a block
@@ -705,7 +917,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     poll_words(L.exchange + L.xl.qkv + static_cast<size_t>(kv_head) * block, block,
                row_stride(s.hidden_size + 2 * kvw, L.workers), L.epoch_of(step, layer, kPhaseQKV), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { incoming[i] = N::from_payload(p); });
-    __syncthreads();
+    block_sync(sh);
     for (int index = threadIdx.x; index < (group + 1) * half; index += kThreads) {
         const int head = index / half, pair = index - head * half;
         const float c = sh.rope_cs[pair], sn = sh.rope_cs[half + pair];
@@ -715,7 +927,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     }
     for (int index = threadIdx.x; index < dh; index += kThreads)
         sh.vcur[index] = incoming[(group + 1) * dh + index];
-    __syncthreads();  // incoming is dead: the scores may overwrite the region
+    block_sync(sh);  // incoming is dead: the scores may overwrite the region
     if (chunk == 0) {
         for (int index = threadIdx.x; index < (group + 1) * dh; index += kThreads) {
             const float value = sh.rotated[index];
@@ -855,7 +1067,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             }
         }
     }
-    __syncthreads();
+    block_sync(sh);
 
     // Softmax per head, one wave each: the maximum, exp(score - max) in place and its sum;
     // one active chunk then rounds the probabilities exp / sum to the storage type.
@@ -883,7 +1095,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             stat_sum[wave] = sum;
         }
     }
-    __syncthreads();
+    block_sync(sh);
 
     // group * dh <= kThreads: each thread owns at most one output element.
     const int mine = threadIdx.x;
@@ -897,7 +1109,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         const int n = wave;
         for (int first = 0; first < span; first += PB) {
             if (first > 0) {
-                __syncthreads();  // the previous block's V^T has been read
+                block_sync(sh);  // the previous block's V^T has been read
 #pragma unroll
                 for (int j = 0; j < TW; ++j) {
                     if (wave + j * kWaves < kBlockTiles) {
@@ -906,7 +1118,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                         write_vt(first / kTile, j, vb);
                     }
                 }
-                __syncthreads();
+                block_sync(sh);
             }
             if (n < dh / 16) {
 #pragma unroll
@@ -942,7 +1154,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             for (int g = 0; g < MG; ++g)
                 if (g < group)
                     results[g * dh + 16 * n + tr] = o[g];
-        __syncthreads();
+        block_sync(sh);
         if (owner)
             out = results[mine];
     } else {
@@ -985,7 +1197,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         }
         // Reduce over the rows a wave holds (lanes with equal col), then over waves.
         residue_sum<LRK>(acc);
-        __syncthreads();  // probabilities are dead
+        block_sync(sh);  // probabilities are dead
         float* reduction = sh.region;  // [wave][group][dh]
         if (sub == 0)
 #pragma unroll
@@ -994,7 +1206,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 #pragma unroll
                     for (int j = 0; j < PV; ++j)
                         reduction[(wave * group + g) * dh + col * PV + j] = acc[g * PV + j];
-        __syncthreads();
+        block_sync(sh);
         if (owner)
             for (int w = 0; w < kWaves; ++w)
                 out += reduction[w * group * dh + mine];
@@ -1020,13 +1232,13 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         coherent_storef(stats + threadIdx.x * 2 + 1, stat_sum[threadIdx.x]);
     }
     wait_stores();
-    __syncthreads();
+    block_sync(sh);
     uint64_t* counter = L.exchange + L.xl.counters + layer * s.kv_heads + kv_head;
     if (threadIdx.x == 0) {
         const uint64_t before = coherent_fetch_add64(counter, 1ull);
         sh.flag = before == static_cast<uint64_t>(chunks - 1);
     }
-    __syncthreads();
+    block_sync(sh);
     if (!sh.flag)
         return;
     // The last chunk of this head group merges every chunk: out = sum_c w_c P_c / S with
@@ -1073,7 +1285,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         if (lane == 63)
             sh.small[2 * kMaxGroup + wave] = total;
     }
-    __syncthreads();
+    block_sync(sh);
     const int g = o / dh;
     float acc = 0.0f;
     for (int c0 = 0;;) {
@@ -1092,7 +1304,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     float* sums = sh.rotated;  // [slices][outputs] (slices * outputs <= kThreads)
     if (slice < slices)
         sums[slice * outputs + o] = acc;
-    __syncthreads();
+    block_sync(sh);
     if (owner) {
         float total = 0.0f;
         for (int j = 0; j < slices; ++j)
@@ -1102,7 +1314,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     if (threadIdx.x == 0)
         coherent_store64(counter, 0);
     wait_stores();
-    __syncthreads();
+    block_sync(sh);
     if (owner)
         publish<BF16>(attn, mine, N::round(out), out_epoch);
 }
@@ -1110,7 +1322,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 // Wo rows plus the residual (ops.cuh:718-734): r = round(round(Wo a) + x).
 template <bool BF16, int VPL>
 __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, const ti_task_record& t, int step,
-                                                    ti_token_id token, Shared& sh)
+                                                    ti_token_id token, uint32_t slot0, Shared& sh)
 {
     using N = Num<BF16>;
     const int d = L.shape.hidden_size;
@@ -1128,13 +1340,13 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
                        sh.vec[i] = N::from_payload(p);
                        sh.vbits[i] = static_cast<uint16_t>(p);
                    });
-        __syncthreads();
+        block_sync(sh);
         if (begin == 0)
             for (int i = threadIdx.x; i < d; i += kThreads)
                 N::store(L.scratch, L.layout.attention + i, sh.vec[i]);
     };
     gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, L.layout.Wo), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
-                       begin, end, d, gemv_input<BF16>(sh), prepare, [&](int row, const float* dots) {
+                       begin, end, d, gemv_input<BF16>(sh), slot0, sh, prepare, [&](int row, const float* dots) {
                            const float r = N::round(N::round(dots[0]) + residual[row - begin]);
                            N::store(L.scratch, L.layout.r + row, r);
                            publish<BF16>(L.exchange + L.xl.r, row, r, epoch);
@@ -1151,7 +1363,8 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
 // columns that match its input slice; waves then sum their partials through LDS.  D passes are
 // in flight, all issued before the task waits for r.
 template <bool BF16, int VPL>
-__device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
+__device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_record& t, int step, uint32_t slot0,
+                                      Shared& sh)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
@@ -1162,12 +1375,13 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     const int layer = static_cast<int>(t.layer);
     const int r0 = static_cast<int>(t.begin), r1 = static_cast<int>(t.end);
     const RowGeometry<BF16> g(d);
+    const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.ffn_norm), d);
+    auto row_of = [&](int pass) { return g.first_row(r0, pass) + g.sub; };
+#if !TILES_RING
     const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
     const char* gate = L.layer_weight(layer, L.layout.Wgate) + g.col * 16;
     const char* up = L.layer_weight(layer, L.layout.Wup) + g.col * 16;
     const char* down = L.layer_weight(layer, L.layout.Wdown) + g.col * 16;
-    const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.ffn_norm), d);
-    auto row_of = [&](int pass) { return g.first_row(r0, pass) + g.sub; };
     // Lanes past the chunk all read the first 16 bytes of its first row (one cached request
     // per instruction); their product is zero.
     auto issue = [&](int pass, u32x4* w) {
@@ -1187,75 +1401,155 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     for (int s = 0; s < D; ++s)
         issue(s, w[s]);
     issue_fence();
+#endif
 
     poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
     if (threadIdx.x == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
-    __syncthreads();
+    block_sync(sh);
     rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
-    uint32_t ur[VPL * 4];
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-        const u32x4 v = static_cast<const u32x4*>(gemv_input<BF16>(sh))[g.col + k * g.lr];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            ur[k * 4 + q] = v[q];
-    }
-    auto dot = [&](const u32x4* wm) {
-        if constexpr (BF16) {
-            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int k = 0; k < VPL; ++k)
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    a[q] = dot2_bf16(wm[k][q], ur[k * 4 + q], a[q]);
-            return (a[0] + a[1]) + (a[2] + a[3]);
-        } else {
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < VPL; ++k)
-#pragma unroll
-                for (int j = 0; j < PV; ++j)
-                    acc += N::elem(wm[k], j) * __uint_as_float(ur[k * 4 + j]);
-            return acc;
-        }
-    };
+    const InputSlice<VPL> in(gemv_input<BF16>(sh), g.col, g.lr);
     float acc[kOut];
 #pragma unroll
     for (int n = 0; n < kOut; ++n)
         acc[n] = 0.0f;
     const int lane = threadIdx.x & 63;
+    // One product row: gate and up dots, p = round(round(silu(round(gate))) * round(up)) (zero
+    // past the chunk), then the lane's slice of the down row times p.
+    auto product_row = [&](const u32x4* wg, const u32x4* wu, const u32x4* wd, int row) {
+        float gate_dot = VPL > 1 ? group_sum<64>(in.template dot<BF16>(wg)) : group_sum(in.template dot<BF16>(wg), g.lr);
+        float up_dot = VPL > 1 ? group_sum<64>(in.template dot<BF16>(wu)) : group_sum(in.template dot<BF16>(wu), g.lr);
+        // The group's sums sit in its last lane (in every lane when the group has <= 16).
+        if (g.lr == 64) {
+            gate_dot = lane_value(gate_dot, 63);
+            up_dot = lane_value(up_dot, 63);
+        } else if (g.lr == 32) {
+            gate_dot = __shfl(gate_dot, (lane & 32) | 31);
+            up_dot = __shfl(up_dot, (lane & 32) | 31);
+        }
+        const float gr = N::round(gate_dot);
+        const float silu = N::round(gr / (1.0f + expf(-gr)));
+        const float p = row < r1 ? N::round(silu * N::round(up_dot)) : 0.0f;
+        if (row < r1 && g.col == g.lr - 1)
+            N::store(L.scratch, L.layout.product + row, p);
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+#pragma unroll
+            for (int j = 0; j < PV; ++j)
+                acc[k * PV + j] += N::elem(wd[k], j) * p;
+    };
+#if TILES_RING
+    // Two phases over the ring.  Gate and up of row r0 + j are slots slot0 + 2 j and + 1: wave
+    // w takes rows j = w, w + 8, ... (the exchange worker's passes) and leaves p_j in LDS.  The
+    // down rows follow as slots slot0 + 2 n + j, each read by every wave: wave w owns output
+    // columns 256 w + 4 lane .. + 3 and sums row j into accumulator j mod 8, the wave that
+    // holds row j in the exchange worker.  The eight accumulators are then added in wave order,
+    // the exchange worker's cross-wave sum, so both publish the same bits with no reduction
+    // through LDS.
+    static_assert(BF16 && VPL * 64 == kRingRowVectors, "ring rows are whole bf16 hidden rows");
+    static_assert(kOut == 32 && kWaves == 8, "a lane owns 4 columns of the down rows in 8 classes");
+    static_assert(2 * (kWaves + 1) <= kRingSlots, "a wave's two rows of gate and up fit the ring");
+    (void)row_of;
+    (void)D;
+    (void)NV;
+    (void)product_row;
+    (void)acc;
+    const int rows = r1 - r0;
+    float* pvals = sh.small;  // p of each row of the chunk (rows <= kMaxTaskRows)
+    int have = 0;
+    // Phase 1, two rows per wave at a time (j and j + 8): their reductions overlap.
+    auto product = [&](const u32x4* wg, const u32x4* wu, int j) {
+        const float gate_dot = lane_value(group_sum<64>(in.template dot<BF16>(wg)), 63);
+        const float up_dot = lane_value(group_sum<64>(in.template dot<BF16>(wu)), 63);
+        const float gr = N::round(gate_dot);
+        const float silu = N::round(gr / (1.0f + expf(-gr)));
+        const float p = N::round(silu * N::round(up_dot));
+        if (g.col == 63) {
+            N::store(L.scratch, L.layout.product + r0 + j, p);
+            pvals[j] = p;
+        }
+    };
+    for (int j = g.wave; j < rows; j += 2 * kWaves) {
+        const bool second = j + kWaves < rows;
+        const int last = second ? j + kWaves : j;
+        // Before waiting, release everything below this wave's first slot: a wave waiting for
+        // slots beyond the window must not hold the window back (every wave's two rows span 18
+        // slots, inside the ring).
+        ring_release(sh, slot0 + 2u * static_cast<uint32_t>(j));
+        ring_wait(sh, slot0 + 2u * static_cast<uint32_t>(last) + 1u, have);
+        u32x4 w[4][VPL];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int row = m < 2 ? j : last;  // the second pair repeats the first without a second row
+            const u32x4* ring = ring_row(sh, slot0 + 2u * static_cast<uint32_t>(row) + (m & 1));
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+                w[m][k] = ring[k * 64 + g.col];
+        }
+        ring_release(sh, slot0 + 2u * static_cast<uint32_t>(min(j + 2 * kWaves, rows)));
+        product(w[0], w[1], j);
+        if (second)
+            product(w[2], w[3], j + kWaves);
+    }
+    ring_release(sh, slot0 + 2u * static_cast<uint32_t>(rows));
+    block_sync(sh);
+    // Phase 2, eight down rows per wait: every read issues before any is used.
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    float part[kWaves][4];
+#pragma unroll
+    for (int c = 0; c < kWaves; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            part[c][e] = 0.0f;
+    const uint32_t down0 = slot0 + 2u * static_cast<uint32_t>(rows);
+    const int column = g.wave * 256 + 4 * lane;
+    for (int j0 = 0; j0 < rows; j0 += kWaves) {
+        const int count = min(kWaves, rows - j0);
+        ring_wait(sh, down0 + static_cast<uint32_t>(j0 + count - 1), have);
+        u32x2 wd[kWaves];
+        float pj[kWaves];
+#pragma unroll
+        for (int c = 0; c < kWaves; ++c) {
+            const int j = j0 + (c < count ? c : 0);  // past the chunk: re-read a row, weight 0
+            wd[c] = reinterpret_cast<const u32x2*>(ring_row(sh, down0 + static_cast<uint32_t>(j)))[column / 4];
+            pj[c] = pvals[j];
+        }
+        ring_release(sh, down0 + static_cast<uint32_t>(j0 + count));
+#pragma unroll
+        for (int c = 0; c < kWaves; ++c) {
+            if (c < count) {
+                part[c][0] += __uint_as_float(wd[c][0] << 16) * pj[c];
+                part[c][1] += __uint_as_float(wd[c][0] & 0xffff0000u) * pj[c];
+                part[c][2] += __uint_as_float(wd[c][1] << 16) * pj[c];
+                part[c][3] += __uint_as_float(wd[c][1] & 0xffff0000u) * pj[c];
+            }
+        }
+    }
+    const uint32_t out_epoch = L.epoch_of(step, layer, kPhaseFfn);
+    uint64_t* chunk_partials = L.exchange + L.xl.ffn + static_cast<size_t>(t.chunk) * d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float total = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kWaves; ++c)
+            total += part[c][e];
+        coherent_store64(chunk_partials + column + e, (static_cast<uint64_t>(out_epoch) << 32) | __float_as_uint(total));
+    }
+    return;
+#else
+    (void)slot0;
     for (int base = 0; g.first_row(r0, base) < r1; base += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
             const int pass = base + s;
             if (g.first_row(r0, pass) >= r1)
                 break;
-            float gate = VPL > 1 ? group_sum<64>(dot(&w[s][0])) : group_sum(dot(&w[s][0]), g.lr);
-            float up = VPL > 1 ? group_sum<64>(dot(&w[s][VPL])) : group_sum(dot(&w[s][VPL]), g.lr);
-            // The group's sums sit in its last lane (in every lane when the group has <= 16).
-            if (g.lr == 64) {
-                gate = lane_value(gate, 63);
-                up = lane_value(up, 63);
-            } else if (g.lr == 32) {
-                gate = __shfl(gate, (lane & 32) | 31);
-                up = __shfl(up, (lane & 32) | 31);
-            }
-            const int row = row_of(pass);
-            const float gr = N::round(gate);
-            const float silu = N::round(gr / (1.0f + expf(-gr)));
-            const float p = row < r1 ? N::round(silu * N::round(up)) : 0.0f;
-            if (row < r1 && g.col == g.lr - 1)
-                N::store(L.scratch, L.layout.product + row, p);
-#pragma unroll
-            for (int k = 0; k < VPL; ++k)
-#pragma unroll
-                for (int j = 0; j < PV; ++j)
-                    acc[k * PV + j] += N::elem(w[s][2 * VPL + k], j) * p;
+            product_row(&w[s][0], &w[s][VPL], &w[s][2 * VPL], row_of(pass));
             issue(pass + D, w[s]);
         }
     }
+#endif
     // Lanes of one wave that hold the same columns (several rows per pass) add up first.
     if (g.lr < 64)
         residue_sum(acc, g.lr);
@@ -1266,11 +1560,11 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     uint64_t* partials = L.exchange + L.xl.ffn + static_cast<size_t>(t.chunk) * d;
     float* reduction = sh.region;
     const int slice = g.lr * PV;
-    constexpr int KS = VPL >= 2 ? 2 : 1;
-    static_assert(kWaves * 64 * PV * KS <= kRegionFloats, "FFN reduction rounds exceed the work region");
+    constexpr int KS = VPL >= 2 && kWaves * 64 * PV * 2 <= kLdsRegionFloats ? 2 : 1;
+    static_assert(kWaves * 64 * PV * KS <= kLdsRegionFloats, "FFN reduction rounds exceed the work region");
 #pragma unroll
     for (int k0 = 0; k0 < VPL; k0 += KS) {
-        __syncthreads();
+        block_sync(sh);
         if (g.sub == 0)
 #pragma unroll
             for (int kk = 0; kk < KS; ++kk)
@@ -1281,7 +1575,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
                         u32x4{__float_as_uint(acc[k * PV + 4 * h]), __float_as_uint(acc[k * PV + 4 * h + 1]),
                               __float_as_uint(acc[k * PV + 4 * h + 2]), __float_as_uint(acc[k * PV + 4 * h + 3])};
                 }
-        __syncthreads();
+        block_sync(sh);
         for (int o = threadIdx.x; o < KS * slice; o += kThreads) {
             const int kk = o / slice, c = o - kk * slice;
             float total = 0.0f;
@@ -1381,7 +1675,7 @@ __device__ __forceinline__ void final_normalized(const Launch<BF16>& L, int step
     const int layers = L.stack.layers;
     poll_words(L.exchange + L.xl.hidden(layers % 2), d, row_stride(d, L.workers), L.epoch_of(step, layers - 1, kPhaseY),
                L.exchange, L.xl, sh, [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
-    __syncthreads();
+    block_sync(sh);
     rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
 }
 
@@ -1398,7 +1692,7 @@ __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const t
 // logits round to the storage type, then widen; the largest value wins, the lowest ID among
 // equals, and any non-finite logit makes the candidate kNonFinite.
 template <bool BF16, int VPL>
-__device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
+__device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_record& t, int step, uint32_t slot0, Shared& sh)
 {
     const int d = L.shape.hidden_size;
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
@@ -1407,7 +1701,7 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     const uint32_t row_bytes = static_cast<uint32_t>(d) * Num<BF16>::kBytes;
     const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
     gemv<BF16, VPL, 1, 4>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
-                       begin, end, d, gemv_input<BF16>(sh),
+                       begin, end, d, gemv_input<BF16>(sh), slot0, sh,
                        [&]() { final_normalized(L, step, scale, sh); },
                        [&](int row, const float* dots) {
                            const float logit = Num<BF16>::round(dots[0]);
@@ -1421,7 +1715,7 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     }
     if (lane == 0)
         sh.candidates[wave] = best;
-    __syncthreads();
+    block_sync(sh);
     if (threadIdx.x == 0) {
         ti_candidate result = sh.candidates[0];
         for (int w = 1; w < kWaves; ++w)
@@ -1455,12 +1749,12 @@ __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, S
             b = coherent_load64(words + 1);
             return step == 0 || (static_cast<uint32_t>(a >> 32) == epoch && static_cast<uint32_t>(b >> 32) == epoch);
         };
-        if (!__syncthreads_and(read())) {
+        if (!block_sync_and(sh, read())) {
             const int n = slots - base < kThreads ? slots - base : kThreads;
             wait_witnesses(n, [&](int j) { return candidates + 2 * static_cast<size_t>(base + j) + 1; }, epoch, L.exchange,
                            L.xl, sh);
             uint32_t spins = 0;
-            while (!__syncthreads_and(read()) && !sh.aborted) {
+            while (!block_sync_and(sh, read()) && !sh.aborted) {
                 __builtin_amdgcn_s_sleep(2);
                 if (threadIdx.x == 0)
                     stuck(L.exchange, L.xl, ++spins, sh);
@@ -1475,14 +1769,14 @@ __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, S
     }
     if ((threadIdx.x & 63) == 0)
         sh.candidates[wave_id()] = best;
-    __syncthreads();
+    block_sync(sh);
     if (threadIdx.x == 0) {
         ti_candidate result = sh.candidates[0];
         for (int w = 1; w < kWaves; ++w)
             keep_better(result, sh.candidates[w]);
         sh.token = result.id;
     }
-    __syncthreads();
+    block_sync(sh);
     return sh.token;
 }
 
@@ -1502,8 +1796,225 @@ __device__ void record_choice(const Launch<BF16>& L, int step, ti_token_id token
     }
 }
 
+// Ring slots a task consumes: one per weight row it streams (gate, up and down per FFN row).
+__device__ inline uint32_t ring_slots(const ti_task_record& t)
+{
+    switch (t.opcode) {
+    case TI_OP_QKV:
+    case TI_OP_OUTPUT_PROJECTION:
+    case TI_OP_LOGITS: return t.end - t.begin;
+    case TI_OP_FFN: return 3 * (t.end - t.begin);
+    default: return 0;
+    }
+}
+
+#if TILES_RING
+// ---------------------------------------------------------------- weight ring (streamer side)
+
+// The weight rows a worker's instruction stream consumes, in the order its compute waves
+// consume them (ring_slots), repeated once per step: slot s of the launch belongs to the task
+// whose slots hold it, at its local position (address()).  The walker keeps the current
+// task's row bases, so each lane can compute the address of a different slot.
+template <bool BF16, bool kCached>
+struct RowWalker {
+    const Launch<BF16>& L;
+    const Shared& sh;
+    ti_worker_task_range stream;
+    uint32_t d, kvw;
+    uint64_t row_bytes;
+    uint32_t index = 0;           // the current task's record
+    uint32_t first = 0, count = 0;  // its first slot (of the launch) and its slot count
+    uint32_t begin = 0, ffn_rows = 0, qkv = 0, lim0 = 0, lim1 = 0;
+    uint64_t base0 = 0, base1 = 0, base2 = 0;  // row 0 of each matrix (QKV: of each region's row numbering)
+
+    __device__ RowWalker(const Launch<BF16>& launch, const Shared& shared, ti_worker_task_range range)
+        : L(launch), sh(shared), stream(range)
+    {
+        d = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(L.shape.hidden_size));
+        kvw = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(L.shape.kv_heads * L.shape.head_dim));
+        row_bytes = static_cast<uint64_t>(d) * Num<BF16>::kBytes;
+    }
+    // Records come from LDS when the stream is cached there: a record read from memory is a
+    // load whose use waits for every weight load the wave has in flight.
+    __device__ ti_task_record record(uint32_t i) const
+    {
+        if constexpr (kCached)
+            return sh.stream[i];
+        else
+            return load_record(L.instructions + stream.begin + i);
+    }
+    __device__ uint32_t slots_per_step() const
+    {
+        uint32_t n = 0;
+        for (uint32_t i = 0; i < stream.count; ++i)
+            n += ring_slots(record(i));
+        return n;
+    }
+    // A weight's address, as a value known to be uniform (kept in scalar registers).
+    __device__ uint64_t weight(uint32_t layer, uint32_t region) const
+    {
+        return uniform64(reinterpret_cast<uint64_t>(L.layer_weight(static_cast<int>(layer), region)));
+    }
+    __device__ static uint64_t uniform64(uint64_t v)
+    {
+        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+        return (static_cast<uint64_t>(hi) << 32) | lo;
+    }
+    // Opens the first task with rows at or after record `from` (wrapping to the next step).
+    __device__ void open(uint32_t from)
+    {
+        index = from;
+        ti_task_record t = record(index);
+        while (ring_slots(t) == 0) {
+            index = index + 1 == stream.count ? 0 : index + 1;
+            t = record(index);
+        }
+        count = __builtin_amdgcn_readfirstlane(ring_slots(t));
+        const uint32_t opcode = __builtin_amdgcn_readfirstlane(t.opcode);
+        const uint32_t layer = __builtin_amdgcn_readfirstlane(t.layer);
+        begin = __builtin_amdgcn_readfirstlane(t.begin);
+        ffn_rows = opcode == TI_OP_FFN ? __builtin_amdgcn_readfirstlane(t.end - t.begin) : 0u;
+        qkv = opcode == TI_OP_QKV;
+        lim0 = lim1 = 0xffffffffu;
+        if (opcode == TI_OP_QKV) {
+            base0 = weight(layer, L.layout.Wq);
+            base1 = weight(layer, L.layout.Wk) - d * row_bytes;
+            base2 = weight(layer, L.layout.Wv) - (d + kvw) * row_bytes;
+            lim0 = d;
+            lim1 = d + kvw;
+        } else if (opcode == TI_OP_OUTPUT_PROJECTION) {
+            base0 = weight(layer, L.layout.Wo);
+        } else if (opcode == TI_OP_FFN) {
+            base0 = weight(layer, L.layout.Wgate);
+            base1 = weight(layer, L.layout.Wup);
+            base2 = weight(layer, L.layout.Wdown);
+        } else {
+            base0 = uniform64(reinterpret_cast<uint64_t>(L.stack_weight(L.stack.lm_head_offset)));
+        }
+    }
+    __device__ void advance()
+    {
+        first += count;
+        open(index + 1 == stream.count ? 0 : index + 1);
+    }
+    // Address of slot `slot` of the current task (per lane).  An FFN task of n rows streams
+    // gate and up of each row (slots 2 j, 2 j + 1), then the n down rows (slots 2 n + j).
+    __device__ uint64_t address(uint32_t slot) const
+    {
+        const uint32_t local = slot - first;
+        const bool pair = local < 2 * ffn_rows;
+        const uint32_t row = begin + (ffn_rows == 0 ? local : (pair ? local >> 1 : local - 2 * ffn_rows));
+        const uint32_t m = ffn_rows == 0 ? 0u : (pair ? (local & 1u) : 2u);
+        const uint32_t select = qkv ? (row >= lim0) + (row >= lim1) : m;
+        // Arithmetic on all three bases: a select among the members would become one load
+        // through a selected member address, which keeps the walker in scratch memory.
+        const uint64_t b0 = base0, b1 = base1, b2 = base2;
+        const uint64_t take1 = 0ull - static_cast<uint64_t>(select == 1);
+        const uint64_t take2 = 0ull - static_cast<uint64_t>(select == 2);
+        const uint64_t base = b0 ^ ((b0 ^ b1) & take1) ^ ((b0 ^ b2) & take2);
+        return base + row * row_bytes;
+    }
+};
+
+// Streamer wave q: the weight rows of slots q, q + 4, q + 8, ... of the launch
+// (slots_per_step x steps slots in all) go through a register queue, kStageRows rows deep,
+// into ring[slot % kRingSlots].  A slot is written once every compute wave released it
+// (released[] + kRingSlots > slot); landed[q] then announces it.  Loads of the next rows issue
+// while earlier rows wait for space, so HBM streams during the compute waves' dependency waits
+// until both ring and queue are full.  Whole rows per wave keep the handshake (space check,
+// announcement, addressing) to one per 4 KB.
+template <int VPL, bool kCached>
+__device__ __forceinline__ void stream_weights(const Launch<true>& L, const ti_worker_task_range& stream, Shared& sh)
+{
+    static_assert(VPL * 64 == kRingRowVectors, "streamer waves move whole rows");
+    static_assert(kRingSlots % kStreamWaves == 0, "each streamer wave owns fixed ring slots");
+    const uint32_t q = static_cast<uint32_t>(wave_id() - kWaves);
+    const int lane = threadIdx.x & 63;
+    RowWalker<true, kCached> walker(L, sh, stream);
+    // Every control value of this loop is wave-uniform (scalar): an exit the compiler took for
+    // divergent would mask the loop and collapse the count of loads it keeps in flight.
+    const uint32_t per_step = __builtin_amdgcn_readfirstlane(walker.slots_per_step());
+    const uint32_t total = per_step * static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(L.steps));
+    if (total <= q)
+        return;
+    walker.open(0);
+    constexpr uint32_t kStride = kStreamWaves;
+    constexpr uint32_t kBatch = kStride * kStageRows;  // slots between this wave's batches
+    // Lane k < kStageRows computes the address of slot n + 4 k (past the launch's last slot: the
+    // last row again, never written to the ring).
+    auto fill = [&](uint32_t n) {
+        const uint32_t slot = min(n + kStride * static_cast<uint32_t>(lane), total - 1);
+        uint64_t mine = 0;
+        while (true) {
+            const uint32_t end = walker.first + walker.count;
+            if (slot >= walker.first && slot < end)
+                mine = walker.address(slot);
+            if (!__any(lane < kStageRows && slot >= end))
+                break;
+            walker.advance();
+        }
+        return mine;
+    };
+    const uint32_t lane_bytes = static_cast<uint32_t>(lane) * 16u;
+    auto row_of = [&](uint64_t mine, int k) {
+        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(mine), k);
+        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(mine >> 32), k);
+        return reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | lo) + lane_bytes;
+    };
+    u32x4 staged[kStageRows][VPL];
+    uint64_t addresses = fill(q);
+#pragma unroll
+    for (int k = 0; k < kStageRows; ++k) {
+        const char* row = row_of(addresses, k);
+#pragma unroll
+        for (int v = 0; v < VPL; ++v)
+            staged[k][v] = load_weights(row + v * 1024);
+    }
+    int freed = kRingSlots;  // slots below this may be written
+    uint32_t spins = 0;
+    bool quit = false;
+    for (uint32_t n = q; n < total && !quit; n += kBatch) {
+        addresses = fill(n + kBatch);
+#pragma unroll
+        for (int k = 0; k < kStageRows; ++k) {
+            const uint32_t slot = n + kStride * static_cast<uint32_t>(k);
+            if (slot < total && !quit) {
+                while (static_cast<int>(slot) >= freed) {
+                    freed = lds_min<kWaves>(sh.released) + kRingSlots;
+                    if (static_cast<int>(slot) < freed)
+                        break;
+                    // The compute waves left (or a wait gave up): write nothing more and leave
+                    // after this batch.  A return from here would make the compiler wait for
+                    // every load in flight before each ring write.
+                    const int leave = __builtin_amdgcn_readfirstlane(lds_read(&sh.stop) | sh.aborted);
+                    if (leave || ++spins > kRingSpinLimit) {
+                        quit = true;
+                        freed = 0x7fffffff;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                u32x4* dst = sh.ring + (slot % kRingSlots) * kRingRowVectors + lane;
+#pragma unroll
+                for (int v = 0; v < VPL; ++v)
+                    dst[v * 64] = staged[k][v];
+                // One wave's LDS accesses execute in order: the row is in LDS before the count
+                // that announces it.
+                asm volatile("" ::: "memory");
+                lds_write(&sh.landed[q], static_cast<int>(slot) + 1);
+            }
+            const char* row = row_of(addresses, k);
+#pragma unroll
+            for (int v = 0; v < VPL; ++v)
+                staged[k][v] = load_weights(row + v * 1024);
+        }
+    }
+}
+#endif
+
 template <bool BF16, int VPL, int LRK>
-__global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launch)
+__global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> launch)
 {
     __shared__ Shared sh;
     // The launch record lives in LDS: referenced from many inlined operations, a kernel
@@ -1516,6 +2027,18 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
         sh.xsave_tag = 0;
         sh.rsave_tag = 0;
     }
+#if TILES_RING
+    if (threadIdx.x < kWaves) {
+        sh.arrive[threadIdx.x] = 0;
+        sh.released[threadIdx.x] = 0;
+    }
+    if (threadIdx.x < kStreamWaves)
+        sh.landed[threadIdx.x] = static_cast<int>(threadIdx.x) - (kStreamWaves - 1);
+    if (threadIdx.x < 2)
+        sh.failed[threadIdx.x] = 0;
+    if (threadIdx.x == 0)
+        sh.stop = 0;
+#endif
     __syncthreads();
     const Launch<BF16>& L = record;
     const bool generating = L.selection.generated != nullptr;
@@ -1524,11 +2047,28 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
     const ti_worker_task_range stream = load_record(L.streams + blockIdx.x);
     // The worker's instruction records move to LDS once: read from memory as each task
     // starts, every record would cost a dependent memory round trip between two tasks.
-    const bool cached = stream.count <= static_cast<uint32_t>(kMaxStreamRecords);
+    const bool cached = stream.count <= static_cast<uint32_t>(kLdsStreamRecords);
     if (cached)
-        for (uint32_t i = threadIdx.x; i < stream.count; i += kThreads)
+        for (uint32_t i = threadIdx.x; i < stream.count; i += kBlockThreads)
             sh.stream[i] = load_record(L.instructions + stream.begin + i);
     __syncthreads();
+#if TILES_RING
+    if (wave_id() >= kWaves) {
+        if (cached)
+            stream_weights<VPL, true>(L, stream, sh);
+        else
+            stream_weights<VPL, false>(L, stream, sh);
+        return;
+    }
+#endif
+    // The compute waves leave: streamer waves waiting for ring space stop too.
+    auto leave = [&]() {
+#if TILES_RING
+        if (threadIdx.x == 0)
+            lds_write(&sh.stop, 1);
+#endif
+    };
+    uint32_t ring_slot = 0;  // ring slot of the next streamed weight row
     for (int step = 0; step < L.steps; ++step) {
         // The previous step's K/V cache stores complete before this step publishes anything.
         wait_stores();
@@ -1540,12 +2080,16 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
         } else if (L.device_tokens != nullptr) {
             token = global(L.device_tokens)[step];
         }
-        if (L.stack.full_stack && (token < 0 || token >= L.stack.vocab_size))
+        if (L.stack.full_stack && (token < 0 || token >= L.stack.vocab_size)) {
+            leave();
             return;
+        }
         for (uint32_t index = stream.begin; index < stream.begin + stream.count; ++index) {
             const ti_task_record task = cached ? sh.stream[index - stream.begin] : load_record(L.instructions + index);
             if (task.opcode == TI_OP_BARRIER)
                 continue;  // waves synchronize through the exchange words
+            const uint32_t slot0 = ring_slot;
+            ring_slot += ring_slots(task);
             // Optional timeline: 100 MHz device clock (s_memrealtime) at the start of every
             // instruction of the launch's last step, when its first exchange read returned,
             // when its inputs were complete, and at its end (diagnostic_context.cu:257-285).
@@ -1555,10 +2099,10 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
                 sh.mark_ready = 0;
             }
             switch (task.opcode) {
-            case TI_OP_QKV: op_qkv<BF16, VPL>(L, task, step, token, sh); break;
+            case TI_OP_QKV: op_qkv<BF16, VPL>(L, task, step, token, slot0, sh); break;
             case TI_OP_ATTENTION_SCORES: op_attention<BF16, LRK>(L, task, step, sh); break;
-            case TI_OP_OUTPUT_PROJECTION: op_output_projection<BF16, VPL>(L, task, step, token, sh); break;
-            case TI_OP_FFN: op_ffn<BF16, VPL>(L, task, step, sh); break;
+            case TI_OP_OUTPUT_PROJECTION: op_output_projection<BF16, VPL>(L, task, step, token, slot0, sh); break;
+            case TI_OP_FFN: op_ffn<BF16, VPL>(L, task, step, slot0, sh); break;
             case TI_OP_FFN_REDUCE: op_ffn_reduce<BF16>(L, task, step, sh); break;
             case TI_OP_EMBEDDING: {
                 const int d = L.shape.hidden_size;
@@ -1568,10 +2112,10 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
                 break;
             }
             case TI_OP_FINAL_RMS_NORM: op_final_rms_norm(L, task, step, sh); break;
-            case TI_OP_LOGITS: op_logits<BF16, VPL>(L, task, step, sh); break;
+            case TI_OP_LOGITS: op_logits<BF16, VPL>(L, task, step, slot0, sh); break;
             default: break;  // attention_values: merged inside the scores tasks
             }
-            __syncthreads();
+            block_sync(sh);
             if (L.timeline && threadIdx.x == 0) {
                 global(L.timeline)[4 * static_cast<size_t>(index) + 1] = sh.mark_read;
                 global(L.timeline)[4 * static_cast<size_t>(index) + 2] = sh.mark_ready;
@@ -1581,11 +2125,15 @@ __global__ __launch_bounds__(kThreads, 1) void decoder_worker(Launch<BF16> launc
         if (sh.aborted) {
             if (threadIdx.x == 0 && generating && blockIdx.x == 0)
                 global(L.selection.status)[TI_STATUS_ERROR] = TI_DEVICE_SYNC_TIMEOUT;
+            leave();
             return;
         }
-        if (generating && token == L.selection.eos_id)
+        if (generating && token == L.selection.eos_id) {
+            leave();
             return;
+        }
     }
+    leave();
 }
 
 // ---------------------------------------------------------------- host side of the launch
@@ -1625,7 +2173,7 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     L.workers = p.workers;
     void* args[] = {&L};
     const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decoder_worker<BF16, VPL, LRK>),
-                                                    dim3(p.workers), dim3(kThreads), args, 0, stream);
+                                                    dim3(p.workers), dim3(kBlockThreads), args, 0, stream);
     if (e != hipSuccess)
         return hip_fail(e, "cooperative worker launch");
     return TI_OK;
