@@ -314,6 +314,39 @@ __device__ inline bool stuck(uint64_t* exchange, const ExchangeLayout& xl, uint3
     return false;
 }
 
+// Wave 0 alone: waits until one "witness" word every `stride` words of src[0, count) carries
+// `epoch` (8 loads in flight per lane, a back-off between rounds).
+__device__ inline void wait_witness_words(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
+                                          const ExchangeLayout& xl, Shared& sh)
+{
+    constexpr int kWitnessBatch = 8;
+    const int lane = threadIdx.x & 63;
+    const int witnesses = (count + stride - 1) / stride;
+    uint32_t spins = 0;
+    while (true) {
+        bool mine = true;
+        // Witness j is word j * stride; lanes past the last witness check the last word.
+        for (int j0 = 0; j0 <= witnesses; j0 += 64 * kWitnessBatch) {
+            uint64_t v[kWitnessBatch];
+#pragma unroll
+            for (int u = 0; u < kWitnessBatch; ++u) {
+                const int j = j0 + u * 64 + lane;
+                v[u] = coherent_load64(src + (j < witnesses ? j * stride : count - 1));
+            }
+#pragma unroll
+            for (int u = 0; u < kWitnessBatch; ++u)
+                mine &= static_cast<uint32_t>(v[u] >> 32) == epoch;
+        }
+        if (__all(mine))
+            break;
+        __builtin_amdgcn_s_sleep(2);
+        if (lane == 0)
+            stuck(exchange, xl, ++spins, sh);
+        if (__any(sh.aborted))
+            break;
+    }
+}
+
 // Reads `count` (at most kLdsHidden) exchange words from `src` until each carries `epoch`
 // and hands each payload to `sink(index, payload)`.  Block-wide: every thread must call it.
 // The first read is optimistic (one coherent round trip when the producers are done).  If any
@@ -328,7 +361,6 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
                                           const ExchangeLayout& xl, Shared& sh, Sink sink)
 {
     constexpr int kBatch = (kLdsHidden + kThreads - 1) / kThreads;
-    constexpr int kWitnessBatch = 8;
     uint64_t w[kBatch];
 #pragma unroll
     for (int k = 0; k < kBatch; ++k)
@@ -350,33 +382,8 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
     if (threadIdx.x == 0 && sh.mark_read == 0)
         sh.mark_read = __builtin_amdgcn_s_memrealtime();
     if (!all_present) {
-        if (threadIdx.x < 64) {
-            const int lane = threadIdx.x;
-            const int witnesses = (count + stride - 1) / stride;
-            uint32_t spins = 0;
-            while (true) {
-                bool mine = true;
-                // Witness j is word j * stride; lanes past the last witness check the last word.
-                for (int j0 = 0; j0 <= witnesses; j0 += 64 * kWitnessBatch) {
-                    uint64_t v[kWitnessBatch];
-#pragma unroll
-                    for (int u = 0; u < kWitnessBatch; ++u) {
-                        const int j = j0 + u * 64 + lane;
-                        v[u] = coherent_load64(src + (j < witnesses ? j * stride : count - 1));
-                    }
-#pragma unroll
-                    for (int u = 0; u < kWitnessBatch; ++u)
-                        mine &= static_cast<uint32_t>(v[u] >> 32) == epoch;
-                }
-                if (__all(mine))
-                    break;
-                __builtin_amdgcn_s_sleep(2);
-                if (lane == 0)
-                    stuck(exchange, xl, ++spins, sh);
-                if (__any(sh.aborted))
-                    break;
-            }
-        }
+        if (threadIdx.x < 64)
+            wait_witness_words(src, count, stride, epoch, exchange, xl, sh);
         block_sync(sh);
         uint32_t spins = 0;
         while (!block_sync_and(sh, read()) && !sh.aborted) {
@@ -397,6 +404,18 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
     wait_stores();
     if (threadIdx.x == 0)
         sh.mark_ready = __builtin_amdgcn_s_memrealtime();
+}
+
+// The input poll of a GEMV task, followed by a barrier: the sink's LDS writes are then visible
+// to every wave.  (Polling from wave 0 alone, so that the other waves' prefetched weights stay
+// ahead of no reads, measured slower: one wave needs more coherent round trips, and a round trip
+// costs about 1.5 us under full HBM load.)
+template <typename Sink>
+__device__ __forceinline__ void poll_input(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
+                                          const ExchangeLayout& xl, Shared& sh, Sink sink)
+{
+    poll_words(src, count, stride, epoch, exchange, xl, sh, sink);
+    block_sync(sh);
 }
 
 // One exchange word, waited for by the calling thread alone.
@@ -488,8 +507,9 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, in
             if (i < d)
                 dst[i] = sh.xsave[i] = v[k];
         }
+        block_sync(sh);
     } else {
-        poll_words(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
+        poll_input(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
                    L.exchange, L.xl, sh, [&](int i, uint32_t p) { dst[i] = sh.xsave[i] = Num<BF16>::from_payload(p); });
     }
     if (threadIdx.x == 0)
@@ -606,6 +626,7 @@ struct RowGeometry {
 template <int VPL>
 struct InputSlice {
     uint32_t r[VPL * 4];
+    __device__ InputSlice() {}
     __device__ InputSlice(const void* u, int col, int lr)
     {
 #pragma unroll
@@ -641,18 +662,90 @@ struct InputSlice {
     }
 };
 
-// Dot products of rows [r0, r1) of NM matrices of hidden width with the vector u in LDS
-// (sh.vbits for bf16 storage, sh.vec for fp32: see gemv_input).  emit(row, dots) runs in each
-// row group's last lane with one dot per matrix.
+// The norm scale of a lane's GEMV input slice (its 16-byte vectors col + k lr of a hidden row),
+// loaded before the task waits for its input.
+template <int VPL>
+struct SliceScale {
+    u32x4 v[VPL];
+};
+
+template <bool BF16, int VPL>
+__device__ __forceinline__ SliceScale<VPL> load_slice_scale(const void* scale, int d)
+{
+    const RowGeometry<BF16> g(d);
+    SliceScale<VPL> s;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k)
+        s.v[k] = global(static_cast<const u32x4*>(scale))[g.col + k * g.lr];
+    return s;
+}
+
+// rms_norm_lds's values for one lane's GEMV input slice, computed by every wave on its own: the
+// statistic repeats rms_norm_lds's association exactly (each thread's strided sum, the 64-lane
+// sum of each of the 8 waves, the waves in order), so the slice is bit-identical to what
+// rms_norm_lds leaves in LDS, without its three barriers and its LDS round trip.  v holds the
+// input as FP32 values (every wave's writes visible).
+template <bool BF16, int VPL>
+__device__ __forceinline__ InputSlice<VPL> normalized_slice(const float* v, int d, const SliceScale<VPL>& scale, float eps)
+{
+    using N = Num<BF16>;
+    // Elements per thread of rms_norm_lds's strided sum that this shape can fill (its hidden size
+    // is at most VPL x 64 vectors); the ones past it add +0.0 there.
+    constexpr int KH = VPL * 64 * N::kPerVec / kThreads > 0 ? VPL * 64 * N::kPerVec / kThreads : 1;
+    static_assert(KH <= kLdsHidden / kThreads, "the slice norm reads inside the LDS vector");
+    const int lane = threadIdx.x & 63;
+    float sums[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        float x[KH];
+#pragma unroll
+        for (int k = 0; k < KH; ++k)
+            x[k] = v[k * kThreads + w * 64 + lane];
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KH; ++k)
+            sum += k * kThreads + w * 64 + lane < d ? x[k] * x[k] : 0.0f;
+        sums[w] = group_sum<64>(sum);
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+        total += lane_value(sums[w], 63);
+    const float inv = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
+    const RowGeometry<BF16> g(d);
+    InputSlice<VPL> in;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int first = (g.col + k * g.lr) * N::kPerVec;
+        float n[N::kPerVec];
+#pragma unroll
+        for (int e = 0; e < N::kPerVec; ++e)
+            n[e] = N::round(N::round(v[first + e] * inv) * N::elem(scale.v[k], e));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if constexpr (BF16)
+                in.r[k * 4 + q] = pack_bf16(n[2 * q], n[2 * q + 1]);
+            else
+                in.r[k * 4 + q] = __float_as_uint(n[q]);
+        }
+    }
+    return in;
+}
+
+// Dot products of rows [r0, r1) of NM matrices of hidden width with an input vector: prepare()
+// (block-wide) waits for the task's inputs, make_slice() then gives each lane its slice of the
+// vector (InputSlice).  emit(row, dots) runs in each row group's last lane with one dot per
+// matrix.
 //
 // Exchange worker: row_offset(m, row) is the byte offset from `base` of a row of matrix m
 // (below 2 GiB).  D passes of loads are in flight; all D issue before `prepare`, which runs
 // block-wide, waits for the task's inputs and writes u, so weight latency overlaps the wait.
 // Streaming worker: row r0 + j is ring slot slot0 + j (NM == 1); wave w takes rows j = w,
 // w + 8, ... as in the exchange worker's passes, so both compute the same sums.
-template <bool BF16, int VPL, int NM, int DEPTH = 0, typename RowOffset, typename Prepare, typename Emit>
-__device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int r0, int r1, int cols, const void* u,
-                                    uint32_t slot0, Shared& sh, Prepare prepare, Emit emit)
+template <bool BF16, int VPL, int NM, int DEPTH = 0, typename RowOffset, typename Prepare, typename MakeSlice,
+          typename Emit>
+__device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int r0, int r1, int cols, uint32_t slot0,
+                                    Shared& sh, Prepare prepare, MakeSlice make_slice, Emit emit)
 {
     using N = Num<BF16>;
     constexpr int K = VPL * NM;
@@ -664,7 +757,7 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
     (void)row_offset;
     (void)D;
     prepare();
-    const InputSlice<VPL> in(u, g.col, g.lr);
+    const InputSlice<VPL> in = make_slice();
     const int rows = r1 - r0;
     int have = 0;
     for (int j = g.wave; j < rows; j += kWaves) {
@@ -710,7 +803,7 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
         issue(s, w[s]);
     issue_fence();
     prepare();
-    const InputSlice<VPL> in(u, g.col, g.lr);
+    const InputSlice<VPL> in = make_slice();
     for (int pass0 = 0; active(pass0); pass0 += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
@@ -766,14 +859,11 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
         const uint32_t first = q ? 0u : static_cast<uint32_t>(k ? d : d + kvw);
         return (region + (static_cast<uint32_t>(row) - first) * static_cast<uint32_t>(d)) * N::kBytes;
     };
-    const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.attn_norm), d);
-    auto prepare = [&]() {
-        load_hidden(L, layer, step, token, sh.vec, sh);
-        block_sync(sh);
-        rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
-    };
+    const SliceScale<VPL> scale = load_slice_scale<BF16, VPL>(L.layer_weight(layer, L.layout.attn_norm), d);
+    auto prepare = [&]() { load_hidden(L, layer, step, token, sh.vec, sh); };
+    auto make_slice = [&]() { return normalized_slice<BF16, VPL>(sh.vec, d, scale, L.numeric.rms_norm_eps); };
     float* staged_v = sh.small;  // this task's V rows, for the cache stores after the GEMV
-    gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, 0), row_offset, begin, end, d, gemv_input<BF16>(sh), slot0, sh, prepare,
+    gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, 0), row_offset, begin, end, d, slot0, sh, prepare, make_slice,
                        [&](int row, const float* dots) {
         const float value = N::round(dots[0]);
         publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
@@ -784,8 +874,12 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     if (end <= first_v)
         return;
     block_sync(sh);
+    // Wave 0 stores the V rows (at most 64 per task); every wave's next input poll waits for its
+    // stores before this worker publishes anything else.
     void* cache = L.cache(layer, L.layout.value);
-    for (int row = first_v + static_cast<int>(threadIdx.x); row < end; row += kThreads) {
+    if (wave_id() != 0)
+        return;
+    for (int row = first_v + (static_cast<int>(threadIdx.x) & 63); row < end; row += 64) {
         const size_t index = static_cast<size_t>(position) * kvw + (row - d - kvw);
         if constexpr (BF16)
             coherent_store16(static_cast<uint16_t*>(cache) + index,
@@ -1334,19 +1428,20 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
     auto prepare = [&]() {
         for (int i = begin + static_cast<int>(threadIdx.x); i < end; i += kThreads)
             residual[i - begin] = input_element(L, layer, step, token, i, sh);
-        poll_words(L.exchange + L.xl.attn, d, (L.shape.query_heads / L.shape.kv_heads) * L.shape.head_dim,
+        poll_input(L.exchange + L.xl.attn, d, (L.shape.query_heads / L.shape.kv_heads) * L.shape.head_dim,
                    L.epoch_of(step, layer, kPhaseAttn), L.exchange, L.xl, sh,
                    [&](int i, uint32_t p) {
                        sh.vec[i] = N::from_payload(p);
                        sh.vbits[i] = static_cast<uint16_t>(p);
                    });
-        block_sync(sh);
         if (begin == 0)
             for (int i = threadIdx.x; i < d; i += kThreads)
                 N::store(L.scratch, L.layout.attention + i, sh.vec[i]);
     };
     gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, L.layout.Wo), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
-                       begin, end, d, gemv_input<BF16>(sh), slot0, sh, prepare, [&](int row, const float* dots) {
+                       begin, end, d, slot0, sh, prepare,
+                       [&]() { return InputSlice<VPL>(gemv_input<BF16>(sh), RowGeometry<BF16>(d).col, RowGeometry<BF16>(d).lr); },
+                       [&](int row, const float* dots) {
                            const float r = N::round(N::round(dots[0]) + residual[row - begin]);
                            N::store(L.scratch, L.layout.r + row, r);
                            publish<BF16>(L.exchange + L.xl.r, row, r, epoch);
@@ -1375,7 +1470,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     const int layer = static_cast<int>(t.layer);
     const int r0 = static_cast<int>(t.begin), r1 = static_cast<int>(t.end);
     const RowGeometry<BF16> g(d);
-    const NormScale scale = load_scale<BF16>(L.layer_weight(layer, L.layout.ffn_norm), d);
+    const SliceScale<VPL> scale = load_slice_scale<BF16, VPL>(L.layer_weight(layer, L.layout.ffn_norm), d);
     auto row_of = [&](int pass) { return g.first_row(r0, pass) + g.sub; };
 #if !TILES_RING
     const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
@@ -1403,13 +1498,11 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     issue_fence();
 #endif
 
-    poll_words(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
+    poll_input(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
     if (threadIdx.x == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
-    block_sync(sh);
-    rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
-    const InputSlice<VPL> in(gemv_input<BF16>(sh), g.col, g.lr);
+    const InputSlice<VPL> in = normalized_slice<BF16, VPL>(sh.vec, d, scale, L.numeric.rms_norm_eps);
     float acc[kOut];
 #pragma unroll
     for (int n = 0; n < kOut; ++n)
@@ -1667,22 +1760,23 @@ __device__ inline void keep_better(ti_candidate& best, ti_candidate other)
         best = other;
 }
 
-// Final norm of the last layer's output into sh.vec (decoder_stack.py:126-132).
+// The last layer's output into sh.vec, visible to every wave (the final norm's input,
+// decoder_stack.py:126-132).
 template <bool BF16>
-__device__ __forceinline__ void final_normalized(const Launch<BF16>& L, int step, const NormScale& scale, Shared& sh)
+__device__ __forceinline__ void final_input(const Launch<BF16>& L, int step, Shared& sh)
 {
     const int d = L.shape.hidden_size;
     const int layers = L.stack.layers;
-    poll_words(L.exchange + L.xl.hidden(layers % 2), d, row_stride(d, L.workers), L.epoch_of(step, layers - 1, kPhaseY),
+    poll_input(L.exchange + L.xl.hidden(layers % 2), d, row_stride(d, L.workers), L.epoch_of(step, layers - 1, kPhaseY),
                L.exchange, L.xl, sh, [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
-    block_sync(sh);
-    rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
 }
 
 template <bool BF16>
 __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
-    final_normalized(L, step, load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), L.shape.hidden_size), sh);
+    const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), L.shape.hidden_size);
+    final_input(L, step, sh);
+    rms_norm_lds<BF16>(sh.vec, L.shape.hidden_size, scale, L.numeric.rms_norm_eps, sh);
     void* hidden = (L.stack.layers + 1) % 2 == 0 ? L.input : L.output;
     for (int i = static_cast<int>(t.begin) + threadIdx.x; i < static_cast<int>(t.end); i += kThreads)
         Num<BF16>::store(hidden, i, sh.vec[i]);
@@ -1699,10 +1793,10 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     const int lane = threadIdx.x & 63, wave = wave_id();
     ti_candidate best{-INFINITY, 0x7fffffff};
     const uint32_t row_bytes = static_cast<uint32_t>(d) * Num<BF16>::kBytes;
-    const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
+    const SliceScale<VPL> scale = load_slice_scale<BF16, VPL>(L.stack_weight(L.stack.final_norm_offset), d);
     gemv<BF16, VPL, 1, 4>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
-                       begin, end, d, gemv_input<BF16>(sh), slot0, sh,
-                       [&]() { final_normalized(L, step, scale, sh); },
+                       begin, end, d, slot0, sh, [&]() { final_input(L, step, sh); },
+                       [&]() { return normalized_slice<BF16, VPL>(sh.vec, d, scale, L.numeric.rms_norm_eps); },
                        [&](int row, const float* dots) {
                            const float logit = Num<BF16>::round(dots[0]);
                            global(L.logits)[row] = logit;
