@@ -1533,16 +1533,16 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
                 acc[k * PV + j] += N::elem(wd[k], j) * p;
     };
 #if TILES_RING
-    // Two phases over the ring.  Gate and up of row r0 + j are slots slot0 + 2 j and + 1: wave
-    // w takes rows j = w, w + 8, ... (the exchange worker's passes) and leaves p_j in LDS.  The
-    // down rows follow as slots slot0 + 2 n + j, each read by every wave: wave w owns output
-    // columns 256 w + 4 lane .. + 3 and sums row j into accumulator j mod 8, the wave that
-    // holds row j in the exchange worker.  The eight accumulators are then added in wave order,
-    // the exchange worker's cross-wave sum, so both publish the same bits with no reduction
-    // through LDS.
+    // Passes of 8 rows over the ring: a pass of n rows is 3 n slots from slot0 + 24 p, the gate
+    // and up rows of each row, then the n down rows.  Wave w computes p of the pass's row w into
+    // LDS; after the block meets, every wave reads the pass's down rows at its own output columns
+    // 256 w + 4 lane .. + 3 and adds row j into accumulator j mod 8, the wave that holds row j in
+    // the exchange worker.  The eight accumulators are then added in wave order, the exchange
+    // worker's cross-wave sum, so both publish the same bits with no reduction through LDS.
+    // The streamer fills the next pass's gate and up rows while this one's down rows are summed.
     static_assert(BF16 && VPL * 64 == kRingRowVectors, "ring rows are whole bf16 hidden rows");
     static_assert(kOut == 32 && kWaves == 8, "a lane owns 4 columns of the down rows in 8 classes");
-    static_assert(2 * (kWaves + 1) <= kRingSlots, "a wave's two rows of gate and up fit the ring");
+    static_assert(3 * kWaves <= kRingSlots, "a pass of the chunk fits the ring");
     (void)row_of;
     (void)D;
     (void)NV;
@@ -1550,44 +1550,6 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     (void)acc;
     const int rows = r1 - r0;
     float* pvals = sh.small;  // p of each row of the chunk (rows <= kMaxTaskRows)
-    int have = 0;
-    // Phase 1, two rows per wave at a time (j and j + 8): their reductions overlap.
-    auto product = [&](const u32x4* wg, const u32x4* wu, int j) {
-        const float gate_dot = lane_value(group_sum<64>(in.template dot<BF16>(wg)), 63);
-        const float up_dot = lane_value(group_sum<64>(in.template dot<BF16>(wu)), 63);
-        const float gr = N::round(gate_dot);
-        const float silu = N::round(gr / (1.0f + expf(-gr)));
-        const float p = N::round(silu * N::round(up_dot));
-        if (g.col == 63) {
-            N::store(L.scratch, L.layout.product + r0 + j, p);
-            pvals[j] = p;
-        }
-    };
-    for (int j = g.wave; j < rows; j += 2 * kWaves) {
-        const bool second = j + kWaves < rows;
-        const int last = second ? j + kWaves : j;
-        // Before waiting, release everything below this wave's first slot: a wave waiting for
-        // slots beyond the window must not hold the window back (every wave's two rows span 18
-        // slots, inside the ring).
-        ring_release(sh, slot0 + 2u * static_cast<uint32_t>(j));
-        ring_wait(sh, slot0 + 2u * static_cast<uint32_t>(last) + 1u, have);
-        u32x4 w[4][VPL];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int row = m < 2 ? j : last;  // the second pair repeats the first without a second row
-            const u32x4* ring = ring_row(sh, slot0 + 2u * static_cast<uint32_t>(row) + (m & 1));
-#pragma unroll
-            for (int k = 0; k < VPL; ++k)
-                w[m][k] = ring[k * 64 + g.col];
-        }
-        ring_release(sh, slot0 + 2u * static_cast<uint32_t>(min(j + 2 * kWaves, rows)));
-        product(w[0], w[1], j);
-        if (second)
-            product(w[2], w[3], j + kWaves);
-    }
-    ring_release(sh, slot0 + 2u * static_cast<uint32_t>(rows));
-    block_sync(sh);
-    // Phase 2, eight down rows per wait: every read issues before any is used.
     typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
     float part[kWaves][4];
 #pragma unroll
@@ -1595,20 +1557,49 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             part[c][e] = 0.0f;
-    const uint32_t down0 = slot0 + 2u * static_cast<uint32_t>(rows);
     const int column = g.wave * 256 + 4 * lane;
+    int have = 0;
     for (int j0 = 0; j0 < rows; j0 += kWaves) {
         const int count = min(kWaves, rows - j0);
-        ring_wait(sh, down0 + static_cast<uint32_t>(j0 + count - 1), have);
+        const uint32_t pass0 = slot0 + 3u * static_cast<uint32_t>(j0);  // this pass: 2 count gate/up slots, count down slots
+        const uint32_t down0 = pass0 + 2u * static_cast<uint32_t>(count);
+        if (g.wave < count) {
+            const int j = j0 + g.wave;
+            const uint32_t slot = pass0 + 2u * static_cast<uint32_t>(g.wave);
+            ring_release(sh, slot);  // nothing of this chunk below its gate row (progress: see ring_release)
+            ring_wait(sh, slot + 1, have);
+            const u32x4* ring_gate = ring_row(sh, slot);
+            const u32x4* ring_up = ring_row(sh, slot + 1);
+            u32x4 wg[VPL], wu[VPL];
+#pragma unroll
+            for (int k = 0; k < VPL; ++k) {
+                wg[k] = ring_gate[k * 64 + g.col];
+                wu[k] = ring_up[k * 64 + g.col];
+            }
+            ring_release(sh, down0);
+            const float gate_dot = lane_value(group_sum<64>(in.template dot<BF16>(wg)), 63);
+            const float up_dot = lane_value(group_sum<64>(in.template dot<BF16>(wu)), 63);
+            const float gr = N::round(gate_dot);
+            const float silu = N::round(gr / (1.0f + expf(-gr)));
+            const float p = N::round(silu * N::round(up_dot));
+            if (g.col == 63) {
+                N::store(L.scratch, L.layout.product + r0 + j, p);
+                pvals[j] = p;
+            }
+        } else {
+            ring_release(sh, down0);
+        }
+        block_sync(sh);  // the pass's products are in LDS
+        ring_wait(sh, down0 + static_cast<uint32_t>(count - 1), have);
         u32x2 wd[kWaves];
         float pj[kWaves];
 #pragma unroll
         for (int c = 0; c < kWaves; ++c) {
-            const int j = j0 + (c < count ? c : 0);  // past the chunk: re-read a row, weight 0
-            wd[c] = reinterpret_cast<const u32x2*>(ring_row(sh, down0 + static_cast<uint32_t>(j)))[column / 4];
-            pj[c] = pvals[j];
+            const int cc = c < count ? c : 0;  // past the chunk: re-read a row, weight 0
+            wd[c] = reinterpret_cast<const u32x2*>(ring_row(sh, down0 + static_cast<uint32_t>(cc)))[column / 4];
+            pj[c] = pvals[j0 + cc];
         }
-        ring_release(sh, down0 + static_cast<uint32_t>(j0 + count));
+        ring_release(sh, down0 + static_cast<uint32_t>(count));
 #pragma unroll
         for (int c = 0; c < kWaves; ++c) {
             if (c < count) {
@@ -1992,14 +1983,20 @@ struct RowWalker {
         first += count;
         open(index + 1 == stream.count ? 0 : index + 1);
     }
-    // Address of slot `slot` of the current task (per lane).  An FFN task of n rows streams
-    // gate and up of each row (slots 2 j, 2 j + 1), then the n down rows (slots 2 n + j).
+    // Address of slot `slot` of the current task (per lane).  An FFN task streams its rows in
+    // passes of 8 (ffn_pass_slots): gate and up of each row of the pass, then the pass's down
+    // rows.
     __device__ uint64_t address(uint32_t slot) const
     {
         const uint32_t local = slot - first;
-        const bool pair = local < 2 * ffn_rows;
-        const uint32_t row = begin + (ffn_rows == 0 ? local : (pair ? local >> 1 : local - 2 * ffn_rows));
-        const uint32_t m = ffn_rows == 0 ? 0u : (pair ? (local & 1u) : 2u);
+        uint32_t row = begin + local, m = 0;
+        if (ffn_rows != 0) {
+            const uint32_t pass = local / 24u, within = local - 24u * pass;
+            const uint32_t in_pass = min(8u, ffn_rows - 8u * pass);
+            const bool pair = within < 2u * in_pass;
+            row = begin + 8u * pass + (pair ? within >> 1 : within - 2u * in_pass);
+            m = pair ? (within & 1u) : 2u;
+        }
         const uint32_t select = qkv ? (row >= lim0) + (row >= lim1) : m;
         // Arithmetic on all three bases: a select among the members would become one load
         // through a selected member address, which keeps the walker in scratch memory.
