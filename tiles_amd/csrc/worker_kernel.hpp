@@ -732,6 +732,32 @@ __device__ __forceinline__ InputSlice<VPL> normalized_slice(const float* v, int 
     return in;
 }
 
+// The normalized GEMV input of a lane.  Exchange worker: rms_norm_lds (three s_barriers, cheap)
+// and the slice from LDS.  Streaming worker: every wave repeats the statistic
+// (normalized_slice), because its LDS barriers cost about five s_barriers; the eight-fold
+// statistic costs more vector instructions than the exchange worker's barriers save.  Both give
+// the same bits.
+template <bool BF16, int VPL>
+struct NormInput {
+#if TILES_RING
+    SliceScale<VPL> scale;
+    __device__ NormInput(const void* weights, int d) : scale(load_slice_scale<BF16, VPL>(weights, d)) {}
+    __device__ InputSlice<VPL> operator()(Shared& sh, int d, float eps) const
+    {
+        return normalized_slice<BF16, VPL>(sh.vec, d, scale, eps);
+    }
+#else
+    NormScale scale;
+    __device__ NormInput(const void* weights, int d) : scale(load_scale<BF16>(weights, d)) {}
+    __device__ InputSlice<VPL> operator()(Shared& sh, int d, float eps) const
+    {
+        rms_norm_lds<BF16>(sh.vec, d, scale, eps, sh);
+        const RowGeometry<BF16> g(d);
+        return InputSlice<VPL>(gemv_input<BF16>(sh), g.col, g.lr);
+    }
+#endif
+};
+
 // Dot products of rows [r0, r1) of NM matrices of hidden width with an input vector: prepare()
 // (block-wide) waits for the task's inputs, make_slice() then gives each lane its slice of the
 // vector (InputSlice).  emit(row, dots) runs in each row group's last lane with one dot per
@@ -859,9 +885,9 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
         const uint32_t first = q ? 0u : static_cast<uint32_t>(k ? d : d + kvw);
         return (region + (static_cast<uint32_t>(row) - first) * static_cast<uint32_t>(d)) * N::kBytes;
     };
-    const SliceScale<VPL> scale = load_slice_scale<BF16, VPL>(L.layer_weight(layer, L.layout.attn_norm), d);
+    const NormInput<BF16, VPL> norm(L.layer_weight(layer, L.layout.attn_norm), d);
     auto prepare = [&]() { load_hidden(L, layer, step, token, sh.vec, sh); };
-    auto make_slice = [&]() { return normalized_slice<BF16, VPL>(sh.vec, d, scale, L.numeric.rms_norm_eps); };
+    auto make_slice = [&]() { return norm(sh, d, L.numeric.rms_norm_eps); };
     float* staged_v = sh.small;  // this task's V rows, for the cache stores after the GEMV
     gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, 0), row_offset, begin, end, d, slot0, sh, prepare, make_slice,
                        [&](int row, const float* dots) {
@@ -1470,7 +1496,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     const int layer = static_cast<int>(t.layer);
     const int r0 = static_cast<int>(t.begin), r1 = static_cast<int>(t.end);
     const RowGeometry<BF16> g(d);
-    const SliceScale<VPL> scale = load_slice_scale<BF16, VPL>(L.layer_weight(layer, L.layout.ffn_norm), d);
+    const NormInput<BF16, VPL> norm(L.layer_weight(layer, L.layout.ffn_norm), d);
     auto row_of = [&](int pass) { return g.first_row(r0, pass) + g.sub; };
 #if !TILES_RING
     const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
@@ -1502,7 +1528,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
                [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
     if (threadIdx.x == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
-    const InputSlice<VPL> in = normalized_slice<BF16, VPL>(sh.vec, d, scale, L.numeric.rms_norm_eps);
+    const InputSlice<VPL> in = norm(sh, d, L.numeric.rms_norm_eps);
     float acc[kOut];
 #pragma unroll
     for (int n = 0; n < kOut; ++n)
@@ -1784,10 +1810,10 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     const int lane = threadIdx.x & 63, wave = wave_id();
     ti_candidate best{-INFINITY, 0x7fffffff};
     const uint32_t row_bytes = static_cast<uint32_t>(d) * Num<BF16>::kBytes;
-    const SliceScale<VPL> scale = load_slice_scale<BF16, VPL>(L.stack_weight(L.stack.final_norm_offset), d);
+    const NormInput<BF16, VPL> norm(L.stack_weight(L.stack.final_norm_offset), d);
     gemv<BF16, VPL, 1, 4>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
                        begin, end, d, slot0, sh, [&]() { final_input(L, step, sh); },
-                       [&]() { return normalized_slice<BF16, VPL>(sh.vec, d, scale, L.numeric.rms_norm_eps); },
+                       [&]() { return norm(sh, d, L.numeric.rms_norm_eps); },
                        [&](int row, const float* dots) {
                            const float logit = Num<BF16>::round(dots[0]);
                            global(L.logits)[row] = logit;
