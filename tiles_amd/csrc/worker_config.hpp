@@ -42,6 +42,7 @@ inline constexpr int kPhaseAttn = 1;
 inline constexpr int kPhaseR = 2;
 inline constexpr int kPhaseFfn = 3;
 inline constexpr int kPhaseY = 4;
+inline constexpr int kPhaseAttnPart = 5;  // attention chunk partials of a split context
 inline constexpr int kPhaseCandidate = 0;
 inline constexpr int kPhases = 8;
 
@@ -57,12 +58,20 @@ struct ExchangeLayout {
     size_t r;            // attention block output
     size_t ffn;          // FP32 down partials, [ffn_chunks][hidden]
     size_t candidates;   // greedy candidates, 2 words per slot
-    size_t counters;     // per (layer, kv_head): attention chunks finished
+    size_t parts;        // split attention, per K/V head and chunk: the group's FP32 partial P V, then (max, sum) per head
     size_t total;
     // A conditional, not an indexed array: a dynamic index into the launch record would put
     // the whole record in scratch memory.
     __host__ __device__ size_t hidden(int index) const { return index % 2 == 0 ? hidden0 : hidden1; }
 };
+
+// Words of one split-attention chunk's partial for one K/V head: group x head_dim outputs, then
+// (max, sum) for each of the group's query heads.
+__host__ __device__ inline size_t attention_part_words(const ti_model_shape& s)
+{
+    const size_t group = s.kv_heads > 0 ? static_cast<size_t>(s.query_heads / s.kv_heads) : 0;
+    return group * (static_cast<size_t>(s.head_dim) + 2);
+}
 
 __host__ __device__ inline ExchangeLayout exchange_layout(const ti_model_shape& s, int layers, int slots)
 {
@@ -77,8 +86,9 @@ __host__ __device__ inline ExchangeLayout exchange_layout(const ti_model_shape& 
     x.r = x.attn + d;
     x.ffn = x.r + d;
     x.candidates = x.ffn + static_cast<size_t>(s.ffn_chunks) * d;
-    x.counters = x.candidates + 2 * static_cast<size_t>(slots > 0 ? slots : 1);
-    x.total = x.counters + static_cast<size_t>(layers) * s.kv_heads;
+    x.parts = x.candidates + 2 * static_cast<size_t>(slots > 0 ? slots : 1);
+    x.total = x.parts + static_cast<size_t>(s.kv_heads) * s.attention_chunks * attention_part_words(s);
+    (void)layers;
     return x;
 }
 

@@ -1340,60 +1340,78 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             publish<BF16>(attn, mine, N::round(out), out_epoch);
         return;
     }
-    // Partial of this chunk: [chunk][head][dh] then statistics [chunk][head][2].
-    float* partials = L.partials;
-    float* stats_base = L.partials + static_cast<size_t>(s.attention_chunks) * s.query_heads * dh;
-    float* partial = partials + (static_cast<size_t>(chunk) * s.query_heads + first_head) * dh;
-    float* stats = stats_base + (static_cast<size_t>(chunk) * s.query_heads + first_head) * 2;
-    if (owner)
-        coherent_storef(partial + mine, out);
-    if (threadIdx.x < group) {
-        coherent_storef(stats + threadIdx.x * 2, stat_max[threadIdx.x]);
-        coherent_storef(stats + threadIdx.x * 2 + 1, stat_sum[threadIdx.x]);
-    }
-    wait_stores();
-    block_sync(sh);
-    uint64_t* counter = L.exchange + L.xl.counters + layer * s.kv_heads + kv_head;
-    if (threadIdx.x == 0) {
-        const uint64_t before = coherent_fetch_add64(counter, 1ull);
-        sh.flag = before == static_cast<uint64_t>(chunks - 1);
-    }
-    block_sync(sh);
-    if (!sh.flag)
-        return;
-    // The last chunk of this head group merges every chunk: out = sum_c w_c P_c / S with
-    // w_c = exp(max_c - M), M = max_c max_c and S = sum_c w_c sum_c.  Every load of the merge
-    // goes out before any is used: the chunk partials first (threads split an output's chunks
-    // `slices` ways, kBatch chunks each), then wave g's lanes load head g's chunk statistics
-    // (one chunk per lane) into LDS.
+    // Split context.  Every chunk but 0 publishes its partial (unnormalized FP32 P V of each
+    // head, then each head's max and sum of exp) as exchange words and is done: the words carry
+    // the epoch, so no store acknowledgement and no arrival counter stand between a chunk and
+    // the merge.  Chunk 0 merges: out = sum_c w_c P_c / S with w_c = exp(max_c - M),
+    // M = max_c max_c and S = sum_c w_c sum_c, its own chunk from registers and LDS.
     const int outputs = group * dh;
+    const int part_words = static_cast<int>(attention_part_words(s));
+    const uint32_t part_epoch = L.epoch_of(step, layer, kPhaseAttnPart);
+    uint64_t* blocks = L.exchange + L.xl.parts + static_cast<size_t>(kv_head) * s.attention_chunks * part_words;
+    if (chunk != 0) {
+        uint64_t* mine_block = blocks + static_cast<size_t>(chunk) * part_words;
+        const uint64_t tag = static_cast<uint64_t>(part_epoch) << 32;
+        if (owner)
+            coherent_store64(mine_block + mine, tag | __float_as_uint(out));
+        if (threadIdx.x < group) {
+            coherent_store64(mine_block + outputs + 2 * threadIdx.x, tag | __float_as_uint(stat_max[threadIdx.x]));
+            coherent_store64(mine_block + outputs + 2 * threadIdx.x + 1, tag | __float_as_uint(stat_sum[threadIdx.x]));
+        }
+        return;
+    }
+    // Threads split an output's chunks `slices` ways, kBatch chunks at a time; wave g's lanes
+    // read head g's statistics (one chunk per lane) into LDS.  Every read of a round issues
+    // before any is looked at; a round with a word missing is read again (chunk 0's words come
+    // from this worker and are always present).
     const int slices = kThreads / outputs;
     const int o = static_cast<int>(threadIdx.x) % outputs, slice = static_cast<int>(threadIdx.x) / outputs;
-    const float* column = partials + static_cast<size_t>(first_head) * dh + o;
-    const size_t chunk_stride = static_cast<size_t>(s.query_heads) * dh;
     constexpr int kBatch = 32;
     float part[kBatch];
-    // Unconditional loads (past the last chunk they re-read it): a load whose use is a select
-    // would wait for it before the next one issues.
-    auto load_part = [&](int c0) {
+    float* weight = sh.region;                      // [chunks][group]
+    float* chunk_sum = sh.region + chunks * group;  // [chunks][group]
+    auto read_round = [&](int c0, bool with_stats) {
+        uint64_t w[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int c = min(c0 + slice + k * slices, chunks - 1);
-            part[k] = coherent_loadf(column + static_cast<size_t>(c) * chunk_stride);
+            w[k] = coherent_load64(blocks + static_cast<size_t>(c) * part_words + o);
+        }
+        bool ok = true;
+        if (with_stats && wave < group) {
+            for (int c = lane; c < chunks; c += 64) {
+                const uint64_t* st = blocks + static_cast<size_t>(c) * part_words + outputs + 2 * wave;
+                const uint64_t cm = c > 0 ? coherent_load64(st) : 0, cs = c > 0 ? coherent_load64(st + 1) : 0;
+                ok &= c == 0 || (static_cast<uint32_t>(cm >> 32) == part_epoch && static_cast<uint32_t>(cs >> 32) == part_epoch);
+                weight[c * group + wave] = c > 0 ? __uint_as_float(static_cast<uint32_t>(cm)) : stat_max[wave];
+                chunk_sum[c * group + wave] = c > 0 ? __uint_as_float(static_cast<uint32_t>(cs)) : stat_sum[wave];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int c = min(c0 + slice + k * slices, chunks - 1);
+            if (c == 0) {
+                part[k] = out;  // slice 0, thread o: the owner of output o
+            } else {
+                ok &= static_cast<uint32_t>(w[k] >> 32) == part_epoch;
+                part[k] = __uint_as_float(static_cast<uint32_t>(w[k]));
+            }
+        }
+        return ok;
+    };
+    auto read_until_present = [&](int c0, bool with_stats) {
+        uint32_t spins = 0;
+        while (!block_sync_and(sh, read_round(c0, with_stats)) && !sh.aborted) {
+            __builtin_amdgcn_s_sleep(2);
+            if (threadIdx.x == 0)
+                stuck(L.exchange, L.xl, ++spins, sh);
         }
     };
-    load_part(0);
-    float* weight = sh.region;                      // [chunks][group]
-    float* chunk_sum = sh.region + chunks * group;  // [chunks][group]
+    read_until_present(0, true);
     if (wave < group) {
         float m = -INFINITY;
-        for (int c = lane; c < chunks; c += 64) {
-            const float* st = stats_base + (static_cast<size_t>(c) * s.query_heads + first_head + wave) * 2;
-            const float cm = coherent_loadf(st), cs = coherent_loadf(st + 1);
-            weight[c * group + wave] = cm;
-            chunk_sum[c * group + wave] = cs;
-            m = fmaxf(m, cm);
-        }
+        for (int c = lane; c < chunks; c += 64)
+            m = fmaxf(m, weight[c * group + wave]);
         m = lane_value(group_max(m, 64), 63);
         float total = 0.0f;
         for (int c = lane; c < chunks; c += 64) {
@@ -1418,7 +1436,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         c0 += kBatch * slices;
         if (c0 >= chunks)
             break;
-        load_part(c0);
+        read_until_present(c0, false);
     }
     static_assert(kThreads <= (kMaxGroup + 1) * kMaxHeadDim, "merge sums exceed their LDS area");
     float* sums = sh.rotated;  // [slices][outputs] (slices * outputs <= kThreads)
@@ -1431,10 +1449,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             total += sums[j * outputs + mine];
         out = total / sh.small[2 * kMaxGroup + mine / dh];
     }
-    if (threadIdx.x == 0)
-        coherent_store64(counter, 0);
-    wait_stores();
-    block_sync(sh);
+    wait_stores();  // the K row (chunk 0 stores it) is in the cache before anyone sees this output
     if (owner)
         publish<BF16>(attn, mine, N::round(out), out_epoch);
 }
