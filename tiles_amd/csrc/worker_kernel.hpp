@@ -62,6 +62,18 @@ constexpr int kLdsRegionFloats = kRegionFloats;
 constexpr int kLdsStreamRecords = kMaxStreamRecords;
 #endif
 
+// The thread's index in the block, re-read at each use through an empty asm statement that the
+// compiler may neither move nor merge.  Address arithmetic on threadIdx.x is otherwise hoisted
+// out of the task loop to the kernel's start: those values then live across every task, exceed
+// the 256 VGPRs of a wave at 8 waves per CU, and are spilled to scratch and reloaded from
+// memory (behind the weight stream) inside the tasks.
+__device__ inline unsigned tid()
+{
+    unsigned t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // This thread's wave, as a value the compiler knows to be uniform across the wave (a scalar),
 // so that branches on it stay scalar branches.
 __device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6); }
@@ -320,7 +332,7 @@ __device__ inline void wait_witness_words(const uint64_t* src, int count, int st
                                           const ExchangeLayout& xl, Shared& sh)
 {
     constexpr int kWitnessBatch = 8;
-    const int lane = threadIdx.x & 63;
+    const int lane = tid() & 63;
     const int witnesses = (count + stride - 1) / stride;
     uint32_t spins = 0;
     while (true) {
@@ -368,7 +380,7 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
     auto read = [&]() {
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-            const int index = k * kThreads + static_cast<int>(threadIdx.x);
+            const int index = k * kThreads + static_cast<int>(tid());
             if (k * kThreads < count)  // block-uniform; lanes past count re-read the last word
                 w[k] = coherent_load64(src + (index < count ? index : count - 1));
         }
@@ -379,22 +391,22 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
         return ok;
     };
     const bool all_present = block_sync_and(sh, read());
-    if (threadIdx.x == 0 && sh.mark_read == 0)
+    if (tid() == 0 && sh.mark_read == 0)
         sh.mark_read = __builtin_amdgcn_s_memrealtime();
     if (!all_present) {
-        if (threadIdx.x < 64)
+        if (tid() < 64)
             wait_witness_words(src, count, stride, epoch, exchange, xl, sh);
         block_sync(sh);
         uint32_t spins = 0;
         while (!block_sync_and(sh, read()) && !sh.aborted) {
             __builtin_amdgcn_s_sleep(2);
-            if (threadIdx.x == 0)
+            if (tid() == 0)
                 stuck(exchange, xl, ++spins, sh);
         }
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
-        const int index = k * kThreads + static_cast<int>(threadIdx.x);
+        const int index = k * kThreads + static_cast<int>(tid());
         if (index < count)
             sink(index, static_cast<uint32_t>(w[k]));
     }
@@ -402,7 +414,7 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
     // before anything it publishes from here on, which is what every later reader of those rows
     // follows.  The loads above already returned, so this waits only for stores.
     wait_stores();
-    if (threadIdx.x == 0)
+    if (tid() == 0)
         sh.mark_ready = __builtin_amdgcn_s_memrealtime();
 }
 
@@ -442,8 +454,8 @@ __device__ __forceinline__ void wait_witnesses(int n, Witness witness, uint32_t 
                                               const ExchangeLayout& xl, Shared& sh)
 {
     constexpr int kBatch = 8;
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
+    if (tid() < 64) {
+        const int lane = tid();
         uint32_t spins = 0;
         while (true) {
             bool mine = true;
@@ -498,12 +510,12 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, in
         float v[kLdsHidden / kThreads];
 #pragma unroll
         for (int k = 0; k < kLdsHidden / kThreads; ++k) {  // all loads in flight together
-            const int i = k * kThreads + static_cast<int>(threadIdx.x);
+            const int i = k * kThreads + static_cast<int>(tid());
             v[k] = Num<BF16>::load(row, i < d ? i : 0);
         }
 #pragma unroll
         for (int k = 0; k < kLdsHidden / kThreads; ++k) {
-            const int i = k * kThreads + static_cast<int>(threadIdx.x);
+            const int i = k * kThreads + static_cast<int>(tid());
             if (i < d)
                 dst[i] = sh.xsave[i] = v[k];
         }
@@ -512,7 +524,7 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, in
         poll_input(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
                    L.exchange, L.xl, sh, [&](int i, uint32_t p) { dst[i] = sh.xsave[i] = Num<BF16>::from_payload(p); });
     }
-    if (threadIdx.x == 0)
+    if (tid() == 0)
         sh.xsave_tag = L.epoch_of(step, layer, kPhaseQKV);
 }
 
@@ -544,7 +556,7 @@ __device__ __forceinline__ float attention_output_element(const Launch<BF16>& L,
 
 // ---------------------------------------------------------------- RMSNorm (ops.cuh:145-219)
 
-// A norm's scale elements threadIdx.x + k * kThreads, loaded into registers before the task
+// A norm's scale elements tid() + k * kThreads, loaded into registers before the task
 // waits for its input (a load issued after the wait would add a full memory latency).
 struct NormScale {
     float v[kLdsHidden / kThreads];
@@ -558,7 +570,7 @@ __device__ __forceinline__ NormScale load_scale(const void* scale, int d)
     NormScale s;
 #pragma unroll
     for (int k = 0; k < kLdsHidden / kThreads; ++k) {
-        const int i = k * kThreads + static_cast<int>(threadIdx.x);
+        const int i = k * kThreads + static_cast<int>(tid());
         s.v[k] = Num<BF16>::load(scale, i < d ? i : d - 1);
     }
     return s;
@@ -573,13 +585,13 @@ __device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& s
     float x[kLdsHidden / kThreads];  // all reads first (v holds kLdsHidden floats)
 #pragma unroll
     for (int k = 0; k < kLdsHidden / kThreads; ++k)
-        x[k] = v[k * kThreads + threadIdx.x];
+        x[k] = v[k * kThreads + tid()];
     float sum = 0.0f;
 #pragma unroll
     for (int k = 0; k < kLdsHidden / kThreads; ++k)
-        sum += k * kThreads + static_cast<int>(threadIdx.x) < d ? x[k] * x[k] : 0.0f;
+        sum += k * kThreads + static_cast<int>(tid()) < d ? x[k] * x[k] : 0.0f;
     sum = group_sum<64>(sum);
-    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int lane = tid() & 63, wave = wave_id();
     block_sync(sh);
     if (lane == 63)
         sh.small[wave] = sum;
@@ -590,7 +602,7 @@ __device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& s
     const float inv = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
 #pragma unroll
     for (int k = 0; k < kLdsHidden / kThreads; ++k) {
-        const int i = k * kThreads + static_cast<int>(threadIdx.x);
+        const int i = k * kThreads + static_cast<int>(tid());
         if (i < d) {
             v[i] = Num<BF16>::round(Num<BF16>::round(v[i] * inv) * scale.v[k]);
             if constexpr (BF16)
@@ -613,7 +625,7 @@ struct RowGeometry {
         lr = nvec < 64 ? nvec : 64;
         rows_per_wave = 64 / lr;
         pass_rows = kWaves * rows_per_wave;
-        const int lane = threadIdx.x & 63;
+        const int lane = tid() & 63;
         wave = wave_id();
         sub = lane / lr;
         col = lane % lr;
@@ -693,7 +705,7 @@ __device__ __forceinline__ InputSlice<VPL> normalized_slice(const float* v, int 
     // is at most VPL x 64 vectors); the ones past it add +0.0 there.
     constexpr int KH = VPL * 64 * N::kPerVec / kThreads > 0 ? VPL * 64 * N::kPerVec / kThreads : 1;
     static_assert(KH <= kLdsHidden / kThreads, "the slice norm reads inside the LDS vector");
-    const int lane = threadIdx.x & 63;
+    const int lane = tid() & 63;
     float sums[kWaves];
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
@@ -905,7 +917,7 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     void* cache = L.cache(layer, L.layout.value);
     if (wave_id() != 0)
         return;
-    for (int row = first_v + (static_cast<int>(threadIdx.x) & 63); row < end; row += 64) {
+    for (int row = first_v + (static_cast<int>(tid()) & 63); row < end; row += 64) {
         const size_t index = static_cast<size_t>(position) * kvw + (row - d - kvw);
         if constexpr (BF16)
             coherent_store16(static_cast<uint16_t*>(cache) + index,
@@ -976,7 +988,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const int end = static_cast<int>(static_cast<int64_t>(length) * (chunk + 1) / chunks);
     const int span = end - begin;
 
-    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int lane = tid() & 63, wave = wave_id();
     const int sub = lane / LRK, col = lane % LRK;    // vector path: row and 16-byte slice
     const int tr = lane % kTile, tk = lane / kTile;  // matrix path: tile row and 8-element slice
     void* key_cache = L.cache(layer, L.layout.key);
@@ -1025,7 +1037,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 
     // cos/sin of the position's RoPE angles, rounded (ops.cuh:125-140).
     constexpr int half = dh / 2;
-    for (int pair = threadIdx.x; pair < half; pair += kThreads) {
+    for (int pair = tid(); pair < half; pair += kThreads) {
         const float angle = static_cast<float>(position) * global(L.rope)[pair];
         sh.rope_cs[pair] = N::round(cosf(angle));
         sh.rope_cs[half + pair] = N::round(sinf(angle));
@@ -1038,18 +1050,18 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                row_stride(s.hidden_size + 2 * kvw, L.workers), L.epoch_of(step, layer, kPhaseQKV), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { incoming[i] = N::from_payload(p); });
     block_sync(sh);
-    for (int index = threadIdx.x; index < (group + 1) * half; index += kThreads) {
+    for (int index = tid(); index < (group + 1) * half; index += kThreads) {
         const int head = index / half, pair = index - head * half;
         const float c = sh.rope_cs[pair], sn = sh.rope_cs[half + pair];
         const float a = incoming[head * dh + pair], b = incoming[head * dh + pair + half];
         sh.rotated[head * dh + pair] = N::round(N::round(a * c) - N::round(b * sn));
         sh.rotated[head * dh + pair + half] = N::round(N::round(b * c) + N::round(a * sn));
     }
-    for (int index = threadIdx.x; index < dh; index += kThreads)
+    for (int index = tid(); index < dh; index += kThreads)
         sh.vcur[index] = incoming[(group + 1) * dh + index];
     block_sync(sh);  // incoming is dead: the scores may overwrite the region
     if (chunk == 0) {
-        for (int index = threadIdx.x; index < (group + 1) * dh; index += kThreads) {
+        for (int index = tid(); index < (group + 1) * dh; index += kThreads) {
             const float value = sh.rotated[index];
             if (index < group * dh) {
                 N::store(L.scratch, L.layout.q_rot + first_head * dh + index, value);
@@ -1218,7 +1230,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     block_sync(sh);
 
     // group * dh <= kThreads: each thread owns at most one output element.
-    const int mine = threadIdx.x;
+    const int mine = tid();
     const bool owner = mine < group * dh;
     float out = 0.0f;
     if constexpr (kMfma) {
@@ -1354,9 +1366,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         const uint64_t tag = static_cast<uint64_t>(part_epoch) << 32;
         if (owner)
             coherent_store64(mine_block + mine, tag | __float_as_uint(out));
-        if (threadIdx.x < group) {
-            coherent_store64(mine_block + outputs + 2 * threadIdx.x, tag | __float_as_uint(stat_max[threadIdx.x]));
-            coherent_store64(mine_block + outputs + 2 * threadIdx.x + 1, tag | __float_as_uint(stat_sum[threadIdx.x]));
+        if (tid() < group) {
+            coherent_store64(mine_block + outputs + 2 * tid(), tag | __float_as_uint(stat_max[tid()]));
+            coherent_store64(mine_block + outputs + 2 * tid() + 1, tag | __float_as_uint(stat_sum[tid()]));
         }
         return;
     }
@@ -1365,17 +1377,19 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     // before any is looked at; a round with a word missing is read again (chunk 0's words come
     // from this worker and are always present).
     const int slices = kThreads / outputs;
-    const int o = static_cast<int>(threadIdx.x) % outputs, slice = static_cast<int>(threadIdx.x) / outputs;
-    constexpr int kBatch = 32;
+    const int o = static_cast<int>(tid()) % outputs, slice = static_cast<int>(tid()) / outputs;
+    constexpr int kBatch = 8;
     float part[kBatch];
     float* weight = sh.region;                      // [chunks][group]
     float* chunk_sum = sh.region + chunks * group;  // [chunks][group]
     auto read_round = [&](int c0, bool with_stats) {
+        // Only the words of chunks 1 .. chunks - 1 are read: a slot past the last chunk, or of
+        // chunk 0, issues no load.
         uint64_t w[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-            const int c = min(c0 + slice + k * slices, chunks - 1);
-            w[k] = coherent_load64(blocks + static_cast<size_t>(c) * part_words + o);
+            const int c = c0 + slice + k * slices;
+            w[k] = c > 0 && c < chunks ? coherent_load64(blocks + static_cast<size_t>(c) * part_words + o) : 0;
         }
         bool ok = true;
         if (with_stats && wave < group) {
@@ -1389,10 +1403,10 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-            const int c = min(c0 + slice + k * slices, chunks - 1);
+            const int c = c0 + slice + k * slices;
             if (c == 0) {
                 part[k] = out;  // slice 0, thread o: the owner of output o
-            } else {
+            } else if (c < chunks) {
                 ok &= static_cast<uint32_t>(w[k] >> 32) == part_epoch;
                 part[k] = __uint_as_float(static_cast<uint32_t>(w[k]));
             }
@@ -1403,7 +1417,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         uint32_t spins = 0;
         while (!block_sync_and(sh, read_round(c0, with_stats)) && !sh.aborted) {
             __builtin_amdgcn_s_sleep(2);
-            if (threadIdx.x == 0)
+            if (tid() == 0)
                 stuck(L.exchange, L.xl, ++spins, sh);
         }
     };
@@ -1467,7 +1481,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
     float* residual = sh.small;  // rows [begin, end)
     const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
     auto prepare = [&]() {
-        for (int i = begin + static_cast<int>(threadIdx.x); i < end; i += kThreads)
+        for (int i = begin + static_cast<int>(tid()); i < end; i += kThreads)
             residual[i - begin] = input_element(L, layer, step, token, i, sh);
         poll_input(L.exchange + L.xl.attn, d, (L.shape.query_heads / L.shape.kv_heads) * L.shape.head_dim,
                    L.epoch_of(step, layer, kPhaseAttn), L.exchange, L.xl, sh,
@@ -1476,7 +1490,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
                        sh.vbits[i] = static_cast<uint16_t>(p);
                    });
         if (begin == 0)
-            for (int i = threadIdx.x; i < d; i += kThreads)
+            for (int i = tid(); i < d; i += kThreads)
                 N::store(L.scratch, L.layout.attention + i, sh.vec[i]);
     };
     gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, L.layout.Wo), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
@@ -1541,14 +1555,14 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
 
     poll_input(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
-    if (threadIdx.x == 0)
+    if (tid() == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
     const InputSlice<VPL> in = norm(sh, d, L.numeric.rms_norm_eps);
     float acc[kOut];
 #pragma unroll
     for (int n = 0; n < kOut; ++n)
         acc[n] = 0.0f;
-    const int lane = threadIdx.x & 63;
+    const int lane = tid() & 63;
     // One product row: gate and up dots, p = round(round(silu(round(gate))) * round(up)) (zero
     // past the chunk), then the lane's slice of the down row times p.
     auto product_row = [&](const u32x4* wg, const u32x4* wu, const u32x4* wd, int row) {
@@ -1701,7 +1715,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
                               __float_as_uint(acc[k * PV + 4 * h + 2]), __float_as_uint(acc[k * PV + 4 * h + 3])};
                 }
         block_sync(sh);
-        for (int o = threadIdx.x; o < KS * slice; o += kThreads) {
+        for (int o = tid(); o < KS * slice; o += kThreads) {
             const int kk = o / slice, c = o - kk * slice;
             float total = 0.0f;
             for (int wv = 0; wv < kWaves; ++wv)
@@ -1730,7 +1744,7 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
     while (tpr > 1 && tpr * rows > kThreads)
         tpr >>= 1;
     const int slots = kThreads / tpr;
-    const int slot = threadIdx.x / tpr, lane = threadIdx.x % tpr;
+    const int slot = tid() / tpr, lane = tid() % tpr;
     const uint64_t* base = L.exchange + L.xl.ffn;
     for (int first = 0; first < rows; first += slots) {
         const int row = begin + first + slot;
@@ -1810,7 +1824,7 @@ __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const t
     final_input(L, step, sh);
     rms_norm_lds<BF16>(sh.vec, L.shape.hidden_size, scale, L.numeric.rms_norm_eps, sh);
     void* hidden = (L.stack.layers + 1) % 2 == 0 ? L.input : L.output;
-    for (int i = static_cast<int>(t.begin) + threadIdx.x; i < static_cast<int>(t.end); i += kThreads)
+    for (int i = static_cast<int>(t.begin) + tid(); i < static_cast<int>(t.end); i += kThreads)
         Num<BF16>::store(hidden, i, sh.vec[i]);
 }
 
@@ -1822,7 +1836,7 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
 {
     const int d = L.shape.hidden_size;
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
-    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int lane = tid() & 63, wave = wave_id();
     ti_candidate best{-INFINITY, 0x7fffffff};
     const uint32_t row_bytes = static_cast<uint32_t>(d) * Num<BF16>::kBytes;
     const NormInput<BF16, VPL> norm(L.stack_weight(L.stack.final_norm_offset), d);
@@ -1842,7 +1856,7 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     if (lane == 0)
         sh.candidates[wave] = best;
     block_sync(sh);
-    if (threadIdx.x == 0) {
+    if (tid() == 0) {
         ti_candidate result = sh.candidates[0];
         for (int w = 1; w < kWaves; ++w)
             keep_better(result, sh.candidates[w]);
@@ -1866,7 +1880,7 @@ __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, S
     ti_candidate best{-INFINITY, 0x7fffffff};
     const uint64_t* candidates = L.exchange + L.xl.candidates;
     for (int base = 0; base < slots; base += kThreads) {  // block-uniform
-        const int slot = base + static_cast<int>(threadIdx.x);
+        const int slot = base + static_cast<int>(tid());
         const bool real = slot < slots;
         const uint64_t* words = candidates + 2 * static_cast<size_t>(real ? slot : 0);
         uint64_t a, b;
@@ -1882,7 +1896,7 @@ __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, S
             uint32_t spins = 0;
             while (!block_sync_and(sh, read()) && !sh.aborted) {
                 __builtin_amdgcn_s_sleep(2);
-                if (threadIdx.x == 0)
+                if (tid() == 0)
                     stuck(L.exchange, L.xl, ++spins, sh);
             }
         }
@@ -1893,10 +1907,10 @@ __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, S
         ti_candidate other{__shfl_xor(best.value, offset), __shfl_xor(best.id, offset)};
         keep_better(best, other);
     }
-    if ((threadIdx.x & 63) == 0)
+    if ((tid() & 63) == 0)
         sh.candidates[wave_id()] = best;
     block_sync(sh);
-    if (threadIdx.x == 0) {
+    if (tid() == 0) {
         ti_candidate result = sh.candidates[0];
         for (int w = 1; w < kWaves; ++w)
             keep_better(result, sh.candidates[w]);
@@ -2062,7 +2076,7 @@ __device__ __forceinline__ void stream_weights(const Launch<true>& L, const ti_w
     static_assert(VPL * 64 == kRingRowVectors, "streamer waves move whole rows");
     static_assert(kRingSlots % kStreamWaves == 0, "each streamer wave owns fixed ring slots");
     const uint32_t q = static_cast<uint32_t>(wave_id() - kWaves);
-    const int lane = threadIdx.x & 63;
+    const int lane = tid() & 63;
     RowWalker<true, kCached> walker(L, sh, stream);
     // Every control value of this loop is wave-uniform (scalar): an exit the compiler took for
     // divergent would mask the loop and collapse the count of loads it keeps in flight.
@@ -2152,7 +2166,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
     // The launch record lives in LDS: referenced from many inlined operations, a kernel
     // argument would be copied to scratch or spread over (and spilled from) SGPRs.
     __shared__ Launch<BF16> record;
-    if (threadIdx.x == 0) {
+    if (tid() == 0) {
         record = launch;
         sh.aborted = 0;
         sh.flag = 0;
@@ -2160,15 +2174,15 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
         sh.rsave_tag = 0;
     }
 #if TILES_RING
-    if (threadIdx.x < kWaves) {
-        sh.arrive[threadIdx.x] = 0;
-        sh.released[threadIdx.x] = 0;
+    if (tid() < kWaves) {
+        sh.arrive[tid()] = 0;
+        sh.released[tid()] = 0;
     }
-    if (threadIdx.x < kStreamWaves)
-        sh.landed[threadIdx.x] = static_cast<int>(threadIdx.x) - (kStreamWaves - 1);
-    if (threadIdx.x < 2)
-        sh.failed[threadIdx.x] = 0;
-    if (threadIdx.x == 0)
+    if (tid() < kStreamWaves)
+        sh.landed[tid()] = static_cast<int>(tid()) - (kStreamWaves - 1);
+    if (tid() < 2)
+        sh.failed[tid()] = 0;
+    if (tid() == 0)
         sh.stop = 0;
 #endif
     __syncthreads();
@@ -2181,7 +2195,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
     // starts, every record would cost a dependent memory round trip between two tasks.
     const bool cached = stream.count <= static_cast<uint32_t>(kLdsStreamRecords);
     if (cached)
-        for (uint32_t i = threadIdx.x; i < stream.count; i += kBlockThreads)
+        for (uint32_t i = tid(); i < stream.count; i += kBlockThreads)
             sh.stream[i] = load_record(L.instructions + stream.begin + i);
     __syncthreads();
 #if TILES_RING
@@ -2196,7 +2210,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
     // The compute waves leave: streamer waves waiting for ring space stop too.
     auto leave = [&]() {
 #if TILES_RING
-        if (threadIdx.x == 0)
+        if (tid() == 0)
             lds_write(&sh.stop, 1);
 #endif
     };
@@ -2207,7 +2221,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
         ti_token_id token = L.token_id;
         if (generating) {
             token = greedy(L, step, sh);
-            if (blockIdx.x == 0 && threadIdx.x == 0)
+            if (blockIdx.x == 0 && tid() == 0)
                 record_choice(L, step, token);
         } else if (L.device_tokens != nullptr) {
             token = global(L.device_tokens)[step];
@@ -2225,7 +2239,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
             // Optional timeline: 100 MHz device clock (s_memrealtime) at the start of every
             // instruction of the launch's last step, when its first exchange read returned,
             // when its inputs were complete, and at its end (diagnostic_context.cu:257-285).
-            if (L.timeline && threadIdx.x == 0) {
+            if (L.timeline && tid() == 0) {
                 global(L.timeline)[4 * static_cast<size_t>(index)] = __builtin_amdgcn_s_memrealtime();
                 sh.mark_read = 0;
                 sh.mark_ready = 0;
@@ -2239,7 +2253,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
             case TI_OP_EMBEDDING: {
                 const int d = L.shape.hidden_size;
                 const void* row = L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) + static_cast<size_t>(token) * d);
-                for (int i = static_cast<int>(task.begin) + threadIdx.x; i < static_cast<int>(task.end); i += kThreads)
+                for (int i = static_cast<int>(task.begin) + tid(); i < static_cast<int>(task.end); i += kThreads)
                     Num<BF16>::store(L.input, i, Num<BF16>::load(row, i));
                 break;
             }
@@ -2248,14 +2262,14 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
             default: break;  // attention_values: merged inside the scores tasks
             }
             block_sync(sh);
-            if (L.timeline && threadIdx.x == 0) {
+            if (L.timeline && tid() == 0) {
                 global(L.timeline)[4 * static_cast<size_t>(index) + 1] = sh.mark_read;
                 global(L.timeline)[4 * static_cast<size_t>(index) + 2] = sh.mark_ready;
                 global(L.timeline)[4 * static_cast<size_t>(index) + 3] = __builtin_amdgcn_s_memrealtime();
             }
         }
         if (sh.aborted) {
-            if (threadIdx.x == 0 && generating && blockIdx.x == 0)
+            if (tid() == 0 && generating && blockIdx.x == 0)
                 global(L.selection.status)[TI_STATUS_ERROR] = TI_DEVICE_SYNC_TIMEOUT;
             leave();
             return;
