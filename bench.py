@@ -33,7 +33,7 @@ KV_BYTES_PER_POSITION = 32_768        # 16 layers x (K + V) x 8 heads x 64 x 2 b
 PEAK_HBM_GBPS = 8000.0                # MI355X published HBM3E bandwidth
 # HBM bytes a ctx-1 generate token moves, measured with rocprofv3 FETCH_SIZE and WRITE_SIZE
 # (calibrated against a known-size read and fill), profiles/decoder_worker_llama1b_bf16_ctx1_hbm_counters.md.
-MEASURED_TRAFFIC_BYTES_PER_TOKEN = 2_696_683_192
+MEASURED_TRAFFIC_BYTES_PER_TOKEN = 2_693_231_756
 
 
 def log(*args) -> None:
