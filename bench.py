@@ -30,6 +30,7 @@ sys.path.insert(0, str(ROOT))
 
 WEIGHT_BYTES = 2_471_628_800          # bf16 weights streamed per token: 1,235,814,400 parameters x 2 bytes
 KV_BYTES_PER_POSITION = 32_768        # 16 layers x (K + V) x 8 heads x 64 x 2 bytes
+LM_HEAD_STEP_BYTES = 525_344_768      # 128256 x 2048 bf16 LM-head rows + the hidden vector and final-norm weight
 PEAK_HBM_GBPS = 8000.0                # MI355X published HBM3E bandwidth
 # HBM bytes a ctx-1 generate token moves, measured with rocprofv3 FETCH_SIZE and WRITE_SIZE
 # (calibrated against a known-size read and fill), profiles/decoder_worker_llama1b_bf16_ctx1_hbm_counters.md.
@@ -82,6 +83,9 @@ def main() -> int:
     # 130-step chunks: the 4160-position context splits into 32 chunks per K/V head, 256
     # attention tasks for 256 workers (128 would give 33 chunks and two tasks to 8 workers).
     parser.add_argument("--chunk-steps", type=int, default=130)
+    parser.add_argument("--ctx32768", action="store_true",
+                        help="also decode 64 tokens at context 32768 (BASELINE config 5: a second package with "
+                             "max_context 32832 and 1024-step attention chunks, the planner's largest: 33 per K/V head)")
     parser.add_argument("--write-package", type=Path, default=None,
                         help="only write the benchmark's package to this directory and its ctx-1 prompt to "
                              "DIR.ctx1.json (for `tiles_amd/tile_runtime bench` under a profiler), then exit")
@@ -137,6 +141,23 @@ def main() -> int:
     floor_ms = total_bytes / new_tokens / (stream_gbps * 1e9) * 1e3
     log(f"ctx1: {ms_per_token * 1e3:.1f} us/token, floor {floor_ms * 1e3:.1f} us")
 
+    # The LM-head step (BASELINE config 2's GEMV: final RMSNorm, 128256 x 2048 bf16 rows, argmax)
+    # inside one decode step: the logits phase of a timeline launch, from the end of the final
+    # norm to the last candidate, against its 525,344,768 bytes.
+    from tiles_amd import timeline as T
+    ctx.set_timeline(True)
+    ctx.wait(ctx.enqueue_reset())
+    ctx.wait(ctx.enqueue_prefill(prompt))
+    ctx.wait(ctx.enqueue_generate(64))
+    plan_dict = json.loads((work / "llama" / "plan.json").read_text())
+    phases = T.budget(plan_dict, ctx.timeline().reshape(-1, 4), len(prompt) + 63, stream_gbps)["by_opcode"]
+    ctx.set_timeline(False)
+    head_us = phases["logits"]["us"]
+    lm_head_step = {"us": head_us, "bytes": LM_HEAD_STEP_BYTES, "GBps": LM_HEAD_STEP_BYTES / (head_us * 1e-6) / 1e9,
+                    "fraction_of_stream_read": LM_HEAD_STEP_BYTES / (head_us * 1e-6) / 1e9 / stream_gbps,
+                    "measured": "logits phase of the last step of a 64-token ctx-1 launch (timeline)"}
+    log(f"LM-head step: {head_us:.1f} us, {lm_head_step['GBps']:.0f} GB/s")
+
     ctx4096 = None
     if not args.no_ctx4096:
         long_prompt = S.prompt(4096, seed=4096)
@@ -157,6 +178,29 @@ def main() -> int:
     # Release device objects while the HIP runtime is alive (profilers finalize at exit).
     del ctx, model, plan
     gc.collect()
+    ctx32768 = None
+    if args.ctx32768:
+        long_context = 32768 + 64
+        start = time.time()
+        S.llama_package(work / "llama32k", long_context, "bfloat16", seed=0, chunk_steps=1024, target=target,
+                        weights=weights)
+        log(f"ctx32768 package built in {time.time() - start:.1f}s")
+        model = R.DecoderModel(R.load_plan(work / "llama32k", verify_weights=False))
+        ctx = model.create_context()
+        start = time.time()
+        ctx.wait(ctx.enqueue_prefill(S.prompt(32768, seed=32768)))
+        prefill_s = time.time() - start
+        result = ctx.wait(ctx.enqueue_generate(64))
+        long_bytes = sum(bytes_per_token(p) for p in range(32768, 32768 + 64))
+        long_ms = result.compute_us / 64 / 1e3
+        long_floor = long_bytes / 64 / (stream_gbps * 1e9) * 1e3
+        ctx32768 = {"ms_per_token": long_ms, "tokens_per_second": 1e3 / long_ms, "floor_ms_per_token": long_floor,
+                    "fraction_of_floor": long_floor / long_ms,
+                    "achieved_GBps": long_bytes / (result.compute_us * 1e-6) / 1e9, "prefill_tokens": 32768,
+                    "prefill_s": prefill_s, "new_tokens": 64, "attention_chunk_steps": 1024}
+        log(f"ctx32768: {long_ms * 1e3:.1f} us/token, floor {long_floor * 1e3:.1f} us")
+        del ctx, model
+        gc.collect()
     baseline = None
     if args.cpu_tokens > 0:
         baseline = cpu_baseline(weights, prompt, args.cpu_tokens)
@@ -188,6 +232,8 @@ def main() -> int:
                      "kernel": "decoder_worker", "launches": launches * steps,
                      "bytes_per_launch": total_bytes / launches, "avg_launch_us": mean_us / launches},
         "ctx4096": ctx4096,
+        "ctx32768": ctx32768,
+        "lm_head_step": lm_head_step,
         "cpu_baseline": baseline,
         "generated_head": generated[:8],
     }

@@ -157,12 +157,13 @@ def test_split_context_attention_merge(target, tmp, dtype):
     (32, 160, 160, 160),   # one slice per head; a fused chunk ending on a block boundary
     (128, 128, 128, 120),  # 64-position V^T blocks: two in one chunk
     (128, 64, 64, 200),    # 128 dims over four 50-position chunks
+    (64, 1024, 1024, 2100),  # three chunks of 700 positions: five V^T blocks and many score tiles per chunk
 ])
 def test_bf16_matrix_attention(target, tmp, head_dim, chunk_steps, fused_steps, context):
     """bf16 heads of 32-128 dims (the matrix-core attention) against the oracle: fused chunks of
     up to 256 positions and split chunks, logits within bf16 rounding and the same greedy token."""
     block = P.BlockSpec(hidden_size=4 * head_dim, intermediate_size=512, num_attention_heads=4, num_key_value_heads=1,
-                        head_dim=head_dim, max_context=320)
+                        head_dim=head_dim, max_context=max(320, context + 8))
     spec = P.StackSpec(block, 2, 512, True)
     weights = K.random_weights(spec, seed=head_dim + context, std=0.08, dtype=torch.float32)
     path = tmp / f"mfma_{head_dim}_{chunk_steps}_{context}"
@@ -280,3 +281,44 @@ def test_llama_bf16_tokens_and_logits(target, tmp, llama_weights):
         top2 = np.sort(want)[-2:]
         if top2[1] - top2[0] > BF16_1B_NOISE_FLOOR:
             assert generated[step] == oracle["tokens"][step]
+
+
+@pytest.mark.slow
+def test_isolated_lm_head_step_token(target, tmp):
+    """The isolated LM-head step: bf16 h ~ N(0, 1) [2048] through the final RMSNorm (weight 1.0)
+    and a GEMV against an untied [128256 x 2048] bf16 matrix ~ N(0, 0.02), then greedy argmax.
+
+    Built as a one-layer stack whose layer weights are all zero, so the layer hands its input
+    on unchanged (attention and FFN outputs are exactly 0, y = x in bf16), and whose embedding
+    rows 0-2 hold three seeded h vectors.  The token must equal the oracle's whenever the
+    oracle's top-2 gap exceeds one bf16 rounding of the top logit; the logits must agree within
+    one bf16 rounding (the GPU and PyTorch CPU accumulate the 2048-term dots in different
+    orders, and every logit is rounded to bf16)."""
+    block = P.BlockSpec(hidden_size=2048, intermediate_size=8192, num_attention_heads=32, num_key_value_heads=8,
+                        head_dim=64, max_context=8)
+    spec = P.StackSpec(block, 1, 128256, False)
+    generator = torch.Generator().manual_seed(2)
+    weights = {}
+    for name in K.weight_names(spec):
+        shape = K.weight_shape(spec, name)
+        weights[name] = torch.ones(shape) if name.endswith("norm") else torch.zeros(shape)
+    weights["lm_head"] = torch.randn(K.weight_shape(spec, "lm_head"), generator=generator) * 0.02
+    h = torch.randn(3, 2048, generator=generator)
+    weights["embedding"][:3] = h
+    weights = {k: v.to(torch.bfloat16) for k, v in weights.items()}
+    K.build_stack_package(spec, weights, target, tmp / "lm_head_step", "bfloat16")
+    _, ctx = context_for(tmp / "lm_head_step")
+    ospec = ref.Spec(hidden_size=2048, intermediate_size=8192, num_attention_heads=32, num_key_value_heads=8,
+                     head_dim=64, max_context=8, layers=1, vocab_size=128256, tie_word_embeddings=False)
+    cache = ref.StackCache.empty(ospec, torch.bfloat16)
+    for token in range(3):
+        got = ctx.collect(ctx.enqueue_decode(token, logits=True))["logits"]
+        with torch.inference_mode():
+            out = ref.decode_token(token, weights, ospec, cache, keep_blocks=True)
+        assert torch.equal(out["blocks"][0]["y"], weights["embedding"][token])  # the layer passes h on unchanged
+        want = out["logits"].float().numpy()
+        rounding = np.abs(want) * 2.0 ** -8 + 1e-6  # half a bf16 ulp of each logit
+        assert np.all(np.abs(got - want) <= 2 * rounding), np.abs(got - want).max()
+        top2 = np.sort(want)[-2:]
+        if top2[1] - top2[0] > 2.0 ** -7 * abs(top2[1]):
+            assert int(got.argmax()) == int(want.argmax()), (token, int(got.argmax()), int(want.argmax()))
