@@ -54,7 +54,10 @@ constexpr int kLdsHidden = kRingHidden;
 constexpr int kLdsRegionFloats = kRingRegionFloats;
 constexpr int kLdsStreamRecords = kRingStreamRecords;
 constexpr int kRingRowVectors = kRingHidden * 2 / 16;  // 16-byte vectors of one bf16 weight row
-constexpr int kStageRows = 7;                          // rows in flight per streamer wave
+// Rows in flight per streamer wave: 12 rows (48 KB) per CU.  HBM streams at 95% of its peak
+// with 32 KB in flight per CU, and every extra byte in flight across the chip lengthens the
+// memory queue that each load waits in (7 rows: 8 us load latency during the FFN, and slower).
+constexpr int kStageRows = 3;
 #else
 constexpr int kBlockThreads = kThreads;
 constexpr int kLdsHidden = kMaxHidden;
