@@ -1209,6 +1209,29 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     float* stat_max = sh.small;
     float* stat_sum = sh.small + kMaxGroup;
     const bool fused = chunks == 1;
+    // Matrix path: the probabilities also go to LDS as the bf16 operands of P V, each head's
+    // positions contiguous and zero up to whole V^T blocks, so that one 16-byte read is a lane's
+    // 8 positions: the fused chunk's rounded probabilities, or a split chunk's exact three bf16
+    // parts (hi + mid + lo, each the next 8 significant bits).  These are the bits the matrix loop
+    // would otherwise pack from the FP32 scores.  Chunks too long for the work region keep that.
+    const int span_pad = (span + PB - 1) / PB * PB;
+    const int parts = fused ? 1 : 3;
+    const int p_offset = (group * span + 7) / 8 * 8;  // floats: after the scores, 16-byte aligned
+    const bool packed_p = kMfma && (p_offset + (parts * group * span_pad + 1) / 2) <= kLdsRegionFloats;
+    uint16_t* pbits = reinterpret_cast<uint16_t*>(scores + p_offset);  // [parts][group][span_pad]
+    auto put_p = [&](int g, int i, float v) {
+        if (fused) {
+            pbits[g * span_pad + i] = static_cast<uint16_t>(__float_as_uint(v) >> 16);
+        } else {
+            const float hi = __uint_as_float(__float_as_uint(v) & 0xffff0000u);
+            const float rest = v - hi;
+            const float mid = __uint_as_float(__float_as_uint(rest) & 0xffff0000u);
+            const float lo = rest - mid;
+            pbits[g * span_pad + i] = static_cast<uint16_t>(__float_as_uint(v) >> 16);
+            pbits[(group + g) * span_pad + i] = static_cast<uint16_t>(__float_as_uint(rest) >> 16);
+            pbits[(2 * group + g) * span_pad + i] = static_cast<uint16_t>(__float_as_uint(lo) >> 16);
+        }
+    };
     if (wave < group) {
         float* row = scores + wave * span;
         float m = -INFINITY;
@@ -1220,11 +1243,20 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             const float e = expf(row[i] - m);
             row[i] = e;
             sum += e;
+            if (packed_p && !fused)
+                put_p(wave, i, e);
         }
         sum = lane_value(group_sum<64>(sum), 63);
         if (fused)
-            for (int i = lane; i < span; i += 64)
-                row[i] = N::round(row[i] / sum);
+            for (int i = lane; i < span; i += 64) {
+                const float v = N::round(row[i] / sum);
+                row[i] = v;
+                if (packed_p)
+                    put_p(wave, i, v);
+            }
+        if (packed_p)
+            for (int i = span + lane; i < span_pad; i += 64)
+                put_p(wave, i, 0.0f);
         if (lane == 63) {
             stat_max[wave] = m;
             stat_sum[wave] = sum;
@@ -1255,7 +1287,24 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 }
                 block_sync(sh);
             }
-            if (n < dh / 16) {
+            if (n < dh / 16 && packed_p) {
+                const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int q = 0; q < PB / 32; ++q) {
+                    const int t0 = first + 32 * q + 8 * tk;
+                    const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + (16 * n + tr) * kVtStride + 32 * q + 8 * tk);
+                    auto operand = [&](int part) {
+                        return tr < group ? *reinterpret_cast<const u32x4*>(pbits + (part * group + tr) * span_pad + t0) : zero;
+                    };
+                    if (fused) {
+                        o = mfma_16x16x32_bf16(operand(0), vb, o);
+                    } else {
+                        o = mfma_16x16x32_bf16(operand(0), vb, o);
+                        o = mfma_16x16x32_bf16(operand(1), vb, o);
+                        o = mfma_16x16x32_bf16(operand(2), vb, o);
+                    }
+                }
+            } else if (n < dh / 16) {
 #pragma unroll
                 for (int q = 0; q < PB / 32; ++q) {
                     const int t0 = first + 32 * q + 8 * tk;
