@@ -1232,7 +1232,36 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             pbits[(2 * group + g) * span_pad + i] = static_cast<uint16_t>(__float_as_uint(lo) >> 16);
         }
     };
-    if (wave < group) {
+    if (wave < group && packed_p && span_pad <= 3 * 64) {
+        // At most one V^T block: the wave's scores stay in registers (3 per lane), read once;
+        // the same maximum, exp, sum order and rounding as below, and no FP32 write-back.
+        const float* row = scores + wave * span;
+        float v[3], e[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int i = lane + 64 * k;
+            v[k] = i < span ? row[i] : -INFINITY;
+        }
+        float m = fmaxf(fmaxf(v[0], v[1]), v[2]);
+        m = lane_value(group_max(m, 64), 63);
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            e[k] = lane + 64 * k < span ? expf(v[k] - m) : 0.0f;
+            sum += e[k];
+        }
+        sum = lane_value(group_sum<64>(sum), 63);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int i = lane + 64 * k;
+            if (i < span_pad)
+                put_p(wave, i, fused ? N::round(e[k] / sum) : e[k]);  // 0 past the span
+        }
+        if (lane == 63) {
+            stat_max[wave] = m;
+            stat_sum[wave] = sum;
+        }
+    } else if (wave < group) {
         float* row = scores + wave * span;
         float m = -INFINITY;
         for (int i = lane; i < span; i += 64)
