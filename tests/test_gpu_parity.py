@@ -251,18 +251,30 @@ def llama_oracle_spec(max_context):
 
 @pytest.mark.slow
 def test_llama_fp32_logits_within_1e4_relative(target, tmp, llama_weights):
+    """The north star's fp32 bar on BASELINE config 1: an 8-token prompt drawn uniformly from the
+    vocabulary with a seed, then 32 greedy tokens; every step's logits within 1e-4 relative of the
+    oracle's (forced along the GPU's tokens), and the same tokens wherever the oracle's top-2 gap
+    exceeds that tolerance."""
     weights = {k: v.float() for k, v in llama_weights.items()}
-    S.llama_package(tmp / "l1b_f32", 64, "float32", target=target, weights=weights, chunk_steps=64)
+    prompt, new_tokens = S.prompt(8, seed=8), 32
+    S.llama_package(tmp / "l1b_f32", len(prompt) + new_tokens + 8, "float32", target=target, weights=weights,
+                    chunk_steps=64)
     _, ctx = context_for(tmp / "l1b_f32")
-    ospec = llama_oracle_spec(64)
-    cache = ref.StackCache.empty(ospec, torch.float32)
-    for token in [S.BOS, 9906, 1917]:
+    ctx.wait(ctx.enqueue_prefill(prompt))
+    generated = ctx.wait(ctx.enqueue_generate(new_tokens)).generated
+    assert len(generated) == new_tokens
+    ospec = llama_oracle_spec(len(prompt) + new_tokens + 8)
+    oracle = ref.generate(prompt, new_tokens, weights, ospec, torch.float32, forced=generated)
+    ctx.wait(ctx.enqueue_reset())
+    ctx.wait(ctx.enqueue_prefill(prompt[:-1]))
+    for step, token in enumerate([prompt[-1]] + generated[:-1]):
         got = ctx.collect(ctx.enqueue_decode(token, logits=True))["logits"]
-        with torch.inference_mode():
-            want = ref.decode_token(token, weights, ospec, cache)["logits"].numpy()
+        want = oracle["logits"][step].numpy()
         scale = np.abs(want).max()
-        assert np.abs(got - want).max() <= 1e-4 * scale, np.abs(got - want).max()
-        assert int(got.argmax()) == int(want.argmax())
+        assert np.abs(got - want).max() <= 1e-4 * scale, (step, np.abs(got - want).max())
+        top2 = np.sort(want)[-2:]
+        if top2[1] - top2[0] > 1e-4 * scale:
+            assert generated[step] == oracle["tokens"][step], step
 
 
 @pytest.mark.slow

@@ -603,13 +603,16 @@ __device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& s
     for (int w = 0; w < kWaves; ++w)
         total += sh.small[w];
     const float inv = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
+    // x[k] still holds v[i]: nobody writes v between the first read and here, and re-reading it
+    // after the barriers made every element a dependent LDS round trip.
 #pragma unroll
     for (int k = 0; k < kLdsHidden / kThreads; ++k) {
         const int i = k * kThreads + static_cast<int>(tid());
         if (i < d) {
-            v[i] = Num<BF16>::round(Num<BF16>::round(v[i] * inv) * scale.v[k]);
+            const float y = Num<BF16>::round(Num<BF16>::round(x[k] * inv) * scale.v[k]);
+            v[i] = y;
             if constexpr (BF16)
-                sh.vbits[i] = static_cast<uint16_t>(float_to_bf16_bits(v[i]));
+                sh.vbits[i] = static_cast<uint16_t>(float_to_bf16_bits(y));
         }
     }
     block_sync(sh);
