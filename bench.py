@@ -6,6 +6,10 @@ Prints ONE JSON line.  The workload of the headline metric (ms/token of batch-1 
 * ctx 4096: 4096 seeded uniform prompt tokens prefilled, then 64 new tokens in one launch
   (reported under ``ctx4096``).
 
+Each runs on a package of the same weights planned for its context: 321 positions with the
+planner's default attention chunking (one fused chunk) for ctx 1, 4160 positions in 130-step
+chunks for ctx 4096.
+
 A "step" is one token of decode (one pass of the hot path); ``ms_per_step`` = ``value``
 = ms/token of the generate launches, timed with HIP events on the context stream (prefill,
 setup and readback excluded, as the reference's ``tile_runtime bench``).  The roofline block
@@ -80,15 +84,18 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-ctx4096", action="store_true")
     parser.add_argument("--cpu-tokens", type=int, default=24)
-    # 130-step chunks: the 4160-position context splits into 32 chunks per K/V head, 256
-    # attention tasks for 256 workers (128 would give 33 chunks and two tasks to 8 workers).
-    parser.add_argument("--chunk-steps", type=int, default=130)
+    # Each configuration runs on a package planned for its context.  ctx 1 (positions 1-256): a
+    # 321-position package with the planner's default chunking, one fused chunk (the planner fuses
+    # contexts up to 384 positions).  ctx 4096: 130-step chunks split the 4160-position context
+    # into 32 chunks per K/V head, 256 attention tasks for 256 workers (128 would give 33 chunks and
+    # two tasks to 8 workers).
+    parser.add_argument("--chunk-steps", type=int, default=130, help="attention chunk steps of the ctx-4096 package")
     parser.add_argument("--ctx32768", action="store_true",
                         help="also decode 64 tokens at context 32768 (BASELINE config 5: a second package with "
                              "max_context 32832 and 1024-step attention chunks, the planner's largest: 33 per K/V head)")
     parser.add_argument("--write-package", type=Path, default=None,
-                        help="only write the benchmark's package to this directory and its ctx-1 prompt to "
-                             "DIR.ctx1.json (for `tiles_amd/tile_runtime bench` under a profiler), then exit")
+                        help="only write the ctx-1 package to this directory and its prompt to DIR.ctx1.json "
+                             "(for `tiles_amd/tile_runtime bench` under a profiler), then exit")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the decode worker is single-GPU); --gpus {args.gpus} is not supported",
@@ -101,26 +108,25 @@ def main() -> int:
     from tiles_amd.tileplan import probe
 
     target = probe.probe_library()
+    new_tokens = 256
+    prompt = [S.BOS]
+    ctx1_context = len(prompt) + new_tokens + 64
     if args.write_package is not None:
-        S.llama_package(args.write_package, 4096 + 64, "bfloat16", seed=0, chunk_steps=args.chunk_steps, target=target)
+        S.llama_package(args.write_package, ctx1_context, "bfloat16", seed=0, target=target)
         Path(f"{args.write_package}.ctx1.json").write_text(json.dumps({"tokens": [S.BOS]}) + "\n")
         log(f"wrote {args.write_package} and {args.write_package}.ctx1.json")
         return 0
     stream_gbps = R.measure_stream_read(2 << 30, 3)
     log(f"measured stream read {stream_gbps:.1f} GB/s")
     work = S.scratch_dir()
-    max_context = 4096 + 64
     start = time.time()
-    spec, weights = S.llama_package(work / "llama", max_context, "bfloat16", seed=0, chunk_steps=args.chunk_steps,
-                                    target=target)
-    log(f"package built in {time.time() - start:.1f}s")
+    spec, weights = S.llama_package(work / "llama", ctx1_context, "bfloat16", seed=0, target=target)
+    log(f"ctx-1 package built in {time.time() - start:.1f}s")
     plan = R.load_plan(work / "llama", verify_weights=False)
     model = R.DecoderModel(plan)
     ctx = model.create_context()
 
     # ctx 1: 1-token prompt, 256 new tokens (4 launches of 64)
-    new_tokens = 256
-    prompt = [S.BOS]
     times, generated = [], None
     for round_ in range(args.warmup + steps):
         ctx.wait(ctx.enqueue_reset())
@@ -158,10 +164,17 @@ def main() -> int:
                     "measured": "logits phase of the last step of a 64-token ctx-1 launch (timeline)"}
     log(f"LM-head step: {head_us:.1f} us, {lm_head_step['GBps']:.0f} GB/s")
 
+    del ctx, model, plan
+    gc.collect()
     ctx4096 = None
     if not args.no_ctx4096:
+        start = time.time()
+        S.llama_package(work / "llama4k", 4096 + 64, "bfloat16", seed=0, chunk_steps=args.chunk_steps, target=target,
+                        weights=weights)
+        log(f"ctx-4096 package built in {time.time() - start:.1f}s")
+        model = R.DecoderModel(R.load_plan(work / "llama4k", verify_weights=False))
+        ctx = model.create_context()
         long_prompt = S.prompt(4096, seed=4096)
-        ctx.wait(ctx.enqueue_reset())
         start = time.time()
         ctx.wait(ctx.enqueue_prefill(long_prompt))
         prefill_s = time.time() - start
@@ -174,10 +187,9 @@ def main() -> int:
                    "achieved_GBps": long_bytes / (result.compute_us * 1e-6) / 1e9,
                    "prefill_tokens": 4096, "prefill_s": prefill_s, "new_tokens": 64}
         log(f"ctx4096: {long_ms * 1e3:.1f} us/token, floor {long_floor * 1e3:.1f} us")
-
-    # Release device objects while the HIP runtime is alive (profilers finalize at exit).
-    del ctx, model, plan
-    gc.collect()
+        # Release device objects while the HIP runtime is alive (profilers finalize at exit).
+        del ctx, model
+        gc.collect()
     ctx32768 = None
     if args.ctx32768:
         long_context = 32768 + 64
@@ -221,7 +233,10 @@ def main() -> int:
         "config": {"workload": "Llama-3.2-1B bf16 batch-1 greedy decode, ctx 1: 1-token prompt, 256 new tokens, "
                                "64 per persistent launch; ctx 4096 (4096-token prompt, 64 new tokens) under ctx4096",
                    "global_batch": 1, "seq_len": len(prompt) + new_tokens, "parallelism": "none",
-                   "attention_chunk_steps": args.chunk_steps, "workers": target["launch"]["worker_count"]},
+                   "packages": {"ctx1": f"max_context {ctx1_context}, planner default attention chunking "
+                                        "(one fused chunk)",
+                                "ctx4096": f"max_context 4160, attention chunk steps {args.chunk_steps}"},
+                   "workers": target["launch"]["worker_count"]},
         "tokens_per_second": 1e3 / ms_per_token,
         "hbm_stream_read_GBps": stream_gbps,
         "floor_ms_per_token": floor_ms,
