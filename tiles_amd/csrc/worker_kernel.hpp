@@ -1143,10 +1143,19 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         for (int j = 0; j < TW; ++j)
             if ((wave + j * kWaves) * kTile < span)
                 tile_scores(wave + j * kWaves, kfirst[j]);
-        for (int tile = wave + TW * kWaves; tile * kTile < span; tile += kWaves) {
-            u32x4 kb[KS];
-            load_tile(krsrc, tile, kb);
-            tile_scores(tile, kb);
+        // Tiles past the preloaded ones (chunks longer than TW * kWaves tiles): kGroup per wave
+        // in flight at once, one wait per group instead of one per tile (tiles past the chunk
+        // read zeros without memory traffic).
+        constexpr int kGroup = kRing ? 2 : 4;  // the streaming worker has 168 VGPRs per wave
+        for (int tile0 = wave + TW * kWaves; tile0 * kTile < span; tile0 += kGroup * kWaves) {
+            u32x4 kb[kGroup][KS];
+#pragma unroll
+            for (int gi = 0; gi < kGroup; ++gi)
+                load_tile(krsrc, tile0 + gi * kWaves, kb[gi]);
+#pragma unroll
+            for (int gi = 0; gi < kGroup; ++gi)
+                if ((tile0 + gi * kWaves) * kTile < span)
+                    tile_scores(tile0 + gi * kWaves, kb[gi]);
         }
 #pragma unroll
         for (int j = 0; j < TW; ++j)
@@ -1306,19 +1315,21 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         // positions (zero past the group or the span), B = the same positions of V^T row 16 n + tr.
         f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
         const int n = wave;
+        // The next block's V tiles load while this block's P V runs.
+        u32x4 vnext[TW][KS];
         for (int first = 0; first < span; first += PB) {
             if (first > 0) {
                 block_sync(sh);  // the previous block's V^T has been read
 #pragma unroll
-                for (int j = 0; j < TW; ++j) {
-                    if (wave + j * kWaves < kBlockTiles) {
-                        u32x4 vb[KS];
-                        load_tile(vrsrc, first / kTile + wave + j * kWaves, vb);
-                        write_vt(first / kTile, j, vb);
-                    }
-                }
+                for (int j = 0; j < TW; ++j)
+                    if (wave + j * kWaves < kBlockTiles)
+                        write_vt(first / kTile, j, vnext[j]);
                 block_sync(sh);
             }
+            if (first + PB < span)  // block-uniform
+#pragma unroll
+                for (int j = 0; j < TW; ++j)
+                    load_tile(vrsrc, (first + PB) / kTile + wave + j * kWaves, vnext[j]);
             if (n < dh / 16 && packed_p) {
                 const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
