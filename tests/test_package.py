@@ -122,6 +122,7 @@ MUTATIONS = [
     ("policy", lambda p: p["model"].update(numeric_policy="x"), "inconsistent numeric policy"),
     ("hidden", lambda p: p["model"].update(hidden_size=48), "unsupported decoder dimensions"),
     ("chunks", lambda p: p["model"].update(attention_chunks=2), "invalid attention chunking"),
+    ("layers", lambda p: p["model"].update(layers=121), "more layers than the bf16 worker's exchange tags allow"),
     ("descriptor", lambda p: p["model"]["tensors"][2].update(shape=[1, 1]), "invalid tensor descriptors"),
     ("fingerprint", lambda p: p["target"].update(kernel_fingerprint="sm86"), "does not match compiled worker"),
     ("workers", lambda p: p["target"].update(worker_count=20), "does not match compiled worker"),

@@ -155,6 +155,14 @@ __device__ inline void coherent_storef(float* p, float v)
 {
     __hip_atomic_store(global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ inline uint32_t coherent_load32(const uint32_t* p)
+{
+    return __hip_atomic_load(global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void coherent_store32(uint32_t* p, uint32_t v)
+{
+    __hip_atomic_store(global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ inline void coherent_store16(uint16_t* p, uint16_t v)
 {
     __hip_atomic_store(global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -121,6 +121,8 @@ std::string check_launch_shape(const ti_worker_program_view& p, const ti_worker_
         return "sequence context capacity reached";
     if (p.stack.full_stack && p.selection_slots <= 0)
         return "stack without selection slots";
+    if (p.weight_dtype == TI_DTYPE_BFLOAT16 && p.stack.layers > kMaxTaggedLayers)
+        return "more layers than the bf16 worker's exchange tags allow (120)";
     // Weight loads address one layer's weights, and the LM head, with 32-bit buffer offsets.
     const uint64_t elem = p.weight_dtype == TI_DTYPE_BFLOAT16 ? 2 : 4;
     if (static_cast<uint64_t>(p.stack.layer_weight_stride) * elem >= kBufferRange ||

@@ -557,6 +557,8 @@ LoadedPlan load_plan(const std::string& package, const ti_target& target, bool v
             "unsupported decoder dimensions");
     const std::string limits = check_shape(s, bf16 ? TI_DTYPE_BFLOAT16 : TI_DTYPE_FLOAT32);
     require(limits.empty(), "decoder dimensions exceed the compiled worker's limits: " + limits);
+    require(!bf16 || layers <= kMaxTaggedLayers,
+            "decoder dimensions exceed the compiled worker's limits: more layers than the bf16 worker's exchange tags allow (120)");
     const int group = s.query_heads / s.kv_heads;
     const int64_t longest = s.max_context <= s.attention_fused_steps
                                 ? 1

@@ -48,8 +48,15 @@ inline constexpr int kPhases = 8;
 
 __host__ __device__ inline uint32_t epochs_per_step(int layers) { return static_cast<uint32_t>(layers + 1) * kPhases; }
 
+// bf16 vector exchanges carry a 16-bit tag of the epoch, which tells epochs apart that are less
+// than 65535 apart; one launch spans 64 x 8 x (layers + 1) epochs.
+inline constexpr int kMaxTaggedLayers = 120;
+static_assert(TI_MAX_LAUNCH_STEPS * kPhases * (kMaxTaggedLayers + 1) < 65535, "tagged exchange epochs");
+
 // Word offsets into the exchange area.  Each word: payload in bits 0-31 (one bf16 or fp32
-// element, or a candidate field), writer's epoch in bits 32-63.
+// element, or a candidate field), writer's epoch in bits 32-63.  In bf16, the vectors every
+// worker reads (hidden0/1, attn, r) hold two elements per word instead, each a 32-bit half with
+// a 16-bit epoch tag (worker_kernel.hpp, exchange_tag), and use the first half of their region.
 struct ExchangeLayout {
     size_t control;      // [0]: nonzero once a worker declared a wait stuck
     size_t hidden0, hidden1;  // layer outputs, alternating like the hidden buffers

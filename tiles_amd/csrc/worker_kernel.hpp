@@ -329,9 +329,33 @@ __device__ inline bool stuck(uint64_t* exchange, const ExchangeLayout& xl, uint3
     return false;
 }
 
+// The bf16 vectors that every worker reads (layer outputs, the attention output, the attention
+// block output) travel as 32-bit halves of exchange words: element i is half i of its region,
+// its bf16 bits in the low 16 bits and exchange_tag(epoch) in the high 16.  A producer publishes
+// an element with one 4-byte store and a reader gets two elements per 8-byte load: the bytes
+// that all 256 workers pull from the few memory channels holding such a vector set the cost of
+// reading it.  The tag is never 0 (a cleared word), and two epochs less than 65535 apart have
+// different tags.  An element's previous contents are at most one launch older than the epoch
+// a reader waits for (every launch writes every element at its first step, and a failed launch
+// requires a reset, which clears the exchange): 64 x 8 x (layers + 1) epochs, below 65535 for
+// the kMaxTaggedLayers layers the launcher accepts.
+__device__ inline uint32_t exchange_tag(uint32_t epoch) { return epoch % 65535u + 1u; }
+
+// Whether exchange word w carries `want`: in its high half (one element per word), or in the
+// high 16 bits of both halves (two tagged bf16 elements per word).
+template <bool kHalves>
+__device__ inline bool word_present(uint64_t w, uint32_t want)
+{
+    if constexpr (kHalves)
+        return static_cast<uint32_t>(w >> 48) == want && (static_cast<uint32_t>(w) >> 16) == want;
+    else
+        return static_cast<uint32_t>(w >> 32) == want;
+}
+
 // Wave 0 alone: waits until one "witness" word every `stride` words of src[0, count) carries
-// `epoch` (8 loads in flight per lane, a back-off between rounds).
-__device__ inline void wait_witness_words(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
+// `want` (8 loads in flight per lane, a back-off between rounds).
+template <bool kHalves>
+__device__ inline void wait_witness_words(const uint64_t* src, int count, int stride, uint32_t want, uint64_t* exchange,
                                           const ExchangeLayout& xl, Shared& sh)
 {
     constexpr int kWitnessBatch = 8;
@@ -350,7 +374,7 @@ __device__ inline void wait_witness_words(const uint64_t* src, int count, int st
             }
 #pragma unroll
             for (int u = 0; u < kWitnessBatch; ++u)
-                mine &= static_cast<uint32_t>(v[u] >> 32) == epoch;
+                mine &= word_present<kHalves>(v[u], want);
         }
         if (__all(mine))
             break;
@@ -362,35 +386,40 @@ __device__ inline void wait_witness_words(const uint64_t* src, int count, int st
     }
 }
 
-// Reads `count` (at most kLdsHidden) exchange words from `src` until each carries `epoch`
-// and hands each payload to `sink(index, payload)`.  Block-wide: every thread must call it.
+// Reads `count` (at most kLdsHidden) exchange elements from `src` until each carries `epoch`
+// and hands each payload to `sink(index, payload)`: one element per word, or with kHalves two
+// tagged bf16 elements per word (exchange_tag; `count` even).  Block-wide: every thread must
+// call it.
 // The first read is optimistic (one coherent round trip when the producers are done).  If any
 // word is still missing, only wave 0 keeps polling, one "witness" word every `stride` words
-// (every producer writes a run of at least `stride` words), with a back-off; the block then
+// (every producer writes a run of at least `stride` elements), with a back-off; the block then
 // re-reads.  Polling the whole vector from every thread of every worker floods the few memory
 // channels that hold it and slows the producers themselves.  Every read issues all its loads
 // before it looks at any of them: a use right after a load waits for it, and a loop of such
 // pairs would pay one round trip per word.
-template <typename Sink>
+template <bool kHalves, typename Sink>
 __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
                                           const ExchangeLayout& xl, Shared& sh, Sink sink)
 {
-    constexpr int kBatch = (kLdsHidden + kThreads - 1) / kThreads;
+    constexpr int kBatch = ((kHalves ? kLdsHidden / 2 : kLdsHidden) + kThreads - 1) / kThreads;
+    const int words = kHalves ? count / 2 : count;
+    const int stride_words = kHalves ? (stride > 1 ? stride / 2 : 1) : stride;
+    const uint32_t want = kHalves ? exchange_tag(epoch) : epoch;
     uint64_t w[kBatch];
 #pragma unroll
     for (int k = 0; k < kBatch; ++k)
-        w[k] = static_cast<uint64_t>(epoch) << 32;
+        w[k] = kHalves ? (static_cast<uint64_t>(want) << 48) | (want << 16) : static_cast<uint64_t>(want) << 32;
     auto read = [&]() {
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int index = k * kThreads + static_cast<int>(tid());
-            if (k * kThreads < count)  // block-uniform; lanes past count re-read the last word
-                w[k] = coherent_load64(src + (index < count ? index : count - 1));
+            if (k * kThreads < words)  // block-uniform; lanes past the end re-read the last word
+                w[k] = coherent_load64(src + (index < words ? index : words - 1));
         }
         bool ok = true;
 #pragma unroll
         for (int k = 0; k < kBatch; ++k)
-            ok &= static_cast<uint32_t>(w[k] >> 32) == epoch;
+            ok &= word_present<kHalves>(w[k], want);
         return ok;
     };
     const bool all_present = block_sync_and(sh, read());
@@ -398,7 +427,7 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
         sh.mark_read = __builtin_amdgcn_s_memrealtime();
     if (!all_present) {
         if (tid() < 64)
-            wait_witness_words(src, count, stride, epoch, exchange, xl, sh);
+            wait_witness_words<kHalves>(src, words, stride_words, want, exchange, xl, sh);
         block_sync(sh);
         uint32_t spins = 0;
         while (!block_sync_and(sh, read()) && !sh.aborted) {
@@ -410,8 +439,14 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
         const int index = k * kThreads + static_cast<int>(tid());
-        if (index < count)
-            sink(index, static_cast<uint32_t>(w[k]));
+        if (index < words) {
+            if constexpr (kHalves) {
+                sink(2 * index, static_cast<uint32_t>(w[k]) & 0xffffu);
+                sink(2 * index + 1, static_cast<uint32_t>(w[k] >> 32) & 0xffffu);
+            } else {
+                sink(index, static_cast<uint32_t>(w[k]));
+            }
+        }
     }
     // This worker's earlier stores (K/V cache rows written after their exchange words) complete
     // before anything it publishes from here on, which is what every later reader of those rows
@@ -421,15 +456,15 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
         sh.mark_ready = __builtin_amdgcn_s_memrealtime();
 }
 
-// The input poll of a GEMV task, followed by a barrier: the sink's LDS writes are then visible
-// to every wave.  (Polling from wave 0 alone, so that the other waves' prefetched weights stay
-// ahead of no reads, measured slower: one wave needs more coherent round trips, and a round trip
-// costs about 1.5 us under full HBM load.)
-template <typename Sink>
+// The input poll of a GEMV task (a vector exchange: tagged halves in bf16), followed by a
+// barrier: the sink's LDS writes are then visible to every wave.  (Polling from wave 0 alone, so
+// that the other waves' prefetched weights stay ahead of no reads, measured slower: one wave
+// needs more coherent round trips, and a round trip costs about 1.5 us under full HBM load.)
+template <bool BF16, typename Sink>
 __device__ __forceinline__ void poll_input(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
                                           const ExchangeLayout& xl, Shared& sh, Sink sink)
 {
-    poll_words(src, count, stride, epoch, exchange, xl, sh, sink);
+    poll_words<BF16>(src, count, stride, epoch, exchange, xl, sh, sink);
     block_sync(sh);
 }
 
@@ -445,6 +480,27 @@ __device__ inline uint32_t poll_one(const uint64_t* src, uint32_t epoch, uint64_
         stuck(exchange, xl, ++spins, sh);
     }
     return static_cast<uint32_t>(w);
+}
+
+// Element `index` of a vector exchange, waited for by the calling thread alone: its payload.
+template <bool BF16>
+__device__ inline uint32_t poll_element(const uint64_t* region, int index, uint32_t epoch, uint64_t* exchange,
+                                        const ExchangeLayout& xl, Shared& sh)
+{
+    if constexpr (BF16) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(region) + index;
+        const uint32_t want = exchange_tag(epoch);
+        uint32_t w = coherent_load32(src);
+        uint32_t spins = 0;
+        while ((w >> 16) != want && !sh.aborted) {
+            __builtin_amdgcn_s_sleep(2);
+            w = coherent_load32(src);
+            stuck(exchange, xl, ++spins, sh);
+        }
+        return w & 0xffffu;
+    } else {
+        return poll_one(region + index, epoch, exchange, xl, sh);
+    }
 }
 
 // Wave 0 waits until each witness word witness(j), j < n, carries `epoch` (8 loads in flight per
@@ -491,6 +547,16 @@ __device__ inline void publish(uint64_t* dst, int index, float rounded, uint32_t
     coherent_store64(dst + index, (static_cast<uint64_t>(epoch) << 32) | Num<BF16>::payload(rounded));
 }
 
+// Element `index` of a vector exchange (tagged halves in bf16, words in FP32).
+template <bool BF16>
+__device__ inline void publish_element(uint64_t* region, int index, float rounded, uint32_t epoch)
+{
+    if constexpr (BF16)
+        coherent_store32(reinterpret_cast<uint32_t*>(region) + index, (exchange_tag(epoch) << 16) | Num<BF16>::payload(rounded));
+    else
+        publish<false>(region, index, rounded, epoch);
+}
+
 // Witness spacing of an exchange written by row tasks that split `n` rows over `workers`
 // (plan_core.py:275-278: every task gets at least n / workers rows).
 __device__ inline int row_stride(int n, int workers) { return n >= workers ? n / workers : 1; }
@@ -524,7 +590,7 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, in
         }
         block_sync(sh);
     } else {
-        poll_input(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
+        poll_input<BF16>(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
                    L.exchange, L.xl, sh, [&](int i, uint32_t p) { dst[i] = sh.xsave[i] = Num<BF16>::from_payload(p); });
     }
     if (tid() == 0)
@@ -544,8 +610,8 @@ __device__ __forceinline__ float input_element(const Launch<BF16>& L, int layer,
                                                     static_cast<size_t>(token) * L.shape.hidden_size),
                                      i)
                    : Num<BF16>::load(L.input, i);
-    return Num<BF16>::from_payload(
-        poll_one(L.exchange + L.xl.hidden(layer % 2) + i, L.epoch_of(step, layer - 1, kPhaseY), L.exchange, L.xl, sh));
+    return Num<BF16>::from_payload(poll_element<BF16>(L.exchange + L.xl.hidden(layer % 2), i,
+                                                      L.epoch_of(step, layer - 1, kPhaseY), L.exchange, L.xl, sh));
 }
 
 // Element i of a layer's attention block output (the FFN's residual).
@@ -554,7 +620,8 @@ __device__ __forceinline__ float attention_output_element(const Launch<BF16>& L,
 {
     if (sh.rsave_tag == L.epoch_of(step, layer, kPhaseR))
         return sh.rsave[i];
-    return Num<BF16>::from_payload(poll_one(L.exchange + L.xl.r + i, L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh));
+    return Num<BF16>::from_payload(
+        poll_element<BF16>(L.exchange + L.xl.r, i, L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh));
 }
 
 // ---------------------------------------------------------------- RMSNorm (ops.cuh:145-219)
@@ -1052,7 +1119,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     // This token's Q heads, K and V of the head group: one packed exchange block.
     const int block = (group + 2) * dh;
     float* incoming = sh.region;  // [group][dh] Q, [dh] K, [dh] V
-    poll_words(L.exchange + L.xl.qkv + static_cast<size_t>(kv_head) * block, block,
+    poll_words<false>(L.exchange + L.xl.qkv + static_cast<size_t>(kv_head) * block, block,
                row_stride(s.hidden_size + 2 * kvw, L.workers), L.epoch_of(step, layer, kPhaseQKV), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { incoming[i] = N::from_payload(p); });
     block_sync(sh);
@@ -1440,11 +1507,11 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     }
 
     const uint32_t out_epoch = L.epoch_of(step, layer, kPhaseAttn);
-    uint64_t* attn = L.exchange + L.xl.attn + first_head * dh;
+    uint64_t* attn = L.exchange + L.xl.attn;
     if (fused) {
         wait_stores();  // the K row is in the cache before anyone sees this output
         if (owner)
-            publish<BF16>(attn, mine, N::round(out), out_epoch);
+            publish_element<BF16>(attn, first_head * dh + mine, N::round(out), out_epoch);
         return;
     }
     // Split context.  Every chunk but 0 publishes its partial (unnormalized FP32 P V of each
@@ -1560,7 +1627,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     }
     wait_stores();  // the K row (chunk 0 stores it) is in the cache before anyone sees this output
     if (owner)
-        publish<BF16>(attn, mine, N::round(out), out_epoch);
+        publish_element<BF16>(attn, first_head * dh + mine, N::round(out), out_epoch);
 }
 
 // Wo rows plus the residual (ops.cuh:718-734): r = round(round(Wo a) + x).
@@ -1578,7 +1645,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
     auto prepare = [&]() {
         for (int i = begin + static_cast<int>(tid()); i < end; i += kThreads)
             residual[i - begin] = input_element(L, layer, step, token, i, sh);
-        poll_input(L.exchange + L.xl.attn, d, (L.shape.query_heads / L.shape.kv_heads) * L.shape.head_dim,
+        poll_input<BF16>(L.exchange + L.xl.attn, d, (L.shape.query_heads / L.shape.kv_heads) * L.shape.head_dim,
                    L.epoch_of(step, layer, kPhaseAttn), L.exchange, L.xl, sh,
                    [&](int i, uint32_t p) {
                        sh.vec[i] = N::from_payload(p);
@@ -1594,7 +1661,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
                        [&](int row, const float* dots) {
                            const float r = N::round(N::round(dots[0]) + residual[row - begin]);
                            N::store(L.scratch, L.layout.r + row, r);
-                           publish<BF16>(L.exchange + L.xl.r, row, r, epoch);
+                           publish_element<BF16>(L.exchange + L.xl.r, row, r, epoch);
                        });
 }
 
@@ -1648,7 +1715,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     issue_fence();
 #endif
 
-    poll_input(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
+    poll_input<BF16>(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
     if (tid() == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
@@ -1888,7 +1955,7 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
                 global(L.block_trace)[static_cast<size_t>(layer) * d + row] = y;
             if (L.ffn_trace)
                 global(L.ffn_trace)[row] = projected;
-            publish<BF16>(L.exchange + L.xl.hidden((layer + 1) % 2), row, y, L.epoch_of(step, layer, kPhaseY));
+            publish_element<BF16>(L.exchange + L.xl.hidden((layer + 1) % 2), row, y, L.epoch_of(step, layer, kPhaseY));
         }
     }
 }
@@ -1908,7 +1975,7 @@ __device__ __forceinline__ void final_input(const Launch<BF16>& L, int step, Sha
 {
     const int d = L.shape.hidden_size;
     const int layers = L.stack.layers;
-    poll_input(L.exchange + L.xl.hidden(layers % 2), d, row_stride(d, L.workers), L.epoch_of(step, layers - 1, kPhaseY),
+    poll_input<BF16>(L.exchange + L.xl.hidden(layers % 2), d, row_stride(d, L.workers), L.epoch_of(step, layers - 1, kPhaseY),
                L.exchange, L.xl, sh, [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
 }
 
