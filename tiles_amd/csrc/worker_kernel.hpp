@@ -468,6 +468,71 @@ __device__ __forceinline__ void poll_input(const uint64_t* src, int count, int s
     block_sync(sh);
 }
 
+// A vector exchange read by the calling wave alone (poll_words's optimistic read, witness wait
+// and re-read, with up to kMaxElements elements), into `sink`; the caller meets the other waves
+// at a barrier afterwards.  Its loads return only after every load the wave issued before them,
+// so a wave that polls this way keeps few loads of its own in flight.
+template <bool BF16, int kMaxElements, typename Sink>
+__device__ __forceinline__ void poll_words_one_wave(const uint64_t* src, int count, int stride, uint32_t epoch,
+                                                   uint64_t* exchange, const ExchangeLayout& xl, Shared& sh, Sink sink)
+{
+    constexpr bool kHalves = BF16;
+    constexpr int kWords = kHalves ? kMaxElements / 2 : kMaxElements;
+    // Rounds of at most 16 words per lane (one round for a 2048-element bf16 vector): more would
+    // spill the registers that hold the wave's weight loads.
+    constexpr int kBatch = (kWords + 63) / 64 < 16 ? (kWords + 63) / 64 : 16;
+    const int lane = static_cast<int>(tid() & 63);
+    const int words = kHalves ? count / 2 : count;
+    const int stride_words = kHalves ? (stride > 1 ? stride / 2 : 1) : stride;
+    const uint32_t want = kHalves ? exchange_tag(epoch) : epoch;
+    for (int w0 = 0; w0 < words; w0 += 64 * kBatch) {
+        uint64_t w[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k)
+            w[k] = kHalves ? (static_cast<uint64_t>(want) << 48) | (want << 16) : static_cast<uint64_t>(want) << 32;
+        auto read = [&]() {
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int index = w0 + k * 64 + lane;
+                if (w0 + k * 64 < words)
+                    w[k] = coherent_load64(src + (index < words ? index : words - 1));
+            }
+            bool ok = true;
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k)
+                ok &= word_present<kHalves>(w[k], want);
+            return ok;
+        };
+        const bool all_present = __all(read());
+        if (lane == 0 && sh.mark_read == 0)
+            sh.mark_read = __builtin_amdgcn_s_memrealtime();
+        if (!all_present) {
+            wait_witness_words<kHalves>(src, words, stride_words, want, exchange, xl, sh);
+            uint32_t spins = 0;
+            while (!__all(read()) && !sh.aborted) {
+                __builtin_amdgcn_s_sleep(2);
+                if (lane == 0)
+                    stuck(exchange, xl, ++spins, sh);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int index = w0 + k * 64 + lane;
+            if (index < words) {
+                if constexpr (kHalves) {
+                    sink(2 * index, static_cast<uint32_t>(w[k]) & 0xffffu);
+                    sink(2 * index + 1, static_cast<uint32_t>(w[k] >> 32) & 0xffffu);
+                } else {
+                    sink(index, static_cast<uint32_t>(w[k]));
+                }
+            }
+        }
+    }
+    wait_stores();
+    if (lane == 0)
+        sh.mark_ready = __builtin_amdgcn_s_memrealtime();
+}
+
 // One exchange word, waited for by the calling thread alone.
 __device__ inline uint32_t poll_one(const uint64_t* src, uint32_t epoch, uint64_t* exchange, const ExchangeLayout& xl,
                                     Shared& sh)
@@ -1673,7 +1738,11 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
 // Wdown^T row i in one pass, so p_i multiplies the down row as soon as the group has it, and
 // every pass loads the same amount (3 x VPL 16-byte vectors per lane).  A lane owns the output
 // columns that match its input slice; waves then sum their partials through LDS.  D passes are
-// in flight, all issued before the task waits for r.
+// in flight per wave.  Waves 1-7 issue all of theirs before the task waits for r; wave 0 issues
+// one, polls r alone and issues the rest.  A wave's loads return in issue order, so polling from
+// waves with D passes queued saw r only when those passes had drained, 5-7 us after the chunk
+// began (the burst is 48 MB across the chip); wave 0 sees it about 2 us sooner (696 against 717
+// us per token at ctx 1, 812 against 834 at ctx 4096).
 template <bool BF16, int VPL>
 __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_record& t, int step, uint32_t slot0,
                                       Shared& sh)
@@ -1709,14 +1778,29 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
         }
     };
     u32x4 w[D][NV];
+    // Waves 1-7 wait for their earlier stores (V cache rows of a QKV task) before their loads, as
+    // the block-wide poll does after its reads, so that every later publish follows those stores.
+    if (g.wave == 0) {
+        issue(0, w[0]);
+        issue_fence();
+        poll_words_one_wave<BF16, kOut * 64>(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR),
+                                             L.exchange, L.xl, sh,
+                                             [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
 #pragma unroll
-    for (int s = 0; s < D; ++s)
-        issue(s, w[s]);
+        for (int s = 1; s < D; ++s)
+            issue(s, w[s]);
+    } else {
+        wait_stores();
+#pragma unroll
+        for (int s = 0; s < D; ++s)
+            issue(s, w[s]);
+    }
     issue_fence();
-#endif
-
+    block_sync(sh);
+#else
     poll_input<BF16>(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
+#endif
     if (tid() == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
     const InputSlice<VPL> in = norm(sh, d, L.numeric.rms_norm_eps);
