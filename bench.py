@@ -38,7 +38,7 @@ LM_HEAD_STEP_BYTES = 525_344_768      # 128256 x 2048 bf16 LM-head rows + the hi
 PEAK_HBM_GBPS = 8000.0                # MI355X published HBM3E bandwidth
 # HBM bytes a ctx-1 generate token moves, measured with rocprofv3 FETCH_SIZE and WRITE_SIZE
 # (calibrated against a known-size read and fill), profiles/decoder_worker_llama1b_bf16_ctx1_hbm_counters.md.
-MEASURED_TRAFFIC_BYTES_PER_TOKEN = 2_693_217_496
+MEASURED_TRAFFIC_BYTES_PER_TOKEN = 2_690_412_504
 
 
 def log(*args) -> None:
