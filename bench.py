@@ -92,7 +92,7 @@ def main() -> int:
     parser.add_argument("--chunk-steps", type=int, default=130, help="attention chunk steps of the ctx-4096 package")
     parser.add_argument("--ctx32768", action="store_true",
                         help="also decode 64 tokens at context 32768 (BASELINE config 5: a second package with "
-                             "max_context 32832 and 1024-step attention chunks, the planner's largest: 33 per K/V head)")
+                             "max_context 32832 and 1026-step attention chunks: 32 per K/V head, one attention task per worker)")
     parser.add_argument("--write-package", type=Path, default=None,
                         help="only write the ctx-1 package to this directory and its prompt to DIR.ctx1.json "
                              "(for `tiles_amd/tile_runtime bench` under a profiler), then exit")
@@ -194,7 +194,7 @@ def main() -> int:
     if args.ctx32768:
         long_context = 32768 + 64
         start = time.time()
-        S.llama_package(work / "llama32k", long_context, "bfloat16", seed=0, chunk_steps=1024, target=target,
+        S.llama_package(work / "llama32k", long_context, "bfloat16", seed=0, chunk_steps=1026, target=target,
                         weights=weights)
         log(f"ctx32768 package built in {time.time() - start:.1f}s")
         model = R.DecoderModel(R.load_plan(work / "llama32k", verify_weights=False))
@@ -209,7 +209,7 @@ def main() -> int:
         ctx32768 = {"ms_per_token": long_ms, "tokens_per_second": 1e3 / long_ms, "floor_ms_per_token": long_floor,
                     "fraction_of_floor": long_floor / long_ms,
                     "achieved_GBps": long_bytes / (result.compute_us * 1e-6) / 1e9, "prefill_tokens": 32768,
-                    "prefill_s": prefill_s, "new_tokens": 64, "attention_chunk_steps": 1024}
+                    "prefill_s": prefill_s, "new_tokens": 64, "attention_chunk_steps": 1026}
         log(f"ctx32768: {long_ms * 1e3:.1f} us/token, floor {long_floor * 1e3:.1f} us")
         del ctx, model
         gc.collect()

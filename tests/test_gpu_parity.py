@@ -158,6 +158,7 @@ def test_split_context_attention_merge(target, tmp, dtype):
     (128, 128, 128, 120),  # 64-position V^T blocks: two in one chunk
     (128, 64, 64, 200),    # 128 dims over four 50-position chunks
     (64, 1024, 1024, 2100),  # three chunks of 700 positions: five V^T blocks and many score tiles per chunk
+    (64, 1056, 1056, 2100),  # two chunks of 1050 positions, past the LDS operand area: P V packs from the FP32 scores
 ])
 def test_bf16_matrix_attention(target, tmp, head_dim, chunk_steps, fused_steps, context):
     """bf16 heads of 32-128 dims (the matrix-core attention) against the oracle: fused chunks of

@@ -22,19 +22,22 @@ inline constexpr int kMaxTaskRows = 512;            // rows of one GEMV task kep
 inline constexpr int kMaxStreamRecords = 1536;      // a worker's instruction stream cached in LDS (longer ones are read from memory)
 // Shared bytes for one attention task's scores of all its query heads, in the package's
 // element type (the planner's chunk capacity, plan_core.py:91-97).  Held as FP32 in LDS.
-inline constexpr int kAttentionSharedBytes = 8192;
+// 8448 bytes are 1056 bf16 steps for a group of 4: a 32,832-position context then splits into
+// 32 chunks per K/V head, one attention task per worker on 256 CUs (1024 steps would give 33
+// chunks, 264 tasks, and two tasks on 8 workers).
+inline constexpr int kAttentionSharedBytes = 8448;
 inline constexpr int kRegionFloats = 9216;          // >= max(kThreads * 8, attention scores, P*V reduction)
 // The streaming worker (bf16 packages of hidden size 2048): 8 compute waves and 4 streamer
 // waves per worker, LDS sized for that hidden size, and a ring of 4 KB weight-row slots.
 inline constexpr int kRingThreads = kThreads + 256;
 inline constexpr int kRingHidden = 2048;
-inline constexpr int kRingRegionFloats = 4096;     // scores of kAttentionSharedBytes, FFN reduction rounds
+inline constexpr int kRingRegionFloats = 4096;     // scores of chunks up to 1024 bf16 steps (longer: exchange worker), FFN reduction rounds
 inline constexpr int kRingStreamRecords = 320;
 inline constexpr int kRingSlots = 24;
 inline constexpr uint64_t kBufferRange = 1ull << 31;   // bytes a weight buffer resource addresses
 inline constexpr uint32_t kSpinLimit = 1u << 20;    // polls before a wait is declared stuck
 inline constexpr const char* kAbi = "tileinfer-decoder-v10";
-inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-stream-ring-v2-b512";
+inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-stream-ring-v3-b512";
 
 // Exchange phases within one (step, layer); the candidates use layer == layers.
 inline constexpr int kPhaseQKV = 0;

@@ -10,9 +10,9 @@ from pathlib import Path
 from .plan import ABI, OPCODES
 
 # The compiled gfx950 worker's constants (tiles_amd/csrc/worker_config.hpp).
-FINGERPRINT = "decoder-gfx950-wave64-exchange-stream-ring-v2-b512"
+FINGERPRINT = "decoder-gfx950-wave64-exchange-stream-ring-v3-b512"
 THREADS = 512
-ATTENTION_SHARED_BYTES = 8192
+ATTENTION_SHARED_BYTES = 8448
 
 
 def normalize(raw: dict) -> dict:
