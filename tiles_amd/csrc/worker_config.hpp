@@ -26,7 +26,10 @@ inline constexpr int kMaxStreamRecords = 1536;      // a worker's instruction st
 // 32 chunks per K/V head, one attention task per worker on 256 CUs (1024 steps would give 33
 // chunks, 264 tasks, and two tasks on 8 workers).
 inline constexpr int kAttentionSharedBytes = 8448;
-inline constexpr int kRegionFloats = 9216;          // >= max(kThreads * 8, attention scores, P*V reduction)
+// >= max(kThreads * 8, attention scores, P*V reduction).  A split chunk of the longest steps
+// also keeps its packed bf16 P*V operands here after its FP32 scores: 4 x 1056 scores, then
+// 3 parts x 4 heads x 1120 padded positions of bf16 = 10,944 floats.
+inline constexpr int kRegionFloats = 11008;
 // The streaming worker (bf16 packages of hidden size 2048): 8 compute waves and 4 streamer
 // waves per worker, LDS sized for that hidden size, and a ring of 4 KB weight-row slots.
 inline constexpr int kRingThreads = kThreads + 256;
