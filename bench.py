@@ -96,6 +96,9 @@ def main() -> int:
     parser.add_argument("--write-package", type=Path, default=None,
                         help="only write the ctx-1 package to this directory and its prompt to DIR.ctx1.json "
                              "(for `tiles_amd/tile_runtime bench` under a profiler), then exit")
+    parser.add_argument("--write-package-ctx4096", type=Path, default=None,
+                        help="only write the ctx-4096 package (max_context 4160, --chunk-steps) to this directory and "
+                             "its 4096-token prompt to DIR.ctx4096.json, then exit")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the decode worker is single-GPU); --gpus {args.gpus} is not supported",
@@ -115,6 +118,12 @@ def main() -> int:
         S.llama_package(args.write_package, ctx1_context, "bfloat16", seed=0, target=target)
         Path(f"{args.write_package}.ctx1.json").write_text(json.dumps({"tokens": [S.BOS]}) + "\n")
         log(f"wrote {args.write_package} and {args.write_package}.ctx1.json")
+        return 0
+    if args.write_package_ctx4096 is not None:
+        out = args.write_package_ctx4096
+        S.llama_package(out, 4096 + 64, "bfloat16", seed=0, chunk_steps=args.chunk_steps, target=target)
+        Path(f"{out}.ctx4096.json").write_text(json.dumps({"tokens": S.prompt(4096, seed=4096)}) + "\n")
+        log(f"wrote {out} and {out}.ctx4096.json")
         return 0
     stream_gbps = R.measure_stream_read(2 << 30, 3)
     log(f"measured stream read {stream_gbps:.1f} GB/s")

@@ -369,7 +369,9 @@ int main(int argc, char** argv)
         case Mode::bench: result = bench(plan, handle, c); break;
         default: throw std::runtime_error("unsupported command");
         }
-        for (const auto& [k, v] : tiles::precision_json(plan).fields())
+        // Named: a range-for over a member of a temporary would iterate a destroyed map.
+        const Json precision = tiles::precision_json(plan);
+        for (const auto& [k, v] : precision.fields())
             result.set(k, v);
         std::cout << result.dump() << std::endl;
         return 0;
