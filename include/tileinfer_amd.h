@@ -92,7 +92,11 @@ typedef struct {
 
 /* WorkerBuffers (launch.cuh:31-45) plus the exchange area this worker synchronizes
  * through.  `exchange` holds ti_exchange_words() 64-bit words, zeroed once at allocation;
- * `epoch` must grow by at least ti_epochs_per_launch() between launches on one exchange area. */
+ * `epoch` starts at 1 and grows by exactly ti_epochs_per_launch() from one launch that ran to
+ * the next on one exchange area.  A launch that returned at once (its selection status already
+ * held EOS or an error) did not run: the next launch takes the epoch it would have had.  A host
+ * that lets the epoch grow by more, or wraps it, first zeroes every exchange word except word 0
+ * and the greedy candidates (bf16 vectors carry a 16-bit tag of the epoch). */
 typedef struct {
     void* input;
     void* output;
@@ -142,6 +146,12 @@ int ti_describe_target(ti_target* out);
 /* 64-bit words of the exchange area one context needs for `shape`. */
 size_t ti_exchange_words(const ti_model_shape* shape, int32_t layers, int32_t selection_slots);
 uint32_t ti_epochs_per_launch(int32_t layers);
+/* The epoch for the next launch after a generation request whose launches used
+ * launch_epochs[0 .. launches) and which selected `generated` tokens before it stopped: the
+ * launch after the last one that ran (the stop the reference resolves in sequence_context.cu:84-99),
+ * or `current` when all ran or the epoch wrapped after the stop.  No device access. */
+uint32_t ti_epoch_after_generation(uint32_t current, const uint32_t* launch_epochs, int32_t launches,
+                                   int32_t generated, int32_t layers);
 
 /* detail::enqueue_worker (launch.cuh:87-88, worker_kernel.cu:240-249): one cooperative launch
  * decoding token.steps ∈ [1, 64] consecutive positions from `position`.  `stream` is a
@@ -202,6 +212,12 @@ int ti_context_wait(ti_context* context, const ti_ticket* ticket, ti_completion*
 int ti_context_diagnostic_sizes(const ti_context* context, size_t* logits, size_t* kv, size_t* block_outputs);
 int ti_context_collect(ti_context* context, const ti_ticket* ticket, float* logits, float* kv,
                        float* block_outputs);
+/* Intermediates of a request made with block_outputs (scratch_snapshot / ffn_snapshot,
+ * diagnostic.hpp:44-46): the scratch vectors of the request's last step widened to float, laid
+ * out as plan.json's storage.scratch regions (q_rot, attention, r and product hold the last
+ * layer's values), and every layer's FFN output before the residual, [layers][hidden]. */
+int ti_context_intermediate_sizes(const ti_context* context, size_t* scratch, size_t* ffn);
+int ti_context_collect_intermediates(ti_context* context, const ti_ticket* ticket, float* scratch, float* ffn);
 /* Timeline mode (diagnostic_context.cu:257-285, main.cpp --timeline-stack): while enabled, every
  * launch stamps each instruction of its last step with the 100 MHz device clock at start, when
  * its first exchange read returned, when its inputs were complete, and at its end (0 where an

@@ -10,6 +10,7 @@ It restates, in PyTorch eager on the CPU, the reference's own decoder oracle:
 * ``apply_rope``                follows decoder_reference.py:159-171
 * ``rms_norm``                  follows decoder_reference.py:183-187
 * ``decode_one``                follows decoder_reference.py:213-270
+* ``append_kv``                 decode_one's K/V rows alone (decoder_reference.py:223-237)
 * ``recompute_prefix``          follows decoder_reference.py:273-312
 * ``final_norm``                follows tileplan/src/tileplan/decoder_stack.py:126-132
 * ``decode_token``              follows decoder_stack.py:135-155
@@ -136,18 +137,36 @@ class StackCache:
         return self.layers[0].position
 
 
-def decode_one(x: torch.Tensor, w: dict, spec: Spec, cache: Cache) -> dict:
-    """Append one token to one block (decoder_reference.py:213-270)."""
-    if cache.position >= spec.max_context:
-        raise ValueError("context capacity reached")
-    p = cache.position
+def _rotated_qkv(x: torch.Tensor, w: dict, spec: Spec, p: int):
+    """The block's normalized input projected to q, k, v, with q and k rotated for position p
+    (decoder_reference.py:223-233)."""
     u = rms_norm(x, w["attn_norm"], spec.rms_norm_eps)
     q = (w["Wq"] @ u).reshape(spec.num_attention_heads, spec.head_dim)
     k = (w["Wk"] @ u).reshape(spec.num_key_value_heads, spec.head_dim)
     v = (w["Wv"] @ u).reshape(spec.num_key_value_heads, spec.head_dim)
     position = torch.tensor(p, dtype=torch.float32)
-    q = apply_rope(q, position, spec)
-    k = apply_rope(k, position, spec)
+    return apply_rope(q, position, spec), apply_rope(k, position, spec), v
+
+
+def append_kv(x: torch.Tensor, w: dict, spec: Spec, cache: Cache) -> None:
+    """The K/V row decode_one appends for input x, without the rest of the block: the same
+    operations, so the cache holds the same bits.  A one-layer stack's cache depends on the
+    tokens alone, so this fills long prefixes of such stacks without their attention."""
+    if cache.position >= spec.max_context:
+        raise ValueError("context capacity reached")
+    p = cache.position
+    _, k, v = _rotated_qkv(x, w, spec, p)
+    cache.k[p] = k
+    cache.v[p] = v
+    cache.position = p + 1
+
+
+def decode_one(x: torch.Tensor, w: dict, spec: Spec, cache: Cache) -> dict:
+    """Append one token to one block (decoder_reference.py:213-270)."""
+    if cache.position >= spec.max_context:
+        raise ValueError("context capacity reached")
+    p = cache.position
+    q, k, v = _rotated_qkv(x, w, spec, p)
     cache.k[p] = k
     cache.v[p] = v
     keys = cache.k[: p + 1, spec.head_to_kv]

@@ -8,9 +8,8 @@ kernel_regression.py:111-297, decoder_regression.py:41-220):
 * a small stack with a long context and 16-step attention chunks: the split-context merge
   path (several chunks per head) vs the oracle, fp32 within 1e-4 relative.
 * random-init Llama-3.2-1B: fp32 per-step logits within 1e-4 relative (the north-star fp32
-  bar); bf16 within the measured noise floor of two valid eager orderings of the same bf16
-  computation (0.078 absolute at most on these logits), greedy tokens equal wherever the
-  oracle's top-2 gap exceeds that floor.
+  bar); bf16 over BASELINE config 3 (256 tokens, 4 launches) within the reference's calibration
+  rule: 1.25 x the drift between the oracle and the bf16 contract evaluated exactly.
 * generation semantics: multi-launch, EOS, capacity, vocabulary and non-finite-logit errors.
 """
 
@@ -23,6 +22,7 @@ import pytest
 import torch
 
 from oracle import decoder as ref
+from tests import contract64 as C64
 from tiles_amd import runtime as R
 from tiles_amd import synthetic as S
 from tiles_amd.tileplan import package as K
@@ -31,10 +31,6 @@ from tiles_amd.tileplan import probe
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).parent / "golden"
-# bf16 Llama-3.2-1B: two valid eager orderings of the oracle (bf16 GEMV vs FP32-accumulated GEMV
-# rounded once) differ by up to 0.078 in a logit (measured, seed 0); the worker must stay within
-# twice that, and agree on the greedy token wherever the oracle's top-2 gap exceeds it.
-BF16_1B_NOISE_FLOOR = 0.08
 
 
 @pytest.fixture(scope="module")
@@ -143,14 +139,34 @@ def test_split_context_attention_merge(target, tmp, dtype):
     if dtype == "float32":
         np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
     else:
-        # flash-style merge keeps unrounded chunk probabilities: bf16 logits differ by rounding only
-        assert np.abs(got - want).max() <= 0.1
-        assert int(got.argmax()) == int(want.argmax()) or np.sort(want)[-1] - np.sort(want)[-2] < 0.1
+        # The chunks merge their softmax statistics first and round P = exp(s - M) / S once, as
+        # eager attention does: the bf16 logits differ from the oracle's as far as two correct
+        # evaluations of the contract do (calibrated_bound).
+        check_bf16_logits(got, want, exact_logits(packed, ospec, tokens))
+
+
+def exact_logits(weights, ospec, tokens):
+    """The last token's logits under the bf16 contract evaluated exactly (tests/contract64.py)."""
+    contract = C64.Contract(weights, ospec)
+    for t in tokens:
+        exact = contract.decode_token(t)["logits"]
+    return exact
+
+
+def check_bf16_logits(got, want, exact, floor=2e-2):
+    """The worker's bf16 logits against the oracle's, bounded by the reference's calibration rule:
+    max(floor, 1.25 x the oracle's drift from the exact contract); the greedy token must be the
+    oracle's wherever its top-2 gap exceeds that bound."""
+    bound = C64.calibrated_bound(float(np.abs(exact - want).max()), floor)
+    err = np.abs(got - want)
+    assert err.max() <= bound, (err.max(), bound)
+    top2 = np.sort(want)[-2:]
+    assert int(got.argmax()) == int(want.argmax()) or top2[1] - top2[0] <= bound
 
 
 @pytest.mark.parametrize("head_dim,chunk_steps,fused_steps,context", [
     (64, 128, 128, 101),   # one fused chunk inside one V^T block
-    (64, 128, 128, 300),   # three chunks of 100 positions: unnormalized probabilities, merged
+    (64, 128, 128, 300),   # three chunks of 100 positions: statistics merged, then probabilities
     (64, 130, 130, 130),   # a second tile for waves 0 and 1 (ten tiles in one block)
     (64, 160, 160, 300),   # two chunks of 150 positions
     (64, 256, 256, 250),   # one fused chunk over two V^T blocks and three rounds of score tiles
@@ -158,11 +174,12 @@ def test_split_context_attention_merge(target, tmp, dtype):
     (128, 128, 128, 120),  # 64-position V^T blocks: two in one chunk
     (128, 64, 64, 200),    # 128 dims over four 50-position chunks
     (64, 1024, 1024, 2100),  # three chunks of 700 positions: five V^T blocks and many score tiles per chunk
-    (64, 1056, 1056, 2100),  # two chunks of 1050 positions, past the LDS operand area: P V packs from the FP32 scores
+    (64, 1056, 1056, 2100),  # two chunks of 1050 positions: the longest chunk the worker takes
 ])
 def test_bf16_matrix_attention(target, tmp, head_dim, chunk_steps, fused_steps, context):
     """bf16 heads of 32-128 dims (the matrix-core attention) against the oracle: fused chunks of
-    up to 256 positions and split chunks, logits within bf16 rounding and the same greedy token."""
+    up to 256 positions and split chunks, logits within the calibrated bf16 bound and the same
+    greedy token."""
     block = P.BlockSpec(hidden_size=4 * head_dim, intermediate_size=512, num_attention_heads=4, num_key_value_heads=1,
                         head_dim=head_dim, max_context=max(320, context + 8))
     spec = P.StackSpec(block, 2, 512, True)
@@ -179,15 +196,9 @@ def test_bf16_matrix_attention(target, tmp, head_dim, chunk_steps, fused_steps, 
     with torch.inference_mode():
         for t in tokens:
             want = ref.decode_token(t, packed, ospec, cache)["logits"].float().numpy()
-    # Bounds from the vector-path attention on the same cases (measured): fused chunks differ from
-    # the oracle by bf16 rounding of the logits (<= 0.031); split chunks keep unrounded chunk
-    # probabilities in the merge, as the reference does, and differ by up to 0.113 (mean 0.028).
-    err = np.abs(got - want)
-    if context <= fused_steps:
-        assert err.max() <= 0.04, err.max()
-    else:
-        assert err.max() <= 0.15 and err.mean() <= 0.035, (err.max(), err.mean())
-    assert int(got.argmax()) == int(want.argmax()) or np.sort(want)[-1] - np.sort(want)[-2] < 0.1
+    # Fused and split chunks alike round the probabilities once with the whole context's
+    # statistics (ops.cuh:612-623, 636-668).
+    check_bf16_logits(got, want, exact_logits(packed, ospec, tokens))
 
 
 def test_generation_semantics(target, tmp):
@@ -279,21 +290,45 @@ def test_llama_fp32_logits_within_1e4_relative(target, tmp, llama_weights):
 
 
 @pytest.mark.slow
-def test_llama_bf16_tokens_and_logits(target, tmp, llama_weights):
-    S.llama_package(tmp / "l1b_bf16", 64, "bfloat16", target=target, weights=llama_weights, chunk_steps=64)
+def test_llama_bf16_config3_generation(target, tmp, llama_weights):
+    """BASELINE config 3 on the random-init Llama-3.2-1B: a 1-token prompt, then 256 greedy
+    tokens in one generate request (4 launches of 64 steps).  The oracle is forced along the
+    worker's tokens and every step's logits are compared.  The bound follows the reference's
+    calibration rule (bf16_checkpoint_tolerances.json): max(2e-2, 1.25 x the drift between the
+    oracle and the bf16 contract evaluated exactly, tests/contract64.py), measured here on the
+    first 16 steps; the RMS error stays within twice the drift's, and the greedy token must be
+    the oracle's wherever its top-2 gap exceeds the bound."""
+    new_tokens = 256
+    S.llama_package(tmp / "l1b_bf16", new_tokens + 8, "bfloat16", target=target, weights=llama_weights)
     _, ctx = context_for(tmp / "l1b_bf16")
     ctx.wait(ctx.enqueue_prefill([S.BOS]))
-    generated = ctx.wait(ctx.enqueue_generate(8)).generated
-    ospec = llama_oracle_spec(64)
-    oracle = ref.generate([S.BOS], 8, llama_weights, ospec, torch.bfloat16, forced=generated)
+    generated = ctx.wait(ctx.enqueue_generate(new_tokens)).generated
+    assert len(generated) == new_tokens
+    ospec = llama_oracle_spec(new_tokens + 8)
+    oracle = ref.generate([S.BOS], new_tokens, llama_weights, ospec, torch.bfloat16, forced=generated)
+    contract = C64.Contract(llama_weights, ospec)
+    drift = []
+    for token in [S.BOS] + generated[:15]:
+        exact = contract.decode_token(token)["logits"]
+        drift.append(np.abs(exact - oracle["logits"][len(drift)].double().numpy()))
+    drift = np.stack(drift)
+    bound = C64.calibrated_bound(float(drift.max()))
     ctx.wait(ctx.enqueue_reset())
+    errors, compared = [], 0
     for step, token in enumerate([S.BOS] + generated[:-1]):
         got = ctx.collect(ctx.enqueue_decode(token, logits=True))["logits"]
         want = oracle["logits"][step].numpy()
-        assert np.abs(got - want).max() <= 2 * BF16_1B_NOISE_FLOOR
+        errors.append(np.abs(got - want))
         top2 = np.sort(want)[-2:]
-        if top2[1] - top2[0] > BF16_1B_NOISE_FLOOR:
-            assert generated[step] == oracle["tokens"][step]
+        if top2[1] - top2[0] > bound:
+            assert generated[step] == oracle["tokens"][step], step
+            compared += 1
+    errors = np.stack(errors)
+    print(f"config 3: max error {errors.max():.4f} (bound {bound}, drift {drift.max():.4f}), RMS "
+          f"{np.sqrt((errors ** 2).mean()):.5f} vs drift {np.sqrt((drift ** 2).mean()):.5f}, within 2e-2: "
+          f"{(errors <= 2e-2).mean():.4f}, tokens compared {compared}/{new_tokens}", flush=True)
+    assert errors.max() <= bound
+    assert np.sqrt((errors ** 2).mean()) <= 2 * np.sqrt((drift ** 2).mean()) + 1e-4
 
 
 @pytest.mark.slow
@@ -303,10 +338,9 @@ def test_isolated_lm_head_step_token(target, tmp):
 
     Built as a one-layer stack whose layer weights are all zero, so the layer hands its input
     on unchanged (attention and FFN outputs are exactly 0, y = x in bf16), and whose embedding
-    rows 0-2 hold three seeded h vectors.  The token must equal the oracle's whenever the
-    oracle's top-2 gap exceeds one bf16 rounding of the top logit; the logits must agree within
-    one bf16 rounding (the GPU and PyTorch CPU accumulate the 2048-term dots in different
-    orders, and every logit is rounded to bf16)."""
+    rows 0-2 hold three seeded h vectors.  The token must equal the oracle's for every vector;
+    the logits must agree within one bf16 rounding (the GPU and PyTorch CPU accumulate the
+    2048-term dots in different orders, and every logit is rounded to bf16)."""
     block = P.BlockSpec(hidden_size=2048, intermediate_size=8192, num_attention_heads=32, num_key_value_heads=8,
                         head_dim=64, max_context=8)
     spec = P.StackSpec(block, 1, 128256, False)
@@ -332,6 +366,6 @@ def test_isolated_lm_head_step_token(target, tmp):
         want = out["logits"].float().numpy()
         rounding = np.abs(want) * 2.0 ** -8 + 1e-6  # half a bf16 ulp of each logit
         assert np.all(np.abs(got - want) <= 2 * rounding), np.abs(got - want).max()
+        # the token id matches bit-exactly (ties to the lowest id).
         top2 = np.sort(want)[-2:]
-        if top2[1] - top2[0] > 2.0 ** -7 * abs(top2[1]):
-            assert int(got.argmax()) == int(want.argmax()), (token, int(got.argmax()), int(want.argmax()))
+        assert int(got.argmax()) == int(want.argmax()), (token, int(got.argmax()), int(want.argmax()), top2)

@@ -174,3 +174,113 @@ def test_greedy_lowest_index_tie():
     logits = torch.tensor([0.5, 2.0, 2.0, -1.0])
     assert ref.greedy(logits) == 1
     assert ref.greedy(torch.zeros(48)) == 0
+
+
+# ---- the oracle's bf16 path against the contract evaluated exactly (tests/contract64.py) ----
+
+from tests import contract64 as C64  # noqa: E402
+
+
+def test_exact_bf16_rounding_routine():
+    """contract64.bf16 rounds float64 directly to bf16: equal to the float32 routine on float32
+    values (ties to even, signs, subnormals), and free of double rounding."""
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(10000).astype(np.float32) * 10.0 ** rng.integers(-40, 30, 10000),
+                        np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -(1.0 + 2.0 ** -8), 2.0 ** -130, 0.0],
+                                 dtype=np.float32)]).astype(np.float32)
+    assert np.array_equal(C64.bf16(x.astype(np.float64)), bf16_round(x).astype(np.float64))
+    # 1 + 2^-8 + 2^-30 lies above the tie: exact rounding goes up, float32 first would tie to even
+    assert C64.bf16(1.0 + 2.0 ** -8 + 2.0 ** -30) == 1.0 + 2.0 ** -7
+    assert C64.bf16(1.0 + 2.0 ** -8) == 1.0
+
+
+def ulp_distance(got: np.ndarray, want: np.ndarray) -> np.ndarray:
+    """|got - want| in bf16 spacings of |want| (spacing 2^-133 at zero)."""
+    _, exponent = np.frexp(want)
+    return np.abs(got - want) / np.ldexp(1.0, np.maximum(exponent, -125) - 8)
+
+
+def bf16_weights(weights: dict) -> dict:
+    return {k: v.to(torch.bfloat16) for k, v in weights.items()}
+
+
+FIELDS = ("q", "k", "v", "attention", "attn_residual", "ffn", "y")
+
+
+def compare_block(out: dict, exact: dict, counts: dict) -> None:
+    for name in FIELDS:
+        got = out[name].double().numpy().reshape(-1)
+        want = exact[name].reshape(-1)
+        distance = ulp_distance(got, want)
+        counts.setdefault(name, []).append(distance)
+
+
+def test_m1_bf16_block_within_one_ulp_of_exact_contract():
+    """The oracle's bf16 decode_one at the m1 shape (every fixture input, split attention over up
+    to six positions) against the exact contract: every intermediate within one bf16 spacing, and
+    at least 97% of elements identical."""
+    spec, _ = load_spec("decoder_m1")
+    weights = bf16_weights(load_npz(GOLDEN / "decoder_m1" / "weights.npz"))
+    cases = load_npz(GOLDEN / "decoder_m1" / "reference_cases.npz")
+    cache = ref.Cache.empty(spec, torch.bfloat16)
+    contract = C64.Contract({f"L0.{k}": v for k, v in weights.items()}, spec)
+    counts: dict = {}
+    with torch.inference_mode():
+        for step, x in enumerate(cases["x"].to(torch.bfloat16)):
+            out = ref.decode_one(x, weights, spec, cache)
+            exact = contract.block(C64.as64(x), 0, step)
+            compare_block(out, exact, counts)
+    for name, distances in counts.items():
+        d = np.concatenate(distances)
+        assert d.max() <= 1.0, (name, d.max())
+        assert (d == 0).mean() >= 0.97, (name, (d == 0).mean())
+
+
+def test_m4_bf16_stack_within_one_ulp_of_exact_contract():
+    spec, _ = load_spec("decoder_m4")
+    weights = bf16_weights(load_npz(GOLDEN / "decoder_m4" / "weights.npz"))
+    cases = load_npz(GOLDEN / "decoder_m4" / "reference_cases.npz")
+    cache = ref.StackCache.empty(spec, torch.bfloat16)
+    contract = C64.Contract(weights, spec)
+    logits, counts = [], {}
+    with torch.inference_mode():
+        for token in cases["token_ids"].tolist():
+            out = ref.decode_token(token, weights, spec, cache, keep_blocks=True)
+            exact = contract.decode_token(token, keep_blocks=True)
+            for block, exact_block in zip(out["blocks"], exact["blocks"]):
+                compare_block(block, exact_block, counts)
+            logits.append(ulp_distance(out["logits"].double().numpy(), exact["logits"]))
+    for name, distances in [*counts.items(), ("logits", logits)]:
+        d = np.concatenate(distances)
+        assert d.max() <= 1.0, (name, d.max())
+        assert (d == 0).mean() >= 0.97, (name, (d == 0).mean())
+
+
+def test_exact_contract_detects_a_dropped_rounding(monkeypatch):
+    """The comparison above has teeth: the contract with the attention probabilities left
+    unrounded (a plausible slip) drifts beyond one spacing from the oracle."""
+    spec, _ = load_spec("decoder_m4")
+    weights = bf16_weights(load_npz(GOLDEN / "decoder_m4" / "weights.npz"))
+    cases = load_npz(GOLDEN / "decoder_m4" / "reference_cases.npz")
+    cache = ref.StackCache.empty(spec, torch.bfloat16)
+    contract = C64.Contract(weights, spec)
+    original = C64.bf16
+    calls = {"n": 0}
+
+    def skip_probability_rounding(x):
+        calls["n"] += 1
+        values = np.asarray(x, dtype=np.float64)
+        # the probabilities are the only rounded [kv_heads, group, t] values whose rows sum to ~1
+        group = spec.num_attention_heads // spec.num_key_value_heads
+        if values.ndim == 3 and values.shape[:2] == (spec.num_key_value_heads, group) and np.allclose(values.sum(-1), 1.0):
+            return values
+        return original(x)
+
+    monkeypatch.setattr(C64, "bf16", skip_probability_rounding)
+    worst = 0.0
+    with torch.inference_mode():
+        for token in cases["token_ids"].tolist():
+            out = ref.decode_token(token, weights, spec, cache, keep_blocks=True)
+            exact = contract.decode_token(token, keep_blocks=True)
+            worst = max(worst, float(ulp_distance(out["logits"].double().numpy(), exact["logits"]).max()))
+    assert calls["n"] > 0 and worst > 1.0

@@ -99,7 +99,8 @@ std::string check_shape(const ti_model_shape& s, int dtype)
     if (static_cast<long>(s.attention_chunk_steps) * group * elem > kAttentionSharedBytes ||
         static_cast<long>(s.attention_chunk_steps) * group > kRegionFloats)
         return "attention chunk exceeds the compiled worker's LDS";
-    if (static_cast<long>(s.attention_chunks) * group * 2 > kRegionFloats)
+    // A split chunk keeps its scores and every chunk's statistics in the work region at once.
+    if (static_cast<long>(s.attention_chunk_steps) * group + 8 + static_cast<long>(s.attention_chunks) * group * 2 > kRegionFloats)
         return "attention chunk count exceeds the compiled worker's merge capacity";
     if (s.intermediate_size % 2 != 0)
         return "odd intermediate size";
@@ -155,6 +156,24 @@ extern "C" size_t ti_exchange_words(const ti_model_shape* shape, int32_t layers,
 }
 
 extern "C" uint32_t ti_epochs_per_launch(int32_t layers) { return TI_MAX_LAUNCH_STEPS * tiles::epochs_per_step(layers); }
+
+extern "C" uint32_t ti_epoch_after_generation(uint32_t current, const uint32_t* launch_epochs, int32_t launches,
+                                              int32_t generated, int32_t layers)
+{
+    if (!launch_epochs || launches <= 0)
+        return current;
+    // The launch that selected the last generated token ran; every later one returned at once.
+    const int used = generated > 0 ? (generated + TI_MAX_LAUNCH_STEPS - 1) / TI_MAX_LAUNCH_STEPS : 1;
+    if (used >= launches)
+        return current;
+    const uint32_t step = ti_epochs_per_launch(layers);
+    for (int i = used - 1; i + 1 < launches; ++i)
+        if (launch_epochs[i + 1] != launch_epochs[i] + step)
+            return current;  // wrapped after the stop: the wrap cleared every polled word
+    if (current != launch_epochs[launches - 1] + step)
+        return current;
+    return launch_epochs[used - 1] + step;
+}
 
 extern "C" int ti_describe_target(ti_target* out)
 {

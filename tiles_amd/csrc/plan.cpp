@@ -488,11 +488,19 @@ void validate_program(const Json& document, LoadedPlan& out)
         for (int worker = 0; worker < workers; ++worker) {
             const Json& lane = entry.at("workers")[static_cast<size_t>(worker)];
             require(lane.is_array(), "invalid worker task list");
+            // The chunks of one K/V head exchange their softmax statistics and wait for each
+            // other, so a worker may run at most one chunk of a head in an attention wave.
+            std::vector<uint32_t> heads;
             for (const auto& item : lane.items()) {
                 const int id = index_in(item, count);
                 const auto& t = tasks[static_cast<size_t>(id)];
                 require(!seen[static_cast<size_t>(id)] && t.wave == w && t.worker == worker,
                         "task is duplicated or assigned to a different wave/worker");
+                if (t.record.opcode == TI_OP_ATTENTION_SCORES) {
+                    require(std::find(heads.begin(), heads.end(), t.record.kv_head) == heads.end(),
+                            "two attention chunks of one K/V head share a worker");
+                    heads.push_back(t.record.kv_head);
+                }
                 seen[static_cast<size_t>(id)] = 1;
                 loads[static_cast<size_t>(worker)] += t.work;
                 streams[static_cast<size_t>(worker)].push_back(t.record);

@@ -144,7 +144,9 @@ struct Ticket {
     int start_position = 0, requested = 0;
     std::unique_ptr<PinnedBuffer> output, status, control;
     hipEvent_t compute_start = nullptr, compute_end = nullptr;
-    std::unique_ptr<PinnedBuffer> logits, kv, blocks;
+    std::unique_ptr<PinnedBuffer> logits, kv, blocks, ffn, scratch;
+    std::vector<uint32_t> launch_epochs;  // generation: the exchange epoch of each launch, in order
+    bool settled = false;                 // generation: the context's epoch has followed its stop
 
     explicit Ticket(Kind k) : kind(k) { check(hipEventCreateWithFlags(&event, hipEventDisableTiming), "ticket event"); }
     ~Ticket()
@@ -162,7 +164,7 @@ struct Context {
     std::shared_ptr<UploadedModel> model;
     hipStream_t stream = nullptr;
     DeviceBuffer input, output, scratch, kv, attention_scores, partials, logits, candidates, exchange, tokens, generated, status;
-    DeviceBuffer block_trace;
+    DeviceBuffer block_trace, ffn_trace;
     DeviceBuffer timeline;
     bool timeline_enabled = false;
     size_t instruction_count = 0;
@@ -223,6 +225,7 @@ struct Context {
         try {
             check(hipEventSynchronize(t->event), "wait for pending generation");
             queued_position = generation_end(*t);
+            settle_epoch(*t);
         } catch (...) {
             valid = false;
             throw;
@@ -253,6 +256,21 @@ struct Context {
         return t.start_position + count;
     }
 
+    // After a generation that stopped early (EOS), the launches after the one that stopped
+    // returned at once and wrote nothing, yet the epoch advanced past each of them.  The bf16
+    // vector exchanges carry a 16-bit tag of the epoch, which tells apart only epochs less than
+    // 65535 apart, so the next launch must follow the last one that ran by exactly one launch's
+    // epochs: the epoch goes back there.  If the epoch wrapped after that launch, the wrap cleared
+    // every word a later launch polls, and the current epoch stands.
+    void settle_epoch(Ticket& t)
+    {
+        if (t.settled || !t.generation || t.launch_epochs.empty())
+            return;
+        t.settled = true;
+        epoch = ti_epoch_after_generation(epoch, t.launch_epochs.data(), static_cast<int32_t>(t.launch_epochs.size()),
+                                          t.status->as<int32_t>()[TI_STATUS_COUNT], model->meta.stack.layers);
+    }
+
     void validate_token(ti_token_id id) const
     {
         if (id < 0 || id >= model->meta.stack.vocab_size)
@@ -274,6 +292,7 @@ struct Context {
         b.kv = kv.ptr;
         b.logits = logits.as<float>();
         b.block_trace = trace ? block_trace.as<float>() : nullptr;
+        b.ffn_trace = trace ? ffn_trace.as<float>() : nullptr;
         b.attention_scores = attention_scores.ptr;
         b.attention_partials = partials.as<float>();
         b.selection = candidates.as<ti_candidate>();
@@ -286,24 +305,38 @@ struct Context {
     {
         const uint32_t step = ti_epochs_per_launch(model->meta.stack.layers);
         if (epoch > 0xffffffffu - 2 * step) {
-            // Wrap: no old word may carry a future epoch.
-            check(hipMemsetAsync(exchange.ptr, 0, exchange.bytes, stream), "clear exchange");
+            // Wrap: no old word may carry a future epoch.  Every word is cleared but the control
+            // word (a timeout raised by the last launch is still to be reported) and the greedy
+            // candidates, which the next launch's first step reads whatever their epoch.
+            const ExchangeLayout xl = exchange_layout(model->meta.shape, model->meta.stack.layers, model->meta.selection_slots);
+            const size_t keep_end = xl.candidates + 2 * static_cast<size_t>(std::max(1, model->meta.selection_slots));
+            char* base = exchange.as<char>();
+            check(hipMemsetAsync(base + sizeof(uint64_t), 0, (xl.candidates - 1) * sizeof(uint64_t), stream), "clear exchange");
+            check(hipMemsetAsync(base + keep_end * sizeof(uint64_t), 0, (model->exchange_words - keep_end) * sizeof(uint64_t), stream),
+                  "clear exchange");
             epoch = 1;
         } else {
             epoch += step;
         }
     }
 
-    // Decodes `steps` positions from `position` in launches of at most 64 steps.
-    void launch(int position, const ti_token_id* ids, int steps, bool trace, ti_selection selection)
+    // Decodes `steps` positions from `position` in launches of at most 64 steps; `epochs`, when
+    // given, receives each launch's exchange epoch.
+    void launch(int position, const ti_token_id* ids, int steps, bool trace, ti_selection selection,
+                std::vector<uint32_t>* epochs = nullptr)
     {
-        if (trace && !block_trace.ptr)
-            block_trace = DeviceBuffer(static_cast<size_t>(model->meta.stack.layers) * model->meta.shape.hidden_size * sizeof(float));
+        if (trace && !block_trace.ptr) {
+            const size_t bytes = static_cast<size_t>(model->meta.stack.layers) * model->meta.shape.hidden_size * sizeof(float);
+            block_trace = DeviceBuffer(bytes);
+            ffn_trace = DeviceBuffer(bytes);
+        }
         for (int first = 0; first < steps; first += TI_MAX_LAUNCH_STEPS) {
             const int count = std::min(TI_MAX_LAUNCH_STEPS, steps - first);
             selection.first = first;
             ti_worker_buffers b = worker_buffers(trace);
             b.epoch = epoch;
+            if (epochs)
+                epochs->push_back(epoch);
             ti_token_input token{-1, ids ? ids + first : nullptr, count};
             check_ti(ti_enqueue_worker(stream, &model->view, &b, position + first, token, selection));
             advance_epoch();
@@ -367,6 +400,16 @@ struct Context {
         if (request.block_outputs && block_trace.ptr) {
             t->blocks = std::make_unique<PinnedBuffer>(block_trace.bytes);
             check(hipMemcpyAsync(t->blocks->ptr, block_trace.ptr, block_trace.bytes, hipMemcpyDeviceToHost, stream), "copy blocks");
+            // Intermediates of the last step (diagnostic.hpp:44-46): the scratch vectors widened
+            // to float, and each layer's FFN output before the residual.
+            t->ffn = std::make_unique<PinnedBuffer>(ffn_trace.bytes);
+            check(hipMemcpyAsync(t->ffn->ptr, ffn_trace.ptr, ffn_trace.bytes, hipMemcpyDeviceToHost, stream), "copy FFN trace");
+            const size_t count = p.scratch_bytes / model->elem();
+            t->scratch = std::make_unique<PinnedBuffer>(count * sizeof(float));
+            DeviceBuffer wide(count * sizeof(float));
+            check_ti(ti_enqueue_widen(stream, scratch.ptr, p.weight_dtype, count, wide.as<float>()));
+            check(hipMemcpyAsync(t->scratch->ptr, wide.ptr, count * sizeof(float), hipMemcpyDeviceToHost, stream), "copy scratch");
+            check(hipStreamSynchronize(stream), "scratch snapshot");
         }
         check(hipEventRecord(t->event, stream), "record ticket");
         t->owner = this;
@@ -425,7 +468,7 @@ struct Context {
             check(hipMemsetAsync(generated.ptr, 0xff, static_cast<size_t>(max_new) * sizeof(ti_token_id), stream), "reset generated tokens");
             check(hipEventRecord(t->compute_start, stream), "timing event");
             ti_selection sel{generated.as<ti_token_id>(), status.as<int32_t>(), 0, eos >= 0 ? eos : -1};
-            launch(t->start_position, nullptr, max_new, diag.block_outputs != 0, sel);
+            launch(t->start_position, nullptr, max_new, diag.block_outputs != 0, sel, &t->launch_epochs);
             check(hipEventRecord(t->compute_end, stream), "timing event");
             check(hipMemcpyAsync(t->output->ptr, generated.ptr, t->output->bytes, hipMemcpyDeviceToHost, stream), "copy generated");
             check(hipMemcpyAsync(t->status->ptr, status.ptr, t->status->bytes, hipMemcpyDeviceToHost, stream), "copy status");
@@ -513,6 +556,7 @@ struct Context {
         out.stop_reason = t->status->as<int32_t>()[TI_STATUS_EOS] ? TI_STOP_EOS : TI_STOP_LIMIT;
         if (is_pending) {
             queued_position = out.position;
+            settle_epoch(*t);
             pending.reset();
         }
         return out;
@@ -693,6 +737,34 @@ extern "C" int ti_context_collect(ti_context* context, const ti_ticket* ticket, 
             std::memcpy(kv, t->kv->ptr, t->kv->bytes);
         if (block_outputs && t->blocks)
             std::memcpy(block_outputs, t->blocks->ptr, t->blocks->bytes);
+    });
+}
+
+extern "C" int ti_context_intermediate_sizes(const ti_context* context, size_t* scratch, size_t* ffn)
+{
+    if (!context)
+        return TI_ERR_INVALID_ARGUMENT;
+    const auto& m = *context->context->model;
+    if (scratch)
+        *scratch = m.meta.scratch_bytes / m.elem();
+    if (ffn)
+        *ffn = static_cast<size_t>(m.meta.stack.layers) * m.meta.shape.hidden_size;
+    return TI_OK;
+}
+
+extern "C" int ti_context_collect_intermediates(ti_context* context, const ti_ticket* ticket, float* scratch, float* ffn)
+{
+    if (!context || !ticket)
+        return TI_ERR_INVALID_ARGUMENT;
+    return guarded(TI_ERR_RUNTIME, [&] {
+        const auto& t = ticket->ticket;
+        context->context->wait(t, nullptr);
+        if (!t->scratch)
+            throw std::runtime_error("intermediates require a request with block outputs");
+        if (scratch)
+            std::memcpy(scratch, t->scratch->ptr, t->scratch->bytes);
+        if (ffn)
+            std::memcpy(ffn, t->ffn->ptr, t->ffn->bytes);
     });
 }
 

@@ -48,7 +48,8 @@ inline constexpr int kPhaseAttn = 1;
 inline constexpr int kPhaseR = 2;
 inline constexpr int kPhaseFfn = 3;
 inline constexpr int kPhaseY = 4;
-inline constexpr int kPhaseAttnPart = 5;  // attention chunk partials of a split context
+inline constexpr int kPhaseAttnPart = 5;   // attention chunk partials of a split context
+inline constexpr int kPhaseAttnStats = 6;  // attention chunk softmax statistics of a split context
 inline constexpr int kPhaseCandidate = 0;
 inline constexpr int kPhases = 8;
 

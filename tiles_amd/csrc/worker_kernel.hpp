@@ -1078,16 +1078,17 @@ __device__ inline int active_chunks(int position, const ti_model_shape& s)
 // RoPE of the group's query heads and current K; chunk 0 stores rotated K into the cache.
 // One active chunk (a prefix of at most attention_fused_steps): scores, exact softmax,
 // probabilities rounded to the storage type, P*V, published as the group's attention output.
-// Several chunks: each chunk keeps (max, sum of exp, unnormalized P*V) in FP32; the chunk
-// that finishes last (an atomic count per head group) merges all of them and publishes.
+// Several chunks: each chunk publishes its softmax statistics, merges every chunk's in chunk
+// order, rounds exp(score - M) / S to the storage type and publishes its FP32 partial P*V;
+// chunk 0 adds the partials in chunk order and publishes the group's output.  The reference
+// runs the same arithmetic as a scores wave and a values wave (ops.cuh:574-673).
 //
 // bf16 heads of 32, 64 or 128 dims compute Q K^T and P V on the matrix cores
 // (v_mfma_f32_16x16x32_bf16): a wave takes 16 positions at a time, lane l holding position
 // l % 16 and dims 8 (l / 16) .. + 7 of every 32 (one 16-byte load per 32 dims), against the
 // group's query heads padded to 16 rows.  V is transposed through LDS a block of positions at
 // a time, so P V runs the positions as the reduced dimension; waves split the head's dims 16
-// at a time.  Unnormalized FP32 probabilities of split chunks enter as the exact sum of three
-// bf16 parts.  Other shapes use the vector path: LRK lanes hold one K/V row (16 bytes each),
+// at a time.  Other shapes use the vector path: LRK lanes hold one K/V row (16 bytes each),
 // rows spread over lanes and waves, partial P V sums reduced across them.
 // Cached K/V rows never change during a token, so the first rows of the chunk, and the
 // position's RoPE angles, are loaded before the task waits for this token's Q/K/V.
@@ -1348,37 +1349,30 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     }
     block_sync(sh);
 
-    // Softmax per head, one wave each: the maximum, exp(score - max) in place and its sum;
-    // one active chunk then rounds the probabilities exp / sum to the storage type.
-    float* stat_max = sh.small;
+    // Softmax per head, one wave each (warp_softmax_statistics, ops.cuh:457-474): the chunk's
+    // maximum and its sum of exp(score - maximum), FP32.  One active chunk rounds the probabilities
+    // exp / sum to the storage type at once (ops.cuh:612-623).  Several active chunks first
+    // exchange their statistics: every chunk merges all of them in chunk order, M = max_c m_c and
+    // S = sum_c s_c exp(m_c - M), and rounds P = exp(score - M) / S to the storage type once
+    // (attention_values_group, ops.cuh:636-668), so that P V sees the probabilities eager
+    // attention rounds whatever the chunking.
+    float* stat_max = sh.small;                    // [group] this chunk's statistics
     float* stat_sum = sh.small + kMaxGroup;
+    float* merged_max = sh.small + 2 * kMaxGroup;  // [group] every chunk's, merged
+    float* merged_sum = sh.small + 3 * kMaxGroup;
     const bool fused = chunks == 1;
-    // Matrix path: the probabilities also go to LDS as the bf16 operands of P V, each head's
-    // positions contiguous and zero up to whole V^T blocks, so that one 16-byte read is a lane's
-    // 8 positions: the fused chunk's rounded probabilities, or a split chunk's exact three bf16
-    // parts (hi + mid + lo, each the next 8 significant bits).  These are the bits the matrix loop
-    // would otherwise pack from the FP32 scores.  Chunks too long for the work region keep that.
+    // Matrix path: the rounded probabilities also go to LDS as the bf16 operands of P V, each
+    // head's positions contiguous and zero up to whole V^T blocks, so that one 16-byte read is a
+    // lane's 8 positions.  Chunks too long for the work region pack them from the FP32 values.
     const int span_pad = (span + PB - 1) / PB * PB;
-    const int parts = fused ? 1 : 3;
     const int p_offset = (group * span + 7) / 8 * 8;  // floats: after the scores, 16-byte aligned
-    const bool packed_p = kMfma && (p_offset + (parts * group * span_pad + 1) / 2) <= kLdsRegionFloats;
-    uint16_t* pbits = reinterpret_cast<uint16_t*>(scores + p_offset);  // [parts][group][span_pad]
-    auto put_p = [&](int g, int i, float v) {
-        if (fused) {
-            pbits[g * span_pad + i] = static_cast<uint16_t>(__float_as_uint(v) >> 16);
-        } else {
-            const float hi = __uint_as_float(__float_as_uint(v) & 0xffff0000u);
-            const float rest = v - hi;
-            const float mid = __uint_as_float(__float_as_uint(rest) & 0xffff0000u);
-            const float lo = rest - mid;
-            pbits[g * span_pad + i] = static_cast<uint16_t>(__float_as_uint(v) >> 16);
-            pbits[(group + g) * span_pad + i] = static_cast<uint16_t>(__float_as_uint(rest) >> 16);
-            pbits[(2 * group + g) * span_pad + i] = static_cast<uint16_t>(__float_as_uint(lo) >> 16);
-        }
-    };
+    // A split chunk also keeps every chunk's statistics after the operands (2 group per chunk).
+    const int stat_floats = fused ? 0 : chunks * 2 * group;
+    const bool packed_p = kMfma && (p_offset + (group * span_pad + 1) / 2 + 3 + stat_floats) <= kLdsRegionFloats;
+    uint16_t* pbits = reinterpret_cast<uint16_t*>(scores + p_offset);  // [group][span_pad]
+    auto put_p = [&](int g, int i, float v) { pbits[g * span_pad + i] = static_cast<uint16_t>(__float_as_uint(v) >> 16); };
     if (wave < group && packed_p && span_pad <= 3 * 64) {
-        // At most one V^T block: the wave's scores stay in registers (3 per lane), read once;
-        // the same maximum, exp, sum order and rounding as below, and no FP32 write-back.
+        // At most one V^T block: the wave's scores stay in registers (3 per lane), read once.
         const float* row = scores + wave * span;
         float v[3], e[3];
 #pragma unroll
@@ -1395,12 +1389,13 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             sum += e[k];
         }
         sum = lane_value(group_sum<64>(sum), 63);
+        if (fused)
 #pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            const int i = lane + 64 * k;
-            if (i < span_pad)
-                put_p(wave, i, fused ? N::round(e[k] / sum) : e[k]);  // 0 past the span
-        }
+            for (int k = 0; k < 3; ++k) {
+                const int i = lane + 64 * k;
+                if (i < span_pad)
+                    put_p(wave, i, N::round(e[k] / sum));  // 0 past the span
+            }
         if (lane == 63) {
             stat_max[wave] = m;
             stat_sum[wave] = sum;
@@ -1414,22 +1409,22 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         float sum = 0.0f;
         for (int i = lane; i < span; i += 64) {
             const float e = expf(row[i] - m);
-            row[i] = e;
+            if (fused)
+                row[i] = e;
             sum += e;
-            if (packed_p && !fused)
-                put_p(wave, i, e);
         }
         sum = lane_value(group_sum<64>(sum), 63);
-        if (fused)
+        if (fused) {
             for (int i = lane; i < span; i += 64) {
                 const float v = N::round(row[i] / sum);
                 row[i] = v;
                 if (packed_p)
                     put_p(wave, i, v);
             }
-        if (packed_p)
-            for (int i = span + lane; i < span_pad; i += 64)
-                put_p(wave, i, 0.0f);
+            if (packed_p)
+                for (int i = span + lane; i < span_pad; i += 64)
+                    put_p(wave, i, 0.0f);
+        }
         if (lane == 63) {
             stat_max[wave] = m;
             stat_sum[wave] = sum;
@@ -1437,9 +1432,87 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     }
     block_sync(sh);
 
+    const int outputs = group * dh;
+    const int part_words = static_cast<int>(attention_part_words(s));
+    uint64_t* blocks = L.exchange + L.xl.parts + static_cast<size_t>(kv_head) * s.attention_chunks * part_words;
+    if (!fused) {
+        // This chunk's (max, sum) per head go out as epoch-tagged exchange words; every chunk of
+        // the head then reads all chunks' words, this chunk's own from LDS.  Every read of a round
+        // issues before any is looked at; a round with a word missing is read again.
+        const uint32_t stat_epoch = L.epoch_of(step, layer, kPhaseAttnStats);
+        if (tid() < 2 * group) {
+            const int g = static_cast<int>(tid()) >> 1;
+            const float value = (tid() & 1) ? stat_sum[g] : stat_max[g];
+            coherent_store64(blocks + static_cast<size_t>(chunk) * part_words + outputs + tid(),
+                             (static_cast<uint64_t>(stat_epoch) << 32) | __float_as_uint(value));
+        }
+        const int stat_words = stat_floats;  // [chunk][max, sum of each head]
+        // After the operands, or after the scores (check_shape: they fit the work region).
+        const int stats_offset = packed_p ? (p_offset + (group * span_pad + 1) / 2 + 3) / 4 * 4 : p_offset;
+        float* all_stats = scores + stats_offset;
+        constexpr int kStatBatch = 2;
+        for (int base = 0; base < stat_words; base += kStatBatch * kThreads) {  // block-uniform
+            uint64_t w[kStatBatch];
+            auto word_index = [&](int u) { return min(base + u * kThreads + static_cast<int>(tid()), stat_words - 1); };
+            auto read = [&]() {
+#pragma unroll
+                for (int u = 0; u < kStatBatch; ++u) {
+                    const int j = word_index(u), c = j / (2 * group);
+                    w[u] = coherent_load64(blocks + static_cast<size_t>(c) * part_words + outputs + (j - c * 2 * group));
+                }
+                bool ok = true;
+#pragma unroll
+                for (int u = 0; u < kStatBatch; ++u)
+                    ok &= word_index(u) / (2 * group) == chunk || static_cast<uint32_t>(w[u] >> 32) == stat_epoch;
+                return ok;
+            };
+            uint32_t spins = 0;
+            while (!block_sync_and(sh, read()) && !sh.aborted) {
+                __builtin_amdgcn_s_sleep(2);
+                if (tid() == 0)
+                    stuck(L.exchange, L.xl, ++spins, sh);
+            }
+#pragma unroll
+            for (int u = 0; u < kStatBatch; ++u) {
+                const int j = base + u * kThreads + static_cast<int>(tid());
+                if (j < stat_words) {
+                    const int c = j / (2 * group), k = j - c * 2 * group;
+                    all_stats[j] = c == chunk ? ((k & 1) ? stat_sum[k >> 1] : stat_max[k >> 1])
+                                              : __uint_as_float(static_cast<uint32_t>(w[u]));
+                }
+            }
+        }
+        block_sync(sh);
+        // The merge, one thread per head, in chunk order as the reference's values task does.
+        if (tid() < group) {
+            const int g = tid();
+            float m = -INFINITY;
+            for (int c = 0; c < chunks; ++c)
+                m = fmaxf(m, all_stats[c * 2 * group + 2 * g]);
+            float total = 0.0f;
+            for (int c = 0; c < chunks; ++c)
+                total += all_stats[c * 2 * group + 2 * g + 1] * expf(all_stats[c * 2 * group + 2 * g] - m);
+            merged_max[g] = m;
+            merged_sum[g] = total;
+        }
+        block_sync(sh);
+        if (wave < group) {
+            const float m = merged_max[wave], total = merged_sum[wave];
+            float* row = scores + wave * span;
+            for (int i = lane; i < (packed_p ? span_pad : span); i += 64) {
+                const float p = i < span ? N::round(expf(row[i] - m) / total) : 0.0f;
+                if (i < span)
+                    row[i] = p;
+                if (packed_p)
+                    put_p(wave, i, p);
+            }
+        }
+        block_sync(sh);
+    }
+
     // group * dh <= kThreads: each thread owns at most one output element.
     const int mine = tid();
-    const bool owner = mine < group * dh;
+    const bool owner = mine < outputs;
     float out = 0.0f;
     if constexpr (kMfma) {
         // Wave n < dh / 16 accumulates output dims 16 n .. 16 n + 15 of every head over the
@@ -1468,16 +1541,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 for (int q = 0; q < PB / 32; ++q) {
                     const int t0 = first + 32 * q + 8 * tk;
                     const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + (16 * n + tr) * kVtStride + 32 * q + 8 * tk);
-                    auto operand = [&](int part) {
-                        return tr < group ? *reinterpret_cast<const u32x4*>(pbits + (part * group + tr) * span_pad + t0) : zero;
-                    };
-                    if (fused) {
-                        o = mfma_16x16x32_bf16(operand(0), vb, o);
-                    } else {
-                        o = mfma_16x16x32_bf16(operand(0), vb, o);
-                        o = mfma_16x16x32_bf16(operand(1), vb, o);
-                        o = mfma_16x16x32_bf16(operand(2), vb, o);
-                    }
+                    const u32x4 pa = tr < group ? *reinterpret_cast<const u32x4*>(pbits + tr * span_pad + t0) : zero;
+                    o = mfma_16x16x32_bf16(pa, vb, o);
                 }
             } else if (n < dh / 16) {
 #pragma unroll
@@ -1488,22 +1553,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
                         p[e] = tr < group && t0 + e < span ? scores[tr * span + t0 + e] : 0.0f;
-                    if (fused) {
-                        o = mfma_16x16x32_bf16(pack8(p), vb, o);
-                    } else {
-                        // p = hi + mid + lo exactly: each part keeps the next 8 significant bits.
-                        float hi[8], mid[8], lo[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            hi[e] = __uint_as_float(__float_as_uint(p[e]) & 0xffff0000u);
-                            const float rest = p[e] - hi[e];
-                            mid[e] = __uint_as_float(__float_as_uint(rest) & 0xffff0000u);
-                            lo[e] = rest - mid[e];
-                        }
-                        o = mfma_16x16x32_bf16(pack8(hi), vb, o);
-                        o = mfma_16x16x32_bf16(pack8(mid), vb, o);
-                        o = mfma_16x16x32_bf16(pack8(lo), vb, o);
-                    }
+                    o = mfma_16x16x32_bf16(pack8(p), vb, o);  // rounded probabilities: exact
                 }
             }
         }
@@ -1579,120 +1629,63 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             publish_element<BF16>(attn, first_head * dh + mine, N::round(out), out_epoch);
         return;
     }
-    // Split context.  Every chunk but 0 publishes its partial (unnormalized FP32 P V of each
-    // head, then each head's max and sum of exp) as exchange words and is done: the words carry
-    // the epoch, so no store acknowledgement and no arrival counter stand between a chunk and
-    // the merge.  Chunk 0 merges: out = sum_c w_c P_c / S with w_c = exp(max_c - M),
-    // M = max_c max_c and S = sum_c w_c sum_c, its own chunk from registers and LDS.
-    const int outputs = group * dh;
-    const int part_words = static_cast<int>(attention_part_words(s));
+    // Split context: every chunk but 0 publishes its FP32 partial P V as exchange words and is
+    // done; chunk 0 adds all partials in chunk order (output_projection, ops.cuh:718-728), rounds
+    // the sum once and publishes the head group's output.  No arrival counter stands between a
+    // chunk and the merge: the words carry the epoch.
     const uint32_t part_epoch = L.epoch_of(step, layer, kPhaseAttnPart);
-    uint64_t* blocks = L.exchange + L.xl.parts + static_cast<size_t>(kv_head) * s.attention_chunks * part_words;
     if (chunk != 0) {
-        uint64_t* mine_block = blocks + static_cast<size_t>(chunk) * part_words;
-        const uint64_t tag = static_cast<uint64_t>(part_epoch) << 32;
         if (owner)
-            coherent_store64(mine_block + mine, tag | __float_as_uint(out));
-        if (tid() < group) {
-            coherent_store64(mine_block + outputs + 2 * tid(), tag | __float_as_uint(stat_max[tid()]));
-            coherent_store64(mine_block + outputs + 2 * tid() + 1, tag | __float_as_uint(stat_sum[tid()]));
-        }
+            coherent_store64(blocks + static_cast<size_t>(chunk) * part_words + mine,
+                             (static_cast<uint64_t>(part_epoch) << 32) | __float_as_uint(out));
         return;
     }
-    // Threads split an output's chunks `slices` ways, kBatch chunks at a time; wave g's lanes
-    // read head g's statistics (one chunk per lane) into LDS.  Every read of a round issues
-    // before any is looked at; a round with a word missing is read again (chunk 0's words come
-    // from this worker and are always present).
-    const int slices = kThreads / outputs;
-    const int o = static_cast<int>(tid()) % outputs, slice = static_cast<int>(tid()) / outputs;
-    constexpr int kBatch = 8;
-    float part[kBatch];
-    float* weight = sh.region;                      // [chunks][group]
-    float* chunk_sum = sh.region + chunks * group;  // [chunks][group]
-    auto read_round = [&](int c0, bool with_stats) {
-        // Only the words of chunks 1 .. chunks - 1 are read: a slot past the last chunk, or of
-        // chunk 0, issues no load.
-        uint64_t w[kBatch];
+    // Rounds of as many chunks' partials as the work region holds ([chunk][output] floats), each
+    // read by all threads, kMergeBatch words per thread in flight at once; then every output's
+    // owner adds its column in chunk order.
+    constexpr int kMergeBatch = 8;
+    float* merge = sh.region;
+    const int per_round = kLdsRegionFloats / outputs;
+    float total = out;  // chunk 0's own partial
+    for (int c0 = 1; c0 < chunks; c0 += per_round) {
+        const int words = min(per_round, chunks - c0) * outputs;
+        block_sync(sh);  // P V's (or the previous round's) LDS reads are done
+        for (int base = 0; base < words; base += kMergeBatch * kThreads) {  // block-uniform
+            uint64_t w[kMergeBatch];
+            auto word_index = [&](int u) { return min(base + u * kThreads + static_cast<int>(tid()), words - 1); };
+            auto read = [&]() {
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int c = c0 + slice + k * slices;
-            w[k] = c > 0 && c < chunks ? coherent_load64(blocks + static_cast<size_t>(c) * part_words + o) : 0;
-        }
-        bool ok = true;
-        if (with_stats && wave < group) {
-            for (int c = lane; c < chunks; c += 64) {
-                const uint64_t* st = blocks + static_cast<size_t>(c) * part_words + outputs + 2 * wave;
-                const uint64_t cm = c > 0 ? coherent_load64(st) : 0, cs = c > 0 ? coherent_load64(st + 1) : 0;
-                ok &= c == 0 || (static_cast<uint32_t>(cm >> 32) == part_epoch && static_cast<uint32_t>(cs >> 32) == part_epoch);
-                weight[c * group + wave] = c > 0 ? __uint_as_float(static_cast<uint32_t>(cm)) : stat_max[wave];
-                chunk_sum[c * group + wave] = c > 0 ? __uint_as_float(static_cast<uint32_t>(cs)) : stat_sum[wave];
+                for (int u = 0; u < kMergeBatch; ++u) {
+                    const int j = word_index(u), c = c0 + j / outputs;
+                    w[u] = coherent_load64(blocks + static_cast<size_t>(c) * part_words + (j - (c - c0) * outputs));
+                }
+                bool ok = true;
+#pragma unroll
+                for (int u = 0; u < kMergeBatch; ++u)
+                    ok &= static_cast<uint32_t>(w[u] >> 32) == part_epoch;
+                return ok;
+            };
+            uint32_t spins = 0;
+            while (!block_sync_and(sh, read()) && !sh.aborted) {
+                __builtin_amdgcn_s_sleep(2);
+                if (tid() == 0)
+                    stuck(L.exchange, L.xl, ++spins, sh);
+            }
+#pragma unroll
+            for (int u = 0; u < kMergeBatch; ++u) {
+                const int j = base + u * kThreads + static_cast<int>(tid());
+                if (j < words)
+                    merge[j] = __uint_as_float(static_cast<uint32_t>(w[u]));
             }
         }
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int c = c0 + slice + k * slices;
-            if (c == 0) {
-                part[k] = out;  // slice 0, thread o: the owner of output o
-            } else if (c < chunks) {
-                ok &= static_cast<uint32_t>(w[k] >> 32) == part_epoch;
-                part[k] = __uint_as_float(static_cast<uint32_t>(w[k]));
-            }
-        }
-        return ok;
-    };
-    auto read_until_present = [&](int c0, bool with_stats) {
-        uint32_t spins = 0;
-        while (!block_sync_and(sh, read_round(c0, with_stats)) && !sh.aborted) {
-            __builtin_amdgcn_s_sleep(2);
-            if (tid() == 0)
-                stuck(L.exchange, L.xl, ++spins, sh);
-        }
-    };
-    read_until_present(0, true);
-    if (wave < group) {
-        float m = -INFINITY;
-        for (int c = lane; c < chunks; c += 64)
-            m = fmaxf(m, weight[c * group + wave]);
-        m = lane_value(group_max(m, 64), 63);
-        float total = 0.0f;
-        for (int c = lane; c < chunks; c += 64) {
-            const float e = expf(weight[c * group + wave] - m);
-            weight[c * group + wave] = e;
-            total += chunk_sum[c * group + wave] * e;
-        }
-        total = group_sum<64>(total);
-        if (lane == 63)
-            sh.small[2 * kMaxGroup + wave] = total;
-    }
-    block_sync(sh);
-    const int g = o / dh;
-    float acc = 0.0f;
-    for (int c0 = 0;;) {
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int c = c0 + slice + k * slices;
-            if (c < chunks)
-                acc += part[k] * weight[c * group + g];
-        }
-        c0 += kBatch * slices;
-        if (c0 >= chunks)
-            break;
-        read_until_present(c0, false);
-    }
-    static_assert(kThreads <= (kMaxGroup + 1) * kMaxHeadDim, "merge sums exceed their LDS area");
-    float* sums = sh.rotated;  // [slices][outputs] (slices * outputs <= kThreads)
-    if (slice < slices)
-        sums[slice * outputs + o] = acc;
-    block_sync(sh);
-    if (owner) {
-        float total = 0.0f;
-        for (int j = 0; j < slices; ++j)
-            total += sums[j * outputs + mine];
-        out = total / sh.small[2 * kMaxGroup + mine / dh];
+        block_sync(sh);
+        if (owner)
+            for (int k = 0; k < words / outputs; ++k)
+                total += merge[k * outputs + mine];
     }
     wait_stores();  // the K row (chunk 0 stores it) is in the cache before anyone sees this output
     if (owner)
-        publish_element<BF16>(attn, first_head * dh + mine, N::round(out), out_epoch);
+        publish_element<BF16>(attn, first_head * dh + mine, N::round(total), out_epoch);
 }
 
 // Wo rows plus the residual (ops.cuh:718-734): r = round(round(Wo a) + x).
@@ -2038,7 +2031,7 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
             if (L.block_trace)
                 global(L.block_trace)[static_cast<size_t>(layer) * d + row] = y;
             if (L.ffn_trace)
-                global(L.ffn_trace)[row] = projected;
+                global(L.ffn_trace)[static_cast<size_t>(layer) * d + row] = projected;
             publish_element<BF16>(L.exchange + L.xl.hidden((layer + 1) % 2), row, y, L.epoch_of(step, layer, kPhaseY));
         }
     }

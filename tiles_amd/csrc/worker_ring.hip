@@ -15,8 +15,8 @@ bool ring_worker_compiled(const ti_model_shape& s, int dtype)
     const int vpl = hidden_vectors_per_lane(s.hidden_size, 2);
     const int lrk = head_vectors(s.head_dim, 2);
     const long group = s.query_heads / s.kv_heads;
-    if (static_cast<long>(s.attention_chunk_steps) * group > kRingRegionFloats ||
-        static_cast<long>(s.attention_chunks) * group * 2 > kRingRegionFloats)
+    if (static_cast<long>(s.attention_chunk_steps) * group + 8 + static_cast<long>(s.attention_chunks) * group * 2 >
+        kRingRegionFloats)
         return false;
     // An FFN chunk's products stay in LDS between its two phases.
     if (s.ffn_chunks <= 0 || (s.intermediate_size + s.ffn_chunks - 1) / s.ffn_chunks > kMaxTaskRows)

@@ -51,11 +51,12 @@ class Completion(C.Structure):
 
 STOP_REASONS = {0: "none", 1: "limit", 2: "eos"}
 EXPORTS = ("ti_error_string", "ti_last_error_message", "ti_abi", "ti_fingerprint", "ti_describe_target",
-           "ti_exchange_words", "ti_epochs_per_launch", "ti_enqueue_worker", "ti_enqueue_zero_unused_kv",
+           "ti_exchange_words", "ti_epochs_per_launch", "ti_epoch_after_generation", "ti_enqueue_worker", "ti_enqueue_zero_unused_kv",
            "ti_enqueue_widen", "ti_measure_stream_read", "ti_load_plan", "ti_load_plan_for_target", "ti_plan_free", "ti_plan_inspect_json",
            "ti_model_create", "ti_model_free", "ti_context_create", "ti_context_free", "ti_context_prefill",
            "ti_context_decode", "ti_context_generate", "ti_context_reset", "ti_context_ready", "ti_context_wait",
-           "ti_context_diagnostic_sizes", "ti_context_collect", "ti_ticket_free", "ti_context_set_timeline",
+           "ti_context_diagnostic_sizes", "ti_context_collect", "ti_context_intermediate_sizes",
+           "ti_context_collect_intermediates", "ti_ticket_free", "ti_context_set_timeline",
            "ti_context_timeline")
 
 _lib = None
@@ -78,6 +79,8 @@ def library() -> C.CDLL:
         lib.ti_exchange_words.restype = C.c_size_t
         lib.ti_epochs_per_launch.argtypes = [C.c_int32]
         lib.ti_epochs_per_launch.restype = C.c_uint32
+        lib.ti_epoch_after_generation.argtypes = [C.c_uint32, C.POINTER(C.c_uint32), C.c_int32, C.c_int32, C.c_int32]
+        lib.ti_epoch_after_generation.restype = C.c_uint32
         lib.ti_measure_stream_read.argtypes = [C.c_size_t, C.c_int32, C.POINTER(C.c_double)]
         lib.ti_load_plan.argtypes = [C.c_char_p, C.c_int32, C.POINTER(P)]
         lib.ti_load_plan_for_target.argtypes = [C.c_char_p, C.POINTER(Target), C.c_int32, C.POINTER(P)]
@@ -99,6 +102,8 @@ def library() -> C.CDLL:
         lib.ti_context_wait.argtypes = [P, P, C.POINTER(Completion), C.POINTER(token_id), C.c_size_t]
         lib.ti_context_diagnostic_sizes.argtypes = [P, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
         lib.ti_context_collect.argtypes = [P, P, C.POINTER(C.c_float), C.POINTER(C.c_float), C.POINTER(C.c_float)]
+        lib.ti_context_intermediate_sizes.argtypes = [P, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        lib.ti_context_collect_intermediates.argtypes = [P, P, C.POINTER(C.c_float), C.POINTER(C.c_float)]
         lib.ti_ticket_free.argtypes = [P]
         lib.ti_ticket_free.restype = None
         lib.ti_context_set_timeline.argtypes = [P, C.c_int32]
@@ -284,3 +289,14 @@ class SequenceContext:
         _check(library().ti_context_collect(self._handle, ticket._handle, logits.ctypes.data_as(fp),
                                             kv.ctypes.data_as(fp), blocks.ctypes.data_as(fp)))
         return {"logits": logits, "kv": kv, "block_outputs": blocks}
+
+    def collect_intermediates(self, ticket: Ticket) -> dict:
+        """Scratch vectors (widened, in plan.json's storage.scratch layout) and each layer's FFN
+        output before the residual, of a request made with block_outputs=True."""
+        scratch, ffn = C.c_size_t(), C.c_size_t()
+        _check(library().ti_context_intermediate_sizes(self._handle, C.byref(scratch), C.byref(ffn)))
+        out = {"scratch": np.zeros(scratch.value, dtype=np.float32), "ffn": np.zeros(ffn.value, dtype=np.float32)}
+        fp = C.POINTER(C.c_float)
+        _check(library().ti_context_collect_intermediates(self._handle, ticket._handle, out["scratch"].ctypes.data_as(fp),
+                                                          out["ffn"].ctypes.data_as(fp)))
+        return out
