@@ -188,6 +188,10 @@ const char* ti_plan_inspect_json(const ti_plan* plan);
 
 int ti_model_create(const ti_plan* plan, ti_model** out);
 void ti_model_free(ti_model* model);
+/* The launch-boundary view of an uploaded model (the WorkerProgramView that
+ * uploaded_plan.cu:14-48 builds): device pointers owned by the model, valid until
+ * ti_model_free.  Lets a host drive ti_enqueue_worker with buffers of its own. */
+int ti_model_program_view(const ti_model* model, ti_worker_program_view* out);
 int ti_context_create(const ti_model* model, ti_context** out);
 void ti_context_free(ti_context* context);
 

@@ -1,0 +1,87 @@
+"""The launch boundary driven by a host of its own, and one model shared by two contexts.
+
+* ``ti_enqueue_worker`` with caller-owned buffers (tests/launch_boundary.py): the model's program
+  view, PyTorch device tensors for every worker buffer, the exchange area zeroed once and the
+  epoch advanced by exactly ``ti_epochs_per_launch`` per launch, as INTEGRATION.md prescribes.
+  Its prefill and multi-launch greedy generation must give the runtime's own tokens and K/V
+  cache bit for bit (the reference's launcher contract, detail/launch.cuh:87-88).
+* two sequence contexts of one uploaded model, interleaved, each bit-identical to a context
+  that ran alone (tileinfer/tests/sequence_context_smoke.cpp:60-166).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from tests.launch_boundary import LaunchHost
+from tiles_amd import runtime as R
+from tiles_amd import synthetic as S
+from tiles_amd.tileplan import package as K
+from tiles_amd.tileplan import plan as P
+from tiles_amd.tileplan import probe
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def package(tmp_path_factory):
+    """Two layers, 16-step attention chunks (the split path from 17 positions on), bf16."""
+    spec = P.StackSpec(P.BlockSpec(hidden_size=256, intermediate_size=512, num_attention_heads=4, num_key_value_heads=1,
+                                   head_dim=64, max_context=240), 2, 512, True)
+    weights = K.random_weights(spec, seed=21, std=0.08, dtype=torch.float32)
+    path = tmp_path_factory.mktemp("boundary") / "pkg"
+    K.build_stack_package(spec, weights, probe.probe_library(), path, "bfloat16", chunk_steps=16)
+    return path
+
+
+def test_enqueue_worker_with_caller_owned_buffers(package):
+    plan = K.read_plan(package)
+    model = R.DecoderModel(R.load_plan(package))
+    prompt = S.prompt(70, seed=3, vocab=512)
+    ctx = model.create_context()
+    ctx.wait(ctx.enqueue_prefill(prompt))
+    ticket = ctx.enqueue_generate(150, kv=True)
+    want = ctx.wait(ticket).generated
+    kv_want = ctx.collect(ticket)["kv"]
+
+    host = LaunchHost(model, plan)
+    host.feed(prompt)
+    got = host.generate(150)
+    assert got == want and len(got) == 150
+    np.testing.assert_array_equal(host.kv_values(), kv_want)
+    launches = 2 + 3  # 70 prompt steps, then 150 generated
+    assert host.epoch == 1 + launches * R.library().ti_epochs_per_launch(2)
+    # a stop mid-launch: the epoch goes back to follow the launch that ran
+    eos = got[5]
+    host2 = LaunchHost(model, plan)
+    host2.feed(prompt)
+    stopped = host2.generate(150, eos=eos)
+    assert stopped == got[: got.index(eos) + 1]
+    assert host2.epoch == 1 + 3 * R.library().ti_epochs_per_launch(2)
+    more = host2.generate(3)  # continues from the stop as the runtime does
+    ctx.wait(ctx.enqueue_reset())
+    ctx.wait(ctx.enqueue_prefill(prompt))
+    ctx.wait(ctx.enqueue_generate(150, eos_id=eos))
+    assert more == ctx.wait(ctx.enqueue_generate(3)).generated
+
+
+def test_two_contexts_share_one_model(package):
+    model = R.DecoderModel(R.load_plan(package))
+    a_prompt, b_prompt = S.prompt(40, seed=5, vocab=512), S.prompt(90, seed=6, vocab=512)
+
+    def alone(prompt, count):
+        ctx = model.create_context()
+        ctx.wait(ctx.enqueue_prefill(prompt))
+        t = ctx.enqueue_generate(count, kv=True)
+        return ctx.wait(t).generated, ctx.collect(t)["kv"]
+
+    want_a, want_b = alone(a_prompt, 70), alone(b_prompt, 100)
+    a, b = model.create_context(), model.create_context()
+    a.enqueue_prefill(a_prompt)
+    b.enqueue_prefill(b_prompt)
+    ta = a.enqueue_generate(70, kv=True)
+    tb = b.enqueue_generate(100, kv=True)
+    assert b.wait(tb).generated == want_b[0]
+    assert a.wait(ta).generated == want_a[0]
+    np.testing.assert_array_equal(a.collect(ta)["kv"], want_a[1])
+    np.testing.assert_array_equal(b.collect(tb)["kv"], want_b[1])

@@ -9,6 +9,7 @@ rejected with the loader's message.
 
 import copy
 import ctypes
+import ctypes as C
 import hashlib
 import json
 import re
@@ -206,3 +207,33 @@ def test_probe_normalization():
     bad["executor"]["abi"] = "tileinfer-decoder-v9"
     with pytest.raises(ValueError, match="lacks required decoder capabilities"):
         probe.normalize(bad)
+
+
+def test_launch_records_match_the_c_layout(tmp_path):
+    """The ctypes mirrors of the launch boundary (tiles_amd/runtime.py) have the C header's field
+    offsets and sizes (a C program built with gcc from include/tileinfer_amd.h prints them)."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("no C compiler")
+    structs = {"ti_worker_program_view": R.ProgramView, "ti_worker_buffers": R.WorkerBuffers,
+               "ti_token_input": R.TokenInput, "ti_selection": R.Selection, "ti_model_shape": R.ModelShape,
+               "ti_layer_layout": R.LayerLayout, "ti_numeric_config": R.NumericConfig, "ti_stack_config": R.StackConfig,
+               "ti_worker_task_range": R.TaskRange, "ti_task_record": R.TaskRecord}
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "tileinfer_amd.h"', "int main(void) {"]
+    for name, mirror in structs.items():
+        lines.append(f'printf("{name} sizeof %zu\\n", sizeof({name}));')
+        for field, _ in mirror._fields_:
+            lines.append(f'printf("{name} {field} %zu\\n", offsetof({name}, {field}));')
+    lines.append("return 0; }")
+    (tmp_path / "layout.c").write_text("\n".join(lines))
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(tmp_path / "layout.c"), "-o", str(tmp_path / "layout")],
+                   check=True)
+    printed = subprocess.run([str(tmp_path / "layout")], check=True, capture_output=True, text=True).stdout
+    for line in printed.splitlines():
+        name, field, value = line.split()
+        mirror = structs[name]
+        expected = C.sizeof(mirror) if field == "sizeof" else getattr(mirror, field).offset
+        assert int(value) == expected, line
+

@@ -635,6 +635,14 @@ extern "C" int ti_model_create(const ti_plan* plan, ti_model** out)
 
 extern "C" void ti_model_free(ti_model* model) { delete model; }
 
+extern "C" int ti_model_program_view(const ti_model* model, ti_worker_program_view* out)
+{
+    if (!model || !out)
+        return TI_ERR_INVALID_ARGUMENT;
+    *out = model->model->view;
+    return TI_OK;
+}
+
 extern "C" int ti_context_create(const ti_model* model, ti_context** out)
 {
     if (!model || !out)

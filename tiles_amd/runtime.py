@@ -31,6 +31,51 @@ class ModelShape(C.Structure):
                                          "attention_fused_steps", "ffn_chunks")]
 
 
+class TaskRange(C.Structure):
+    _fields_ = [("begin", C.c_uint32), ("count", C.c_uint32)]
+
+
+class LayerLayout(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("q", "k", "q_rot", "attention", "r", "product", "key", "value", "attn_norm",
+                                          "Wq", "Wk", "Wv", "Wo", "ffn_norm", "Wgate", "Wup", "Wdown")]
+
+
+class NumericConfig(C.Structure):
+    _fields_ = [(n, C.c_float) for n in ("rms_norm_eps", "rope_theta", "rope_factor", "rope_low_freq_factor",
+                                         "rope_high_freq_factor", "rope_original_context")]
+
+
+class StackConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("layers", "vocab_size", "embedding_offset", "layer_weights_offset",
+                                         "layer_weight_stride", "final_norm_offset", "lm_head_offset",
+                                         "layer_kv_stride", "full_stack")]
+
+
+class ProgramView(C.Structure):
+    """ti_worker_program_view (WorkerProgramView, launch.cuh:10-23)."""
+    _fields_ = [("instructions", C.c_void_p), ("streams", C.c_void_p), ("layout", LayerLayout), ("weights", C.c_void_p),
+                ("rotary_frequencies", C.c_void_p), ("shape", ModelShape), ("workers", C.c_int32),
+                ("selection_slots", C.c_int32), ("numeric", NumericConfig), ("stack", StackConfig),
+                ("weight_dtype", C.c_int32)]
+
+
+class WorkerBuffers(C.Structure):
+    """ti_worker_buffers (WorkerBuffers, launch.cuh:31-45, plus the exchange area and its epoch)."""
+    _fields_ = [(n, C.c_void_p) for n in ("input", "output", "scratch", "kv", "logits", "block_trace",
+                                          "attention_scores", "attention_partials", "selection", "ffn_trace",
+                                          "timeline", "exchange")] + [("epoch", C.c_uint32)]
+
+
+class TokenInput(C.Structure):
+    """ti_token_input (TokenInput, launch.cuh:49-54)."""
+    _fields_ = [("immediate", token_id), ("ids", C.c_void_p), ("steps", C.c_int32)]
+
+
+class Selection(C.Structure):
+    """ti_selection (Selection, launch.cuh:79-85)."""
+    _fields_ = [("generated", C.c_void_p), ("status", C.c_void_p), ("first", C.c_int32), ("eos_id", token_id)]
+
+
 class Target(C.Structure):
     _fields_ = [("name", C.c_char * 256), ("arch", C.c_char * 64)] + [
         (n, C.c_int32) for n in ("major", "minor", "sm_count", "cooperative_launch", "active_blocks_per_sm",
@@ -51,7 +96,8 @@ class Completion(C.Structure):
 
 STOP_REASONS = {0: "none", 1: "limit", 2: "eos"}
 EXPORTS = ("ti_error_string", "ti_last_error_message", "ti_abi", "ti_fingerprint", "ti_describe_target",
-           "ti_exchange_words", "ti_epochs_per_launch", "ti_epoch_after_generation", "ti_enqueue_worker", "ti_enqueue_zero_unused_kv",
+           "ti_exchange_words", "ti_epochs_per_launch", "ti_epoch_after_generation", "ti_enqueue_worker",
+           "ti_model_program_view", "ti_enqueue_zero_unused_kv",
            "ti_enqueue_widen", "ti_measure_stream_read", "ti_load_plan", "ti_load_plan_for_target", "ti_plan_free", "ti_plan_inspect_json",
            "ti_model_create", "ti_model_free", "ti_context_create", "ti_context_free", "ti_context_prefill",
            "ti_context_decode", "ti_context_generate", "ti_context_reset", "ti_context_ready", "ti_context_wait",
@@ -81,6 +127,9 @@ def library() -> C.CDLL:
         lib.ti_epochs_per_launch.restype = C.c_uint32
         lib.ti_epoch_after_generation.argtypes = [C.c_uint32, C.POINTER(C.c_uint32), C.c_int32, C.c_int32, C.c_int32]
         lib.ti_epoch_after_generation.restype = C.c_uint32
+        lib.ti_enqueue_worker.argtypes = [C.c_void_p, C.POINTER(ProgramView), C.POINTER(WorkerBuffers), C.c_int32,
+                                          TokenInput, Selection]
+        lib.ti_model_program_view.argtypes = [P, C.POINTER(ProgramView)]
         lib.ti_measure_stream_read.argtypes = [C.c_size_t, C.c_int32, C.POINTER(C.c_double)]
         lib.ti_load_plan.argtypes = [C.c_char_p, C.c_int32, C.POINTER(P)]
         lib.ti_load_plan_for_target.argtypes = [C.c_char_p, C.POINTER(Target), C.c_int32, C.POINTER(P)]
@@ -199,6 +248,12 @@ class DecoderModel:
         _check(library().ti_model_create(plan._handle, C.byref(handle)))
         self._handle = handle
         self.plan = plan
+
+    def program_view(self) -> ProgramView:
+        """The uploaded model's launch-boundary view (device pointers owned by this model)."""
+        view = ProgramView()
+        _check(library().ti_model_program_view(self._handle, C.byref(view)))
+        return view
 
     def create_context(self) -> "SequenceContext":
         return SequenceContext(self)
