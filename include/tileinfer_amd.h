@@ -159,6 +159,21 @@ uint32_t ti_epoch_after_generation(uint32_t current, const uint32_t* launch_epoc
 int ti_enqueue_worker(void* stream, const ti_worker_program_view* program, const ti_worker_buffers* buffers,
                       int32_t position, ti_token_input token, ti_selection selection);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops that forbid hipMalloc).  ti_enqueue_worker with the exchange
+ * area taken from a library-owned device array of ti_static_exchange_words() 64-bit words
+ * (16 MiB) per GPU; buffers->exchange and buffers->epoch are ignored, every other buffer is the
+ * caller's.  Each call clears that array with a fill kernel, except the greedy candidates, which
+ * carry a generation's previous step into the next launch, and runs the worker at epoch 1, so
+ * calls need no epoch bookkeeping.  A model whose exchange area is larger is rejected
+ * (TI_ERR_INVALID_ARGUMENT).  Allocates nothing.  Every call on a GPU shares its array, which
+ * keeps the last call's candidates: calls that overlap on one GPU race, so a caller serializes
+ * them (one stream, or events), and a generation follows the launches of its own prefix.
+ * `sync_timeout` (device int32, may be NULL) receives 1 when a wait of the launch gave up. */
+int ti_enqueue_worker_static(void* stream, const ti_worker_program_view* program, const ti_worker_buffers* buffers,
+                             int32_t position, ti_token_input token, ti_selection selection, int32_t* sync_timeout);
+size_t ti_static_exchange_words(void);
+
 /* detail::enqueue_zero_unused_kv (launch.cuh:92-94, snapshot.cu:8-23,38-45). */
 int ti_enqueue_zero_unused_kv(void* stream, void* kv, int32_t dtype, size_t count, int32_t layers,
                               int32_t layer_stride, int32_t width, int32_t capacity, int32_t key_offset,

@@ -1,6 +1,6 @@
 """A host of the launch boundary alone — TEST INFRASTRUCTURE ONLY.
 
-Drives ``ti_enqueue_worker`` the way a foreign host would
+Drives ``ti_enqueue_worker`` (and ``ti_enqueue_worker_static``) the way a foreign host would
 (INTEGRATION.md): the uploaded model's program view from ``ti_model_program_view``, every worker
 buffer owned by the caller (PyTorch device tensors here), the exchange area zeroed once, and the
 epoch advanced by exactly ``ti_epochs_per_launch`` from one launch to the next.  Buffer sizes come
@@ -25,9 +25,10 @@ def _ptr(t: torch.Tensor) -> int:
 
 
 class LaunchHost:
-    def __init__(self, model: R.DecoderModel, plan: dict):
+    def __init__(self, model: R.DecoderModel, plan: dict, static: bool = False):
         self.lib = R.library()
         self.view = model.program_view()
+        self.static = static
         storage, m = plan["storage"], plan["model"]
         self.elem = 2 if m["weight_dtype"] == "bfloat16" else 4
         self.hidden, self.vocab = m["hidden_size"], m.get("vocab_size", 1)
@@ -48,6 +49,7 @@ class LaunchHost:
         self.tokens = torch.zeros(self.max_context + MAX_STEPS, dtype=torch.int32, device=dev)
         self.generated = torch.full((self.max_context,), -1, dtype=torch.int32, device=dev)
         self.status = torch.zeros(3, dtype=torch.int32, device=dev)
+        self.timeout = torch.zeros(1, dtype=torch.int32, device=dev)
         self.epoch = 1
         self.position = 0
         self.stream = torch.cuda.current_stream().cuda_stream
@@ -63,7 +65,13 @@ class LaunchHost:
 
     def _launch(self, steps: int, token: R.TokenInput, selection: R.Selection) -> None:
         b = self.buffers()
-        R._check(self.lib.ti_enqueue_worker(self.stream, C.byref(self.view), C.byref(b), self.position, token, selection))
+        if self.static:
+            code = self.lib.ti_enqueue_worker_static(self.stream, C.byref(self.view), C.byref(b), self.position, token,
+                                                     selection, _ptr(self.timeout))
+        else:
+            code = self.lib.ti_enqueue_worker(self.stream, C.byref(self.view), C.byref(b), self.position, token,
+                                              selection)
+        R._check(code)
         self.epoch += self.lib.ti_epochs_per_launch(self.layers)
         self.position += steps
 
@@ -86,8 +94,9 @@ class LaunchHost:
             self._launch(steps, R.TokenInput(-1, None, steps), R.Selection(_ptr(self.generated), _ptr(self.status), first, eos))
         torch.cuda.synchronize()
         n = int(self.status[0].item())
-        array = (C.c_uint32 * len(epochs))(*epochs)
-        self.epoch = self.lib.ti_epoch_after_generation(self.epoch, array, len(epochs), n, self.layers)
+        if not self.static:
+            array = (C.c_uint32 * len(epochs))(*epochs)
+            self.epoch = self.lib.ti_epoch_after_generation(self.epoch, array, len(epochs), n, self.layers)
         self.position = start + n
         return self.generated[:n].tolist()
 

@@ -97,7 +97,7 @@ class Completion(C.Structure):
 STOP_REASONS = {0: "none", 1: "limit", 2: "eos"}
 EXPORTS = ("ti_error_string", "ti_last_error_message", "ti_abi", "ti_fingerprint", "ti_describe_target",
            "ti_exchange_words", "ti_epochs_per_launch", "ti_epoch_after_generation", "ti_enqueue_worker",
-           "ti_model_program_view", "ti_enqueue_zero_unused_kv",
+           "ti_enqueue_worker_static", "ti_static_exchange_words", "ti_model_program_view", "ti_enqueue_zero_unused_kv",
            "ti_enqueue_widen", "ti_measure_stream_read", "ti_load_plan", "ti_load_plan_for_target", "ti_plan_free", "ti_plan_inspect_json",
            "ti_model_create", "ti_model_free", "ti_context_create", "ti_context_free", "ti_context_prefill",
            "ti_context_decode", "ti_context_generate", "ti_context_reset", "ti_context_ready", "ti_context_wait",
@@ -129,6 +129,9 @@ def library() -> C.CDLL:
         lib.ti_epoch_after_generation.restype = C.c_uint32
         lib.ti_enqueue_worker.argtypes = [C.c_void_p, C.POINTER(ProgramView), C.POINTER(WorkerBuffers), C.c_int32,
                                           TokenInput, Selection]
+        lib.ti_enqueue_worker_static.argtypes = [C.c_void_p, C.POINTER(ProgramView), C.POINTER(WorkerBuffers), C.c_int32,
+                                                 TokenInput, Selection, C.c_void_p]
+        lib.ti_static_exchange_words.restype = C.c_size_t
         lib.ti_model_program_view.argtypes = [P, C.POINTER(ProgramView)]
         lib.ti_measure_stream_read.argtypes = [C.c_size_t, C.c_int32, C.POINTER(C.c_double)]
         lib.ti_load_plan.argtypes = [C.c_char_p, C.c_int32, C.POINTER(P)]
