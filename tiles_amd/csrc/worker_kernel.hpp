@@ -142,6 +142,7 @@ struct Launch {
 // shares LDS with the input vector.  A block holds the most positions (a multiple of 32, at most
 // 160) whose rows fit.
 constexpr int kVtElements = kLdsHidden * 3;
+constexpr int kMaxThreadsPadded = kThreads;  // floats of a split chunk's own partial in the work region
 constexpr int vt_block_positions(int dh)
 {
     int positions = 160;
@@ -1078,10 +1079,11 @@ __device__ inline int active_chunks(int position, const ti_model_shape& s)
 // RoPE of the group's query heads and current K; chunk 0 stores rotated K into the cache.
 // One active chunk (a prefix of at most attention_fused_steps): scores, exact softmax,
 // probabilities rounded to the storage type, P*V, published as the group's attention output.
-// Several chunks: each chunk publishes its softmax statistics, merges every chunk's in chunk
-// order, rounds exp(score - M) / S to the storage type and publishes its FP32 partial P*V;
-// chunk 0 adds the partials in chunk order and publishes the group's output.  The reference
-// runs the same arithmetic as a scores wave and a values wave (ops.cuh:574-673).
+// Several chunks: each chunk publishes its softmax statistics, merges every chunk's, rounds
+// exp(score - M) / S to the storage type and publishes its FP32 partial P*V; each chunk then
+// adds one slice of the group's outputs over all chunks' partials, in chunk order, and publishes
+// it.  The reference runs the same arithmetic as a scores wave and a values wave
+// (ops.cuh:574-673).
 //
 // bf16 heads of 32, 64 or 128 dims compute Q K^T and P V on the matrix cores
 // (v_mfma_f32_16x16x32_bf16): a wave takes 16 positions at a time, lane l holding position
@@ -1483,17 +1485,25 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             }
         }
         block_sync(sh);
-        // The merge, one thread per head, in chunk order as the reference's values task does.
-        if (tid() < group) {
-            const int g = tid();
+        // The merge, one wave per head: lane c takes chunk c's statistics, M = max_c m_c and
+        // S = sum_c s_c exp(m_c - M), summed over the lanes in a fixed tree order.  The reference's
+        // values task adds the chunks in chunk order, one thread per head (ops.cuh:644-656); that
+        // order is an FP32 summation order, not a rounding point of the contract, and a serial
+        // chain here cost 1 us per layer at ctx 4096.
+        if (wave < group) {
+            const int g = wave;
             float m = -INFINITY;
-            for (int c = 0; c < chunks; ++c)
+            for (int c = lane; c < chunks; c += 64)
                 m = fmaxf(m, all_stats[c * 2 * group + 2 * g]);
-            float total = 0.0f;
-            for (int c = 0; c < chunks; ++c)
-                total += all_stats[c * 2 * group + 2 * g + 1] * expf(all_stats[c * 2 * group + 2 * g] - m);
-            merged_max[g] = m;
-            merged_sum[g] = total;
+            m = lane_value(group_max(m, 64), 63);
+            float part = 0.0f;
+            for (int c = lane; c < chunks; c += 64)
+                part = fmaf(all_stats[c * 2 * group + 2 * g + 1], expf(all_stats[c * 2 * group + 2 * g] - m), part);
+            const float total = lane_value(group_sum<64>(part), 63);
+            if (lane == 0) {
+                merged_max[g] = m;
+                merged_sum[g] = total;
+            }
         }
         block_sync(sh);
         if (wave < group) {
@@ -1629,63 +1639,77 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             publish_element<BF16>(attn, first_head * dh + mine, N::round(out), out_epoch);
         return;
     }
-    // Split context: every chunk but 0 publishes its FP32 partial P V as exchange words and is
-    // done; chunk 0 adds all partials in chunk order (output_projection, ops.cuh:718-728), rounds
-    // the sum once and publishes the head group's output.  No arrival counter stands between a
-    // chunk and the merge: the words carry the epoch.
+    // Split context: every chunk publishes its FP32 partial P V as exchange words, then merges a
+    // slice of the group's outputs.  Output o belongs to chunk o mod chunks, which reads that
+    // output's partial from every chunk, adds them in chunk order (output_projection,
+    // ops.cuh:718-728), rounds the sum once and publishes it.  The merge's reads are spread over
+    // all the head's chunk workers (one merger reading every chunk's whole partial finished about
+    // 6 us after the other chunks at ctx 4096), and no arrival counter stands between a chunk and
+    // the merge: the words carry the epoch.
     const uint32_t part_epoch = L.epoch_of(step, layer, kPhaseAttnPart);
-    if (chunk != 0) {
-        if (owner)
-            coherent_store64(blocks + static_cast<size_t>(chunk) * part_words + mine,
-                             (static_cast<uint64_t>(part_epoch) << 32) | __float_as_uint(out));
-        return;
-    }
-    // Rounds of as many chunks' partials as the work region holds ([chunk][output] floats), each
-    // read by all threads, kMergeBatch words per thread in flight at once; then every output's
-    // owner adds its column in chunk order.
-    constexpr int kMergeBatch = 8;
-    float* merge = sh.region;
-    const int per_round = kLdsRegionFloats / outputs;
-    float total = out;  // chunk 0's own partial
-    for (int c0 = 1; c0 < chunks; c0 += per_round) {
-        const int words = min(per_round, chunks - c0) * outputs;
-        block_sync(sh);  // P V's (or the previous round's) LDS reads are done
-        for (int base = 0; base < words; base += kMergeBatch * kThreads) {  // block-uniform
-            uint64_t w[kMergeBatch];
-            auto word_index = [&](int u) { return min(base + u * kThreads + static_cast<int>(tid()), words - 1); };
-            auto read = [&]() {
-#pragma unroll
-                for (int u = 0; u < kMergeBatch; ++u) {
-                    const int j = word_index(u), c = c0 + j / outputs;
-                    w[u] = coherent_load64(blocks + static_cast<size_t>(c) * part_words + (j - (c - c0) * outputs));
-                }
-                bool ok = true;
-#pragma unroll
-                for (int u = 0; u < kMergeBatch; ++u)
-                    ok &= static_cast<uint32_t>(w[u] >> 32) == part_epoch;
-                return ok;
-            };
-            uint32_t spins = 0;
-            while (!block_sync_and(sh, read()) && !sh.aborted) {
-                __builtin_amdgcn_s_sleep(2);
-                if (tid() == 0)
-                    stuck(L.exchange, L.xl, ++spins, sh);
-            }
+    if (chunk == 0)
+        wait_stores();  // the K row chunk 0 stored is in the cache before any output of the head is published
+    if (owner)
+        coherent_store64(blocks + static_cast<size_t>(chunk) * part_words + mine,
+                         (static_cast<uint64_t>(part_epoch) << 32) | __float_as_uint(out));
+    const int owned = chunk < outputs ? (outputs - 1 - chunk) / chunks + 1 : 0;  // outputs chunk, chunk + chunks, ...
+    const int words = owned * chunks;                                           // [owned output][chunk]
+    float* own = sh.region;                  // [outputs]: this chunk's partial, for its own slots
+    float* merge = sh.region + kMaxThreadsPadded;  // [owned output][chunk]
+    static_assert(2 * kMaxThreadsPadded <= kLdsRegionFloats, "merge slots exceed the work region");
+    block_sync(sh);  // P V's LDS reads are done
+    if (owner)
+        own[mine] = out;
+    constexpr int kMergeBatch = 2;
+    for (int base = 0; base < words; base += kMergeBatch * kThreads) {  // block-uniform
+        uint64_t w[kMergeBatch];
+        auto slot = [&](int u) { return min(base + u * kThreads + static_cast<int>(tid()), words - 1); };
+        auto read = [&]() {
 #pragma unroll
             for (int u = 0; u < kMergeBatch; ++u) {
-                const int j = base + u * kThreads + static_cast<int>(tid());
-                if (j < words)
-                    merge[j] = __uint_as_float(static_cast<uint32_t>(w[u]));
+                const int j = slot(u), k = j / chunks, c = j - k * chunks;
+                w[u] = coherent_load64(blocks + static_cast<size_t>(c) * part_words + chunk + k * chunks);
+            }
+            bool ok = true;
+#pragma unroll
+            for (int u = 0; u < kMergeBatch; ++u)
+                ok &= slot(u) % chunks == chunk || static_cast<uint32_t>(w[u] >> 32) == part_epoch;
+            return ok;
+        };
+        uint32_t spins = 0;
+        while (!block_sync_and(sh, read()) && !sh.aborted) {
+            __builtin_amdgcn_s_sleep(1);
+            if (tid() == 0)
+                stuck(L.exchange, L.xl, ++spins, sh);
+        }
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+            const int j = base + u * kThreads + static_cast<int>(tid());
+            if (j < words) {
+                const int k = j / chunks, c = j - k * chunks;
+                merge[j] = c == chunk ? own[chunk + k * chunks] : __uint_as_float(static_cast<uint32_t>(w[u]));
             }
         }
-        block_sync(sh);
-        if (owner)
-            for (int k = 0; k < words / outputs; ++k)
-                total += merge[k * outputs + mine];
     }
-    wait_stores();  // the K row (chunk 0 stores it) is in the cache before anyone sees this output
-    if (owner)
-        publish_element<BF16>(attn, first_head * dh + mine, N::round(total), out_epoch);
+    block_sync(sh);
+    if (static_cast<int>(tid()) < owned) {
+        // In chunk order, 8 LDS reads issued at a time (a loop of read-then-add would pay one
+        // LDS round trip per chunk).
+        const int k = tid();
+        const float* column = merge + k * chunks;
+        float total = 0.0f;
+        for (int c0 = 0; c0 < chunks; c0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                v[u] = column[c0 + u < chunks ? c0 + u : 0];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (c0 + u < chunks)
+                    total += v[u];
+        }
+        publish_element<BF16>(attn, first_head * dh + chunk + k * chunks, N::round(total), out_epoch);
+    }
 }
 
 // Wo rows plus the residual (ops.cuh:718-734): r = round(round(Wo a) + x).
