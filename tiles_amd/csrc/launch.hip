@@ -207,9 +207,6 @@ extern "C" int ti_describe_target(ti_target* out)
         std::vector<std::pair<const void*, int>> functions;
         for (const void* f : bf16 ? worker_functions_bf16() : worker_functions_f32())
             functions.emplace_back(f, kThreads);
-        if (bf16)
-            for (const void* f : worker_functions_ring())
-                functions.emplace_back(f, kRingThreads);
         for (const auto& [f, threads] : functions) {
             hipFuncAttributes attributes{};
             int active = 0;
@@ -378,11 +375,5 @@ extern "C" int ti_enqueue_worker(void* stream, const ti_worker_program_view* pro
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (program->weight_dtype != TI_DTYPE_BFLOAT16)
         return launch_worker_f32(s, *program, *buffers, position, token, selection);
-    // TILES_AMD_WORKER selects the worker where a streaming worker exists: "stream" or
-    // "exchange" (read at every launch).  The exchange worker is the default.
-    const char* choice = std::getenv("TILES_AMD_WORKER");
-    const bool stream_worker = choice != nullptr && std::strcmp(choice, "stream") == 0;
-    if (stream_worker && ring_worker_compiled(program->shape, program->weight_dtype))
-        return launch_worker_ring(s, *program, *buffers, position, token, selection);
     return launch_worker_bf16(s, *program, *buffers, position, token, selection);
 }

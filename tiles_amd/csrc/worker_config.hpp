@@ -30,17 +30,10 @@ inline constexpr int kAttentionSharedBytes = 8448;
 // also keeps its packed bf16 P*V operands here after its FP32 scores: 4 x 1056 scores, then
 // 3 parts x 4 heads x 1120 padded positions of bf16 = 10,944 floats.
 inline constexpr int kRegionFloats = 11008;
-// The streaming worker (bf16 packages of hidden size 2048): 8 compute waves and 4 streamer
-// waves per worker, LDS sized for that hidden size, and a ring of 4 KB weight-row slots.
-inline constexpr int kRingThreads = kThreads + 256;
-inline constexpr int kRingHidden = 2048;
-inline constexpr int kRingRegionFloats = 4096;     // scores of chunks up to 1024 bf16 steps (longer: exchange worker), FFN reduction rounds
-inline constexpr int kRingStreamRecords = 320;
-inline constexpr int kRingSlots = 24;
 inline constexpr uint64_t kBufferRange = 1ull << 31;   // bytes a weight buffer resource addresses
 inline constexpr uint32_t kSpinLimit = 1u << 20;    // polls before a wait is declared stuck
 inline constexpr const char* kAbi = "tileinfer-decoder-v10";
-inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-stream-ring-v3-b512";
+inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-v4-b512";
 
 // Exchange phases within one (step, layer); the candidates use layer == layers.
 inline constexpr int kPhaseQKV = 0;
@@ -157,12 +150,6 @@ int launch_worker_bf16(hipStream_t stream, const ti_worker_program_view& p, cons
 int launch_worker_f32(hipStream_t stream, const ti_worker_program_view& p, const ti_worker_buffers& b, int position,
                       ti_token_input token, ti_selection selection);
 std::vector<const void*> worker_functions_bf16();
-// The streaming worker for the program's shape, when one is compiled (ring_worker_compiled)
-// and TILES_AMD_WORKER=stream asks for it.
-bool ring_worker_compiled(const ti_model_shape& s, int dtype);
-int launch_worker_ring(hipStream_t stream, const ti_worker_program_view& p, const ti_worker_buffers& b, int position,
-                       ti_token_input token, ti_selection selection);
-std::vector<const void*> worker_functions_ring();
 std::vector<const void*> worker_functions_f32();
 
 // Thread-local message of the last failed call (ti_last_error_message).

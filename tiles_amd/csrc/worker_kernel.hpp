@@ -31,39 +31,14 @@
 #include "tileinfer_amd.h"
 #include "worker_config.hpp"
 
-// Two builds of this source.  The exchange worker (TILES_RING 0): 8 waves run every task and
-// each task streams its own weights.  The streaming worker (TILES_RING 1, bf16 with hidden
-// size 2048): 8 compute waves run the tasks and 4 streamer waves copy every weight row the
-// worker will consume, in consumption order, into a ring of LDS row slots.  The streamers run
-// ahead across tasks, layers and tokens, so HBM keeps streaming while the compute waves wait
-// for their inputs.  The compute waves' own loads (exchange polls, K/V rows) never sit behind
-// bulk weight loads either: a wave's vector loads return in issue order.
-#ifndef TILES_RING
-#define TILES_RING 0
-#endif
-
 namespace tiles {
 namespace {
 
-constexpr bool kRing = TILES_RING != 0;
-constexpr int kWaves = kThreads / 64;  // compute waves
-#if TILES_RING
-constexpr int kStreamWaves = 4;
-constexpr int kBlockThreads = kThreads + 64 * kStreamWaves;
-constexpr int kLdsHidden = kRingHidden;
-constexpr int kLdsRegionFloats = kRingRegionFloats;
-constexpr int kLdsStreamRecords = kRingStreamRecords;
-constexpr int kRingRowVectors = kRingHidden * 2 / 16;  // 16-byte vectors of one bf16 weight row
-// Rows in flight per streamer wave: 12 rows (48 KB) per CU.  HBM streams at 95% of its peak
-// with 32 KB in flight per CU, and every extra byte in flight across the chip lengthens the
-// memory queue that each load waits in (7 rows: 8 us load latency during the FFN, and slower).
-constexpr int kStageRows = 3;
-#else
+constexpr int kWaves = kThreads / 64;
 constexpr int kBlockThreads = kThreads;
 constexpr int kLdsHidden = kMaxHidden;
 constexpr int kLdsRegionFloats = kRegionFloats;
 constexpr int kLdsStreamRecords = kMaxStreamRecords;
-#endif
 
 // The thread's index in the block, re-read at each use through an empty asm statement that the
 // compiler may neither move nor merge.  Address arithmetic on threadIdx.x is otherwise hoisted
@@ -179,15 +154,6 @@ struct Shared {
     int token;
     uint64_t mark_read;   // timeline: when the instruction's first exchange read returned
     uint64_t mark_ready;  // timeline: when its last exchange wait ended
-#if TILES_RING
-    // Weight rows in consumption order: slot s of the launch lives in ring[s % kRingSlots].
-    alignas(16) u32x4 ring[kRingSlots * kRingRowVectors];
-    alignas(16) int arrive[kWaves];       // barriers each compute wave has reached
-    alignas(16) int released[kWaves];     // per compute wave: the lowest slot it may still read
-    alignas(16) int landed[kStreamWaves]; // streamer wave q writes slots q, q + 4, ...: 1 + its last one
-    int failed[2];                        // block_sync_and: last barrier a wave failed, by parity
-    int stop;                             // the compute waves left the launch
-#endif
 };
 
 // ---------------------------------------------------------------- block synchronization
@@ -199,120 +165,21 @@ __device__ inline void lds_write(int* p, int v) { __hip_atomic_store(p, v, __ATO
 // operations in flight; also a compiler barrier for memory accesses.
 __device__ inline void lds_complete() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-#if TILES_RING
-constexpr uint32_t kRingSpinLimit = 1u << 24;  // polls of an LDS word before a wait is declared stuck
-
-// Minimum of the first N (4 or 8) LDS counters at p (16-byte aligned), read 16 bytes at a
-// time.
-template <int N>
-__device__ inline int lds_min(const int* p)
-{
-    static_assert(N == 4 || N == 8, "whole 16-byte groups");
-    // Through an LDS-address-space pointer: a generic volatile access compiles to a flat load,
-    // which also counts against the vector-memory counter and waits for every load in flight.
-    typedef int i32x4 __attribute__((ext_vector_type(4)));
-    typedef const volatile __attribute__((address_space(3))) i32x4 lds_i32x4;
-    lds_i32x4* q = (lds_i32x4*)(p);
-    i32x4 a = q[0];
-    int m = min(min(a[0], a[1]), min(a[2], a[3]));
-    if constexpr (N == 8) {
-        a = q[1];
-        m = min(m, min(min(a[0], a[1]), min(a[2], a[3])));
-    }
-    return __builtin_amdgcn_readfirstlane(m);
-}
-
-// Barrier of the compute waves (the streamer waves never take part, so s_barrier cannot be
-// used): each wave counts its arrivals in LDS and waits until every compute wave has arrived
-// as often.  Returns the barrier's number.
-__device__ inline int compute_barrier(Shared& sh)
-{
-    const int w = wave_id();
-    lds_complete();  // this wave's LDS writes land before its arrival does
-    const int generation = __builtin_amdgcn_readfirstlane(lds_read(&sh.arrive[w])) + 1;
-    lds_write(&sh.arrive[w], generation);
-    uint32_t spins = 0;
-    while (lds_min<kWaves>(sh.arrive) < generation) {
-        __builtin_amdgcn_s_sleep(1);
-        // A wave that left the launch never arrives (never expected; no wait is endless), and
-        // once a wait gave up, the launch only drains.
-        if (++spins > kRingSpinLimit || sh.aborted) {
-            sh.aborted = 1;
-            break;
-        }
-    }
-    asm volatile("" ::: "memory");
-    return generation;
-}
-#endif
 
 // Barrier of the waves that run tasks.
 __device__ inline void block_sync(Shared& sh)
 {
-#if TILES_RING
-    compute_barrier(sh);
-#else
     (void)sh;
     __syncthreads();
-#endif
 }
 
 // Barrier that also returns whether `pred` held in every task thread.
 __device__ inline bool block_sync_and(Shared& sh, bool pred)
 {
-#if TILES_RING
-    // A failing wave marks the barrier's number in the slot of its parity: a wave that passed
-    // the next barrier cannot overwrite that slot before every wave has read it.
-    const int next = __builtin_amdgcn_readfirstlane(lds_read(&sh.arrive[wave_id()])) + 1;
-    if (!__all(pred))
-        lds_write(&sh.failed[next & 1], next);
-    const int generation = compute_barrier(sh);
-    return lds_read(&sh.failed[generation & 1]) != generation;
-#else
     (void)sh;
     return __syncthreads_and(pred);
-#endif
 }
 
-#if TILES_RING
-// ---------------------------------------------------------------- weight ring (compute side)
-
-// Waits until ring slot `slot` holds its row; `have` caches a bound below which every slot
-// has landed.  Streamer wave q writes the slots s = q (mod 4) in order and then sets
-// landed[q] = s + 1 (q - 3 before its first), so every slot below min(landed) + 3 is there.
-__device__ inline void ring_wait(Shared& sh, uint32_t slot, int& have)
-{
-    uint32_t spins = 0;
-    while (static_cast<int>(slot) >= have) {
-        have = lds_min<kStreamWaves>(sh.landed) + kStreamWaves - 1;
-        if (static_cast<int>(slot) < have)
-            break;
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins > kRingSpinLimit || sh.aborted) {
-            sh.aborted = 1;
-            have = 0x7fffffff;  // read whatever the slot holds; the launch reports the timeout
-            break;
-        }
-    }
-    asm volatile("" ::: "memory");
-}
-
-__device__ inline const u32x4* ring_row(const Shared& sh, uint32_t slot)
-{
-    return sh.ring + (slot % kRingSlots) * kRingRowVectors;
-}
-
-// This wave reads no ring slot below `slot` any more.  Its reads of those slots precede this
-// write in program order, and one wave's LDS accesses execute in order.  Progress: a wave
-// releases everything below the first slot it needs before it waits, and the slots it waits
-// for lie within kRingSlots of that first slot, so the wave holding the lowest release can
-// always be served.
-__device__ inline void ring_release(Shared& sh, uint32_t slot)
-{
-    asm volatile("" ::: "memory");
-    lds_write(&sh.released[wave_id()], static_cast<int>(slot));
-}
-#endif
 
 // ---------------------------------------------------------------- exchange polling
 
@@ -813,91 +680,9 @@ struct InputSlice {
     }
 };
 
-// The norm scale of a lane's GEMV input slice (its 16-byte vectors col + k lr of a hidden row),
-// loaded before the task waits for its input.
-template <int VPL>
-struct SliceScale {
-    u32x4 v[VPL];
-};
-
-template <bool BF16, int VPL>
-__device__ __forceinline__ SliceScale<VPL> load_slice_scale(const void* scale, int d)
-{
-    const RowGeometry<BF16> g(d);
-    SliceScale<VPL> s;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k)
-        s.v[k] = global(static_cast<const u32x4*>(scale))[g.col + k * g.lr];
-    return s;
-}
-
-// rms_norm_lds's values for one lane's GEMV input slice, computed by every wave on its own: the
-// statistic repeats rms_norm_lds's association exactly (each thread's strided sum, the 64-lane
-// sum of each of the 8 waves, the waves in order), so the slice is bit-identical to what
-// rms_norm_lds leaves in LDS, without its three barriers and its LDS round trip.  v holds the
-// input as FP32 values (every wave's writes visible).
-template <bool BF16, int VPL>
-__device__ __forceinline__ InputSlice<VPL> normalized_slice(const float* v, int d, const SliceScale<VPL>& scale, float eps)
-{
-    using N = Num<BF16>;
-    // Elements per thread of rms_norm_lds's strided sum that this shape can fill (its hidden size
-    // is at most VPL x 64 vectors); the ones past it add +0.0 there.
-    constexpr int KH = VPL * 64 * N::kPerVec / kThreads > 0 ? VPL * 64 * N::kPerVec / kThreads : 1;
-    static_assert(KH <= kLdsHidden / kThreads, "the slice norm reads inside the LDS vector");
-    const int lane = tid() & 63;
-    float sums[kWaves];
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-        float x[KH];
-#pragma unroll
-        for (int k = 0; k < KH; ++k)
-            x[k] = v[k * kThreads + w * 64 + lane];
-        float sum = 0.0f;
-#pragma unroll
-        for (int k = 0; k < KH; ++k)
-            sum += k * kThreads + w * 64 + lane < d ? x[k] * x[k] : 0.0f;
-        sums[w] = group_sum<64>(sum);
-    }
-    float total = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-        total += lane_value(sums[w], 63);
-    const float inv = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
-    const RowGeometry<BF16> g(d);
-    InputSlice<VPL> in;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-        const int first = (g.col + k * g.lr) * N::kPerVec;
-        float n[N::kPerVec];
-#pragma unroll
-        for (int e = 0; e < N::kPerVec; ++e)
-            n[e] = N::round(N::round(v[first + e] * inv) * N::elem(scale.v[k], e));
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if constexpr (BF16)
-                in.r[k * 4 + q] = pack_bf16(n[2 * q], n[2 * q + 1]);
-            else
-                in.r[k * 4 + q] = __float_as_uint(n[q]);
-        }
-    }
-    return in;
-}
-
-// The normalized GEMV input of a lane.  Exchange worker: rms_norm_lds (three s_barriers, cheap)
-// and the slice from LDS.  Streaming worker: every wave repeats the statistic
-// (normalized_slice), because its LDS barriers cost about five s_barriers; the eight-fold
-// statistic costs more vector instructions than the exchange worker's barriers save.  Both give
-// the same bits.
+// The normalized GEMV input of a lane: rms_norm_lds, then the lane's slice from LDS.
 template <bool BF16, int VPL>
 struct NormInput {
-#if TILES_RING
-    SliceScale<VPL> scale;
-    __device__ NormInput(const void* weights, int d) : scale(load_slice_scale<BF16, VPL>(weights, d)) {}
-    __device__ InputSlice<VPL> operator()(Shared& sh, int d, float eps) const
-    {
-        return normalized_slice<BF16, VPL>(sh.vec, d, scale, eps);
-    }
-#else
     NormScale scale;
     __device__ NormInput(const void* weights, int d) : scale(load_scale<BF16>(weights, d)) {}
     __device__ InputSlice<VPL> operator()(Shared& sh, int d, float eps) const
@@ -906,7 +691,6 @@ struct NormInput {
         const RowGeometry<BF16> g(d);
         return InputSlice<VPL>(gemv_input<BF16>(sh), g.col, g.lr);
     }
-#endif
 };
 
 // Dot products of rows [r0, r1) of NM matrices of hidden width with an input vector: prepare()
@@ -914,45 +698,18 @@ struct NormInput {
 // vector (InputSlice).  emit(row, dots) runs in each row group's last lane with one dot per
 // matrix.
 //
-// Exchange worker: row_offset(m, row) is the byte offset from `base` of a row of matrix m
-// (below 2 GiB).  D passes of loads are in flight; all D issue before `prepare`, which runs
-// block-wide, waits for the task's inputs and writes u, so weight latency overlaps the wait.
-// Streaming worker: row r0 + j is ring slot slot0 + j (NM == 1); wave w takes rows j = w,
-// w + 8, ... as in the exchange worker's passes, so both compute the same sums.
+// row_offset(m, row) is the byte offset from `base` of a row of matrix m (below 2 GiB).  D passes
+// of loads are in flight; all D issue before `prepare`, which runs block-wide, waits for the
+// task's inputs and writes u, so weight latency overlaps the wait.
 template <bool BF16, int VPL, int NM, int DEPTH = 0, typename RowOffset, typename Prepare, typename MakeSlice,
           typename Emit>
-__device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int r0, int r1, int cols, uint32_t slot0,
-                                    Shared& sh, Prepare prepare, MakeSlice make_slice, Emit emit)
+__device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int r0, int r1, int cols, Shared& sh,
+                                    Prepare prepare, MakeSlice make_slice, Emit emit)
 {
     using N = Num<BF16>;
     constexpr int K = VPL * NM;
     constexpr int D = DEPTH > 0 ? DEPTH : (K <= 4 ? 4 : (K <= 8 ? 2 : 1));
     const RowGeometry<BF16> g(cols);
-#if TILES_RING
-    static_assert(BF16 && NM == 1 && VPL * 64 == kRingRowVectors, "ring rows are whole bf16 hidden rows");
-    (void)base;
-    (void)row_offset;
-    (void)D;
-    prepare();
-    const InputSlice<VPL> in = make_slice();
-    const int rows = r1 - r0;
-    int have = 0;
-    for (int j = g.wave; j < rows; j += kWaves) {
-        const uint32_t slot = slot0 + static_cast<uint32_t>(j);
-        ring_wait(sh, slot, have);
-        const u32x4* ring = ring_row(sh, slot);
-        u32x4 w[VPL];
-#pragma unroll
-        for (int k = 0; k < VPL; ++k)
-            w[k] = ring[k * 64 + g.col];
-        float dots[1] = {group_sum<64>(in.template dot<BF16>(w))};
-        ring_release(sh, slot0 + static_cast<uint32_t>(min(j + kWaves, rows)));
-        if (g.col == 63)
-            emit(r0 + j, dots);
-    }
-    ring_release(sh, slot0 + static_cast<uint32_t>(rows));
-#else
-    (void)slot0;
     (void)sh;
     auto active = [&](int pass) { return g.first_row(r0, pass) < r1; };
     // Lanes past the task read the task's first row from its start, 16 bytes apart per k: one
@@ -1000,7 +757,6 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
         }
     }
     (void)N::kBytes;
-#endif
 }
 
 // ---------------------------------------------------------------- operations
@@ -1016,8 +772,7 @@ __device__ inline const void* gemv_input(const Shared& sh)
 // token's attention takes V from the exchange words, and the worker's next input poll waits for
 // the cache stores before it publishes anything else, so later tokens find the row complete.
 template <bool BF16, int VPL>
-__device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_record& t, int step, ti_token_id token, uint32_t slot0,
-                                       Shared& sh)
+__device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_record& t, int step, ti_token_id token, Shared& sh)
 {
     using N = Num<BF16>;
     const int d = L.shape.hidden_size;
@@ -1040,7 +795,7 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     auto prepare = [&]() { load_hidden(L, layer, step, token, sh.vec, sh); };
     auto make_slice = [&]() { return norm(sh, d, L.numeric.rms_norm_eps); };
     float* staged_v = sh.small;  // this task's V rows, for the cache stores after the GEMV
-    gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, 0), row_offset, begin, end, d, slot0, sh, prepare, make_slice,
+    gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, 0), row_offset, begin, end, d, sh, prepare, make_slice,
                        [&](int row, const float* dots) {
         const float value = N::round(dots[0]);
         publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
@@ -1281,7 +1036,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         // Tiles past the preloaded ones (chunks longer than TW * kWaves tiles): kGroup per wave
         // in flight at once, one wait per group instead of one per tile (tiles past the chunk
         // read zeros without memory traffic).
-        constexpr int kGroup = kRing ? 2 : 4;  // the streaming worker has 168 VGPRs per wave
+        constexpr int kGroup = 4;
         for (int tile0 = wave + TW * kWaves; tile0 * kTile < span; tile0 += kGroup * kWaves) {
             u32x4 kb[kGroup][KS];
 #pragma unroll
@@ -1715,7 +1470,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 // Wo rows plus the residual (ops.cuh:718-734): r = round(round(Wo a) + x).
 template <bool BF16, int VPL>
 __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, const ti_task_record& t, int step,
-                                                    ti_token_id token, uint32_t slot0, Shared& sh)
+                                                    ti_token_id token, Shared& sh)
 {
     using N = Num<BF16>;
     const int d = L.shape.hidden_size;
@@ -1738,7 +1493,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
                 N::store(L.scratch, L.layout.attention + i, sh.vec[i]);
     };
     gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, L.layout.Wo), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
-                       begin, end, d, slot0, sh, prepare,
+                       begin, end, d, sh, prepare,
                        [&]() { return InputSlice<VPL>(gemv_input<BF16>(sh), RowGeometry<BF16>(d).col, RowGeometry<BF16>(d).lr); },
                        [&](int row, const float* dots) {
                            const float r = N::round(N::round(dots[0]) + residual[row - begin]);
@@ -1761,8 +1516,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
 // began (the burst is 48 MB across the chip); wave 0 sees it about 2 us sooner (696 against 717
 // us per token at ctx 1, 812 against 834 at ctx 4096).
 template <bool BF16, int VPL>
-__device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_record& t, int step, uint32_t slot0,
-                                      Shared& sh)
+__device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
@@ -1775,7 +1529,6 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     const RowGeometry<BF16> g(d);
     const NormInput<BF16, VPL> norm(L.layer_weight(layer, L.layout.ffn_norm), d);
     auto row_of = [&](int pass) { return g.first_row(r0, pass) + g.sub; };
-#if !TILES_RING
     const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
     const char* gate = L.layer_weight(layer, L.layout.Wgate) + g.col * 16;
     const char* up = L.layer_weight(layer, L.layout.Wup) + g.col * 16;
@@ -1814,10 +1567,6 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     }
     issue_fence();
     block_sync(sh);
-#else
-    poll_input<BF16>(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR), L.exchange, L.xl, sh,
-               [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
-#endif
     if (tid() == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
     const InputSlice<VPL> in = norm(sh, d, L.numeric.rms_norm_eps);
@@ -1850,97 +1599,6 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
             for (int j = 0; j < PV; ++j)
                 acc[k * PV + j] += N::elem(wd[k], j) * p;
     };
-#if TILES_RING
-    // Passes of 8 rows over the ring: a pass of n rows is 3 n slots from slot0 + 24 p, the gate
-    // and up rows of each row, then the n down rows.  Wave w computes p of the pass's row w into
-    // LDS; after the block meets, every wave reads the pass's down rows at its own output columns
-    // 256 w + 4 lane .. + 3 and adds row j into accumulator j mod 8, the wave that holds row j in
-    // the exchange worker.  The eight accumulators are then added in wave order, the exchange
-    // worker's cross-wave sum, so both publish the same bits with no reduction through LDS.
-    // The streamer fills the next pass's gate and up rows while this one's down rows are summed.
-    static_assert(BF16 && VPL * 64 == kRingRowVectors, "ring rows are whole bf16 hidden rows");
-    static_assert(kOut == 32 && kWaves == 8, "a lane owns 4 columns of the down rows in 8 classes");
-    static_assert(3 * kWaves <= kRingSlots, "a pass of the chunk fits the ring");
-    (void)row_of;
-    (void)D;
-    (void)NV;
-    (void)product_row;
-    (void)acc;
-    const int rows = r1 - r0;
-    float* pvals = sh.small;  // p of each row of the chunk (rows <= kMaxTaskRows)
-    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-    float part[kWaves][4];
-#pragma unroll
-    for (int c = 0; c < kWaves; ++c)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            part[c][e] = 0.0f;
-    const int column = g.wave * 256 + 4 * lane;
-    int have = 0;
-    for (int j0 = 0; j0 < rows; j0 += kWaves) {
-        const int count = min(kWaves, rows - j0);
-        const uint32_t pass0 = slot0 + 3u * static_cast<uint32_t>(j0);  // this pass: 2 count gate/up slots, count down slots
-        const uint32_t down0 = pass0 + 2u * static_cast<uint32_t>(count);
-        if (g.wave < count) {
-            const int j = j0 + g.wave;
-            const uint32_t slot = pass0 + 2u * static_cast<uint32_t>(g.wave);
-            ring_release(sh, slot);  // nothing of this chunk below its gate row (progress: see ring_release)
-            ring_wait(sh, slot + 1, have);
-            const u32x4* ring_gate = ring_row(sh, slot);
-            const u32x4* ring_up = ring_row(sh, slot + 1);
-            u32x4 wg[VPL], wu[VPL];
-#pragma unroll
-            for (int k = 0; k < VPL; ++k) {
-                wg[k] = ring_gate[k * 64 + g.col];
-                wu[k] = ring_up[k * 64 + g.col];
-            }
-            ring_release(sh, down0);
-            const float gate_dot = lane_value(group_sum<64>(in.template dot<BF16>(wg)), 63);
-            const float up_dot = lane_value(group_sum<64>(in.template dot<BF16>(wu)), 63);
-            const float gr = N::round(gate_dot);
-            const float silu = N::round(gr / (1.0f + expf(-gr)));
-            const float p = N::round(silu * N::round(up_dot));
-            if (g.col == 63) {
-                N::store(L.scratch, L.layout.product + r0 + j, p);
-                pvals[j] = p;
-            }
-        } else {
-            ring_release(sh, down0);
-        }
-        block_sync(sh);  // the pass's products are in LDS
-        ring_wait(sh, down0 + static_cast<uint32_t>(count - 1), have);
-        u32x2 wd[kWaves];
-        float pj[kWaves];
-#pragma unroll
-        for (int c = 0; c < kWaves; ++c) {
-            const int cc = c < count ? c : 0;  // past the chunk: re-read a row, weight 0
-            wd[c] = reinterpret_cast<const u32x2*>(ring_row(sh, down0 + static_cast<uint32_t>(cc)))[column / 4];
-            pj[c] = pvals[j0 + cc];
-        }
-        ring_release(sh, down0 + static_cast<uint32_t>(count));
-#pragma unroll
-        for (int c = 0; c < kWaves; ++c) {
-            if (c < count) {
-                part[c][0] += __uint_as_float(wd[c][0] << 16) * pj[c];
-                part[c][1] += __uint_as_float(wd[c][0] & 0xffff0000u) * pj[c];
-                part[c][2] += __uint_as_float(wd[c][1] << 16) * pj[c];
-                part[c][3] += __uint_as_float(wd[c][1] & 0xffff0000u) * pj[c];
-            }
-        }
-    }
-    const uint32_t out_epoch = L.epoch_of(step, layer, kPhaseFfn);
-    uint64_t* chunk_partials = L.exchange + L.xl.ffn + static_cast<size_t>(t.chunk) * d;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        float total = 0.0f;
-#pragma unroll
-        for (int c = 0; c < kWaves; ++c)
-            total += part[c][e];
-        coherent_store64(chunk_partials + column + e, (static_cast<uint64_t>(out_epoch) << 32) | __float_as_uint(total));
-    }
-    return;
-#else
-    (void)slot0;
     for (int base = 0; g.first_row(r0, base) < r1; base += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
@@ -1951,7 +1609,6 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
             issue(pass + D, w[s]);
         }
     }
-#endif
     // Lanes of one wave that hold the same columns (several rows per pass) add up first.
     if (g.lr < 64)
         residue_sum(acc, g.lr);
@@ -2095,7 +1752,7 @@ __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const t
 // logits round to the storage type, then widen; the largest value wins, the lowest ID among
 // equals, and any non-finite logit makes the candidate kNonFinite.
 template <bool BF16, int VPL>
-__device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_record& t, int step, uint32_t slot0, Shared& sh)
+__device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     const int d = L.shape.hidden_size;
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
@@ -2104,7 +1761,7 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     const uint32_t row_bytes = static_cast<uint32_t>(d) * Num<BF16>::kBytes;
     const NormInput<BF16, VPL> norm(L.stack_weight(L.stack.final_norm_offset), d);
     gemv<BF16, VPL, 1, 4>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
-                       begin, end, d, slot0, sh, [&]() { final_input(L, step, sh); },
+                       begin, end, d, sh, [&]() { final_input(L, step, sh); },
                        [&]() { return norm(sh, d, L.numeric.rms_norm_eps); },
                        [&](int row, const float* dots) {
                            const float logit = Num<BF16>::round(dots[0]);
@@ -2199,229 +1856,6 @@ __device__ void record_choice(const Launch<BF16>& L, int step, ti_token_id token
     }
 }
 
-// Ring slots a task consumes: one per weight row it streams (gate, up and down per FFN row).
-__device__ inline uint32_t ring_slots(const ti_task_record& t)
-{
-    switch (t.opcode) {
-    case TI_OP_QKV:
-    case TI_OP_OUTPUT_PROJECTION:
-    case TI_OP_LOGITS: return t.end - t.begin;
-    case TI_OP_FFN: return 3 * (t.end - t.begin);
-    default: return 0;
-    }
-}
-
-#if TILES_RING
-// ---------------------------------------------------------------- weight ring (streamer side)
-
-// The weight rows a worker's instruction stream consumes, in the order its compute waves
-// consume them (ring_slots), repeated once per step: slot s of the launch belongs to the task
-// whose slots hold it, at its local position (address()).  The walker keeps the current
-// task's row bases, so each lane can compute the address of a different slot.
-template <bool BF16, bool kCached>
-struct RowWalker {
-    const Launch<BF16>& L;
-    const Shared& sh;
-    ti_worker_task_range stream;
-    uint32_t d, kvw;
-    uint64_t row_bytes;
-    uint32_t index = 0;           // the current task's record
-    uint32_t first = 0, count = 0;  // its first slot (of the launch) and its slot count
-    uint32_t begin = 0, ffn_rows = 0, qkv = 0, lim0 = 0, lim1 = 0;
-    uint64_t base0 = 0, base1 = 0, base2 = 0;  // row 0 of each matrix (QKV: of each region's row numbering)
-
-    __device__ RowWalker(const Launch<BF16>& launch, const Shared& shared, ti_worker_task_range range)
-        : L(launch), sh(shared), stream(range)
-    {
-        d = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(L.shape.hidden_size));
-        kvw = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(L.shape.kv_heads * L.shape.head_dim));
-        row_bytes = static_cast<uint64_t>(d) * Num<BF16>::kBytes;
-    }
-    // Records come from LDS when the stream is cached there: a record read from memory is a
-    // load whose use waits for every weight load the wave has in flight.
-    __device__ ti_task_record record(uint32_t i) const
-    {
-        if constexpr (kCached)
-            return sh.stream[i];
-        else
-            return load_record(L.instructions + stream.begin + i);
-    }
-    __device__ uint32_t slots_per_step() const
-    {
-        uint32_t n = 0;
-        for (uint32_t i = 0; i < stream.count; ++i)
-            n += ring_slots(record(i));
-        return n;
-    }
-    // A weight's address, as a value known to be uniform (kept in scalar registers).
-    __device__ uint64_t weight(uint32_t layer, uint32_t region) const
-    {
-        return uniform64(reinterpret_cast<uint64_t>(L.layer_weight(static_cast<int>(layer), region)));
-    }
-    __device__ static uint64_t uniform64(uint64_t v)
-    {
-        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-        return (static_cast<uint64_t>(hi) << 32) | lo;
-    }
-    // Opens the first task with rows at or after record `from` (wrapping to the next step).
-    __device__ void open(uint32_t from)
-    {
-        index = from;
-        ti_task_record t = record(index);
-        while (ring_slots(t) == 0) {
-            index = index + 1 == stream.count ? 0 : index + 1;
-            t = record(index);
-        }
-        count = __builtin_amdgcn_readfirstlane(ring_slots(t));
-        const uint32_t opcode = __builtin_amdgcn_readfirstlane(t.opcode);
-        const uint32_t layer = __builtin_amdgcn_readfirstlane(t.layer);
-        begin = __builtin_amdgcn_readfirstlane(t.begin);
-        ffn_rows = opcode == TI_OP_FFN ? __builtin_amdgcn_readfirstlane(t.end - t.begin) : 0u;
-        qkv = opcode == TI_OP_QKV;
-        lim0 = lim1 = 0xffffffffu;
-        if (opcode == TI_OP_QKV) {
-            base0 = weight(layer, L.layout.Wq);
-            base1 = weight(layer, L.layout.Wk) - d * row_bytes;
-            base2 = weight(layer, L.layout.Wv) - (d + kvw) * row_bytes;
-            lim0 = d;
-            lim1 = d + kvw;
-        } else if (opcode == TI_OP_OUTPUT_PROJECTION) {
-            base0 = weight(layer, L.layout.Wo);
-        } else if (opcode == TI_OP_FFN) {
-            base0 = weight(layer, L.layout.Wgate);
-            base1 = weight(layer, L.layout.Wup);
-            base2 = weight(layer, L.layout.Wdown);
-        } else {
-            base0 = uniform64(reinterpret_cast<uint64_t>(L.stack_weight(L.stack.lm_head_offset)));
-        }
-    }
-    __device__ void advance()
-    {
-        first += count;
-        open(index + 1 == stream.count ? 0 : index + 1);
-    }
-    // Address of slot `slot` of the current task (per lane).  An FFN task streams its rows in
-    // passes of 8 (ffn_pass_slots): gate and up of each row of the pass, then the pass's down
-    // rows.
-    __device__ uint64_t address(uint32_t slot) const
-    {
-        const uint32_t local = slot - first;
-        uint32_t row = begin + local, m = 0;
-        if (ffn_rows != 0) {
-            const uint32_t pass = local / 24u, within = local - 24u * pass;
-            const uint32_t in_pass = min(8u, ffn_rows - 8u * pass);
-            const bool pair = within < 2u * in_pass;
-            row = begin + 8u * pass + (pair ? within >> 1 : within - 2u * in_pass);
-            m = pair ? (within & 1u) : 2u;
-        }
-        const uint32_t select = qkv ? (row >= lim0) + (row >= lim1) : m;
-        // Arithmetic on all three bases: a select among the members would become one load
-        // through a selected member address, which keeps the walker in scratch memory.
-        const uint64_t b0 = base0, b1 = base1, b2 = base2;
-        const uint64_t take1 = 0ull - static_cast<uint64_t>(select == 1);
-        const uint64_t take2 = 0ull - static_cast<uint64_t>(select == 2);
-        const uint64_t base = b0 ^ ((b0 ^ b1) & take1) ^ ((b0 ^ b2) & take2);
-        return base + row * row_bytes;
-    }
-};
-
-// Streamer wave q: the weight rows of slots q, q + 4, q + 8, ... of the launch
-// (slots_per_step x steps slots in all) go through a register queue, kStageRows rows deep,
-// into ring[slot % kRingSlots].  A slot is written once every compute wave released it
-// (released[] + kRingSlots > slot); landed[q] then announces it.  Loads of the next rows issue
-// while earlier rows wait for space, so HBM streams during the compute waves' dependency waits
-// until both ring and queue are full.  Whole rows per wave keep the handshake (space check,
-// announcement, addressing) to one per 4 KB.
-template <int VPL, bool kCached>
-__device__ __forceinline__ void stream_weights(const Launch<true>& L, const ti_worker_task_range& stream, Shared& sh)
-{
-    static_assert(VPL * 64 == kRingRowVectors, "streamer waves move whole rows");
-    static_assert(kRingSlots % kStreamWaves == 0, "each streamer wave owns fixed ring slots");
-    const uint32_t q = static_cast<uint32_t>(wave_id() - kWaves);
-    const int lane = tid() & 63;
-    RowWalker<true, kCached> walker(L, sh, stream);
-    // Every control value of this loop is wave-uniform (scalar): an exit the compiler took for
-    // divergent would mask the loop and collapse the count of loads it keeps in flight.
-    const uint32_t per_step = __builtin_amdgcn_readfirstlane(walker.slots_per_step());
-    const uint32_t total = per_step * static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(L.steps));
-    if (total <= q)
-        return;
-    walker.open(0);
-    constexpr uint32_t kStride = kStreamWaves;
-    constexpr uint32_t kBatch = kStride * kStageRows;  // slots between this wave's batches
-    // Lane k < kStageRows computes the address of slot n + 4 k (past the launch's last slot: the
-    // last row again, never written to the ring).
-    auto fill = [&](uint32_t n) {
-        const uint32_t slot = min(n + kStride * static_cast<uint32_t>(lane), total - 1);
-        uint64_t mine = 0;
-        while (true) {
-            const uint32_t end = walker.first + walker.count;
-            if (slot >= walker.first && slot < end)
-                mine = walker.address(slot);
-            if (!__any(lane < kStageRows && slot >= end))
-                break;
-            walker.advance();
-        }
-        return mine;
-    };
-    const uint32_t lane_bytes = static_cast<uint32_t>(lane) * 16u;
-    auto row_of = [&](uint64_t mine, int k) {
-        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(mine), k);
-        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(mine >> 32), k);
-        return reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | lo) + lane_bytes;
-    };
-    u32x4 staged[kStageRows][VPL];
-    uint64_t addresses = fill(q);
-#pragma unroll
-    for (int k = 0; k < kStageRows; ++k) {
-        const char* row = row_of(addresses, k);
-#pragma unroll
-        for (int v = 0; v < VPL; ++v)
-            staged[k][v] = load_weights(row + v * 1024);
-    }
-    int freed = kRingSlots;  // slots below this may be written
-    uint32_t spins = 0;
-    bool quit = false;
-    for (uint32_t n = q; n < total && !quit; n += kBatch) {
-        addresses = fill(n + kBatch);
-#pragma unroll
-        for (int k = 0; k < kStageRows; ++k) {
-            const uint32_t slot = n + kStride * static_cast<uint32_t>(k);
-            if (slot < total && !quit) {
-                while (static_cast<int>(slot) >= freed) {
-                    freed = lds_min<kWaves>(sh.released) + kRingSlots;
-                    if (static_cast<int>(slot) < freed)
-                        break;
-                    // The compute waves left (or a wait gave up): write nothing more and leave
-                    // after this batch.  A return from here would make the compiler wait for
-                    // every load in flight before each ring write.
-                    const int leave = __builtin_amdgcn_readfirstlane(lds_read(&sh.stop) | sh.aborted);
-                    if (leave || ++spins > kRingSpinLimit) {
-                        quit = true;
-                        freed = 0x7fffffff;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-                u32x4* dst = sh.ring + (slot % kRingSlots) * kRingRowVectors + lane;
-#pragma unroll
-                for (int v = 0; v < VPL; ++v)
-                    dst[v * 64] = staged[k][v];
-                // One wave's LDS accesses execute in order: the row is in LDS before the count
-                // that announces it.
-                asm volatile("" ::: "memory");
-                lds_write(&sh.landed[q], static_cast<int>(slot) + 1);
-            }
-            const char* row = row_of(addresses, k);
-#pragma unroll
-            for (int v = 0; v < VPL; ++v)
-                staged[k][v] = load_weights(row + v * 1024);
-        }
-    }
-}
-#endif
-
 template <bool BF16, int VPL, int LRK>
 __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> launch)
 {
@@ -2436,18 +1870,6 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
         sh.xsave_tag = 0;
         sh.rsave_tag = 0;
     }
-#if TILES_RING
-    if (tid() < kWaves) {
-        sh.arrive[tid()] = 0;
-        sh.released[tid()] = 0;
-    }
-    if (tid() < kStreamWaves)
-        sh.landed[tid()] = static_cast<int>(tid()) - (kStreamWaves - 1);
-    if (tid() < 2)
-        sh.failed[tid()] = 0;
-    if (tid() == 0)
-        sh.stop = 0;
-#endif
     __syncthreads();
     const Launch<BF16>& L = record;
     const bool generating = L.selection.generated != nullptr;
@@ -2461,23 +1883,6 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
         for (uint32_t i = tid(); i < stream.count; i += kBlockThreads)
             sh.stream[i] = load_record(L.instructions + stream.begin + i);
     __syncthreads();
-#if TILES_RING
-    if (wave_id() >= kWaves) {
-        if (cached)
-            stream_weights<VPL, true>(L, stream, sh);
-        else
-            stream_weights<VPL, false>(L, stream, sh);
-        return;
-    }
-#endif
-    // The compute waves leave: streamer waves waiting for ring space stop too.
-    auto leave = [&]() {
-#if TILES_RING
-        if (tid() == 0)
-            lds_write(&sh.stop, 1);
-#endif
-    };
-    uint32_t ring_slot = 0;  // ring slot of the next streamed weight row
     for (int step = 0; step < L.steps; ++step) {
         // The previous step's K/V cache stores complete before this step publishes anything.
         wait_stores();
@@ -2490,15 +1895,12 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
             token = global(L.device_tokens)[step];
         }
         if (L.stack.full_stack && (token < 0 || token >= L.stack.vocab_size)) {
-            leave();
             return;
         }
         for (uint32_t index = stream.begin; index < stream.begin + stream.count; ++index) {
             const ti_task_record task = cached ? sh.stream[index - stream.begin] : load_record(L.instructions + index);
             if (task.opcode == TI_OP_BARRIER)
                 continue;  // waves synchronize through the exchange words
-            const uint32_t slot0 = ring_slot;
-            ring_slot += ring_slots(task);
             // Optional timeline: 100 MHz device clock (s_memrealtime) at the start of every
             // instruction of the launch's last step, when its first exchange read returned,
             // when its inputs were complete, and at its end (diagnostic_context.cu:257-285).
@@ -2508,10 +1910,10 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
                 sh.mark_ready = 0;
             }
             switch (task.opcode) {
-            case TI_OP_QKV: op_qkv<BF16, VPL>(L, task, step, token, slot0, sh); break;
+            case TI_OP_QKV: op_qkv<BF16, VPL>(L, task, step, token, sh); break;
             case TI_OP_ATTENTION_SCORES: op_attention<BF16, LRK>(L, task, step, sh); break;
-            case TI_OP_OUTPUT_PROJECTION: op_output_projection<BF16, VPL>(L, task, step, token, slot0, sh); break;
-            case TI_OP_FFN: op_ffn<BF16, VPL>(L, task, step, slot0, sh); break;
+            case TI_OP_OUTPUT_PROJECTION: op_output_projection<BF16, VPL>(L, task, step, token, sh); break;
+            case TI_OP_FFN: op_ffn<BF16, VPL>(L, task, step, sh); break;
             case TI_OP_FFN_REDUCE: op_ffn_reduce<BF16>(L, task, step, sh); break;
             case TI_OP_EMBEDDING: {
                 const int d = L.shape.hidden_size;
@@ -2521,7 +1923,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
                 break;
             }
             case TI_OP_FINAL_RMS_NORM: op_final_rms_norm(L, task, step, sh); break;
-            case TI_OP_LOGITS: op_logits<BF16, VPL>(L, task, step, slot0, sh); break;
+            case TI_OP_LOGITS: op_logits<BF16, VPL>(L, task, step, sh); break;
             default: break;  // attention_values: merged inside the scores tasks
             }
             block_sync(sh);
@@ -2534,15 +1936,12 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
         if (sh.aborted) {
             if (tid() == 0 && generating && blockIdx.x == 0)
                 global(L.selection.status)[TI_STATUS_ERROR] = TI_DEVICE_SYNC_TIMEOUT;
-            leave();
             return;
         }
         if (generating && token == L.selection.eos_id) {
-            leave();
             return;
         }
     }
-    leave();
 }
 
 // ---------------------------------------------------------------- host side of the launch

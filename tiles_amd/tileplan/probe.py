@@ -10,7 +10,7 @@ from pathlib import Path
 from .plan import ABI, OPCODES
 
 # The compiled gfx950 worker's constants (tiles_amd/csrc/worker_config.hpp).
-FINGERPRINT = "decoder-gfx950-wave64-exchange-stream-ring-v3-b512"
+FINGERPRINT = "decoder-gfx950-wave64-exchange-v4-b512"
 THREADS = 512
 ATTENTION_SHARED_BYTES = 8448
 
