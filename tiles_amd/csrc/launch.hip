@@ -102,6 +102,8 @@ std::string check_shape(const ti_model_shape& s, int dtype)
     // A split chunk keeps its scores and every chunk's statistics in the work region at once.
     if (static_cast<long>(s.attention_chunk_steps) * group + 8 + static_cast<long>(s.attention_chunks) * group * 2 > kRegionFloats)
         return "attention chunk count exceeds the compiled worker's merge capacity";
+    if (static_cast<long>(s.max_context) * (s.attention_chunks > 0 ? s.attention_chunks : 1) >= (1L << 31))
+        return "context too long for the worker's 32-bit chunk arithmetic";
     if (s.intermediate_size % 2 != 0)
         return "odd intermediate size";
     return {};

@@ -100,7 +100,7 @@ __host__ __device__ inline ExchangeLayout exchange_layout(const ti_model_shape& 
 }
 
 // Word of [Q; K; V] projection row `row` in the packed per-head exchange block.
-__host__ __device__ inline int qkv_word(int row, const ti_model_shape& s)
+__host__ __device__ constexpr int qkv_word(int row, const ti_model_shape& s)
 {
     const int d = s.hidden_size, dh = s.head_dim, kvw = s.kv_heads * s.head_dim;
     const int group = s.query_heads / s.kv_heads, block = (group + 2) * dh;
@@ -110,6 +110,43 @@ __host__ __device__ inline int qkv_word(int row, const ti_model_shape& s)
         return (row - d) / dh * block + group * dh + (row - d) % dh;
     return (row - d - kvw) / dh * block + (group + 1) * dh + (row - d - kvw) % dh;
 }
+
+// qkv_word without integer division, for a head_dim DH fixed at compile time (a power of two)
+// and inv_group = 1 / group rounded to FP32: (head + 0.5) / group lies at least 1 / (2 group)
+// from an integer, far beyond the product's rounding error, so truncation gives head / group.
+template <int DH>
+__host__ __device__ constexpr int qkv_slot(int row, int d, int kvw, int group, float inv_group)
+{
+    static_assert(DH > 0 && (DH & (DH - 1)) == 0, "head_dim must be a power of two");
+    const int block = (group + 2) * DH;
+    if (row < d) {
+        const int head = row / DH;  // shifts: DH is a compile-time power of two
+        const int kv_head = static_cast<int>((static_cast<float>(head) + 0.5f) * inv_group);
+        return kv_head * block + (head - kv_head * group) * DH + row % DH;
+    }
+    const bool key = row < d + kvw;
+    const int r = key ? row - d : row - d - kvw;
+    return r / DH * block + (key ? group : group + 1) * DH + r % DH;
+}
+
+// qkv_slot agrees with qkv_word on every row of a shape (checked at compile time below).
+template <int DH>
+constexpr bool qkv_slot_agrees(int kv_heads, int group)
+{
+    ti_model_shape s{};
+    s.head_dim = DH;
+    s.kv_heads = kv_heads;
+    s.query_heads = kv_heads * group;
+    s.hidden_size = s.query_heads * DH;
+    const int kvw = kv_heads * DH;
+    for (int row = 0; row < s.hidden_size + 2 * kvw; ++row)
+        if (qkv_slot<DH>(row, s.hidden_size, kvw, group, 1.0f / static_cast<float>(group)) != qkv_word(row, s))
+            return false;
+    return true;
+}
+static_assert(qkv_slot_agrees<64>(8, 4) && qkv_slot_agrees<64>(8, 3) && qkv_slot_agrees<128>(8, 4) &&
+                  qkv_slot_agrees<32>(4, 2) && qkv_slot_agrees<16>(2, 1) && qkv_slot_agrees<64>(64, 3),
+              "qkv_slot must place every row where qkv_word does");
 
 // 16-byte vectors a lane holds of a hidden-width row: rows of `hidden` elements of `elem`
 // bytes are split over min(64, vectors) lanes.

@@ -88,6 +88,12 @@ struct Launch {
     ti_selection selection;
     int selection_slots;
     int workers;
+    // Derived on the host, so that no task divides at run time (an integer division by a
+    // run-time value is a chain of about 40 dependent instructions on this target).
+    int group;              // query heads per K/V head
+    float inv_group;        // 1 / group, rounded
+    int hidden_stride;      // row_stride(hidden_size, workers)
+    int qkv_stride;         // row_stride(hidden_size + 2 x K/V width, workers)
 
     __device__ size_t kv_width() const { return static_cast<size_t>(shape.kv_heads) * shape.head_dim; }
     __device__ const char* layer_weight(int layer, uint32_t offset) const
@@ -112,6 +118,15 @@ struct Launch {
                static_cast<uint32_t>(layer) * kPhases + static_cast<uint32_t>(phase) + 1u;
     }
 };
+
+// The hidden size, a compile-time constant in instantiations with more than one 16-byte vector
+// per lane: the launcher admits power-of-two vector counts only, so rows are then exactly
+// VPL x 64 vectors.  Loops, bounds and row geometry over it then fold to constants.
+template <bool BF16, int VPL>
+__device__ __forceinline__ int hidden_size(const Launch<BF16>& L)
+{
+    return VPL > 1 ? VPL * 64 * Num<BF16>::kPerVec : L.shape.hidden_size;
+}
 
 // bf16 elements of the attention's V^T block: head_dim rows of (block positions + 8).  It
 // shares LDS with the input vector.  A block holds the most positions (a multiple of 32, at most
@@ -492,7 +507,7 @@ __device__ inline void publish_element(uint64_t* region, int index, float rounde
 
 // Witness spacing of an exchange written by row tasks that split `n` rows over `workers`
 // (plan_core.py:275-278: every task gets at least n / workers rows).
-__device__ inline int row_stride(int n, int workers) { return n >= workers ? n / workers : 1; }
+__host__ __device__ inline int row_stride(int n, int workers) { return n >= workers ? n / workers : 1; }
 
 // ---------------------------------------------------------------- layer input and residuals
 
@@ -500,14 +515,16 @@ __device__ inline int row_stride(int n, int workers) { return n >= workers ? n /
 // first layer, the host-written input of a block package, or the previous layer's output.
 // A copy stays in sh.xsave for the layer's residual addition.
 template <bool BF16>
-__device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, int step, ti_token_id token, float* dst,
+__device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int d, int layer, int step, ti_token_id token, float* dst,
                                            Shared& sh)
 {
-    const int d = L.shape.hidden_size;
     if (layer == 0) {
+        // The token is uniform; as a scalar, its row offset (hoisted to the step's start by the
+        // compiler) does not hold two VGPRs across the whole step.
+        const int id = __builtin_amdgcn_readfirstlane(token);
         const void* row = L.stack.full_stack
                               ? static_cast<const void*>(L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) +
-                                                                        static_cast<size_t>(token) * d))
+                                                                        static_cast<size_t>(id) * d))
                               : L.input;
         float v[kLdsHidden / kThreads];
 #pragma unroll
@@ -523,7 +540,7 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int layer, in
         }
         block_sync(sh);
     } else {
-        poll_input<BF16>(L.exchange + L.xl.hidden(layer % 2), d, row_stride(d, L.workers), L.epoch_of(step, layer - 1, kPhaseY),
+        poll_input<BF16>(L.exchange + L.xl.hidden(layer % 2), d, L.hidden_stride, L.epoch_of(step, layer - 1, kPhaseY),
                    L.exchange, L.xl, sh, [&](int i, uint32_t p) { dst[i] = sh.xsave[i] = Num<BF16>::from_payload(p); });
     }
     if (tid() == 0)
@@ -771,12 +788,13 @@ __device__ inline const void* gemv_input(const Shared& sh)
 // and published unrotated.  V rows also go to the cache row of the current position; this
 // token's attention takes V from the exchange words, and the worker's next input poll waits for
 // the cache stores before it publishes anything else, so later tokens find the row complete.
-template <bool BF16, int VPL>
+template <bool BF16, int VPL, int LRK>
 __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_record& t, int step, ti_token_id token, Shared& sh)
 {
     using N = Num<BF16>;
-    const int d = L.shape.hidden_size;
-    const int kvw = static_cast<int>(L.kv_width());
+    constexpr int dh = LRK * N::kPerVec;  // the launcher admits only this head_dim for the instantiation
+    const int d = hidden_size<BF16, VPL>(L);
+    const int kvw = L.shape.kv_heads * dh;
     const int layer = static_cast<int>(t.layer);
     const int position = L.position + step;
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
@@ -792,13 +810,18 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
         return (region + (static_cast<uint32_t>(row) - first) * static_cast<uint32_t>(d)) * N::kBytes;
     };
     const NormInput<BF16, VPL> norm(L.layer_weight(layer, L.layout.attn_norm), d);
-    auto prepare = [&]() { load_hidden(L, layer, step, token, sh.vec, sh); };
+    auto prepare = [&]() { load_hidden(L, d, layer, step, token, sh.vec, sh); };
     auto make_slice = [&]() { return norm(sh, d, L.numeric.rms_norm_eps); };
     float* staged_v = sh.small;  // this task's V rows, for the cache stores after the GEMV
+    // Read once into registers: inside the row loop every field of the LDS launch record would be
+    // re-read after each LDS store.
+    uint64_t* const words = L.exchange + L.xl.qkv;
+    const int group = L.group;
+    const float inv_group = L.inv_group;
     gemv<BF16, VPL, 1, 2>(L.layer_weight(layer, 0), row_offset, begin, end, d, sh, prepare, make_slice,
                        [&](int row, const float* dots) {
         const float value = N::round(dots[0]);
-        publish<BF16>(L.exchange + L.xl.qkv, qkv_word(row, L.shape), value, epoch);
+        publish<BF16>(words, qkv_slot<dh>(row, d, kvw, group, inv_group), value, epoch);
         if (row >= d + kvw)
             staged_v[row - begin] = value;
     });
@@ -876,12 +899,14 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         return;
     const int layer = static_cast<int>(t.layer);
     const int kv_head = static_cast<int>(t.kv_head);
-    const int group = s.query_heads / s.kv_heads;
+    const int group = L.group;
     const int first_head = kv_head * group;
-    const int kvw = static_cast<int>(L.kv_width());
+    const int kvw = s.kv_heads * dh;
     const int length = position + 1;
-    const int begin = static_cast<int>(static_cast<int64_t>(length) * chunk / chunks);
-    const int end = static_cast<int>(static_cast<int64_t>(length) * (chunk + 1) / chunks);
+    // 32-bit: the launcher bounds max_context x attention_chunks below 2^31.
+    const int begin = chunk == 0 ? 0 : static_cast<int>(static_cast<uint32_t>(length * chunk) / static_cast<uint32_t>(chunks));
+    const int end = chunk + 1 == chunks ? length
+                                        : static_cast<int>(static_cast<uint32_t>(length * (chunk + 1)) / static_cast<uint32_t>(chunks));
     const int span = end - begin;
 
     const int lane = tid() & 63, wave = wave_id();
@@ -943,7 +968,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const int block = (group + 2) * dh;
     float* incoming = sh.region;  // [group][dh] Q, [dh] K, [dh] V
     poll_words<false>(L.exchange + L.xl.qkv + static_cast<size_t>(kv_head) * block, block,
-               row_stride(s.hidden_size + 2 * kvw, L.workers), L.epoch_of(step, layer, kPhaseQKV), L.exchange, L.xl, sh,
+               L.qkv_stride, L.epoch_of(step, layer, kPhaseQKV), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) { incoming[i] = N::from_payload(p); });
     block_sync(sh);
     for (int index = tid(); index < (group + 1) * half; index += kThreads) {
@@ -1473,7 +1498,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
                                                     ti_token_id token, Shared& sh)
 {
     using N = Num<BF16>;
-    const int d = L.shape.hidden_size;
+    const int d = hidden_size<BF16, VPL>(L);
     const int layer = static_cast<int>(t.layer);
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseR);
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
@@ -1482,7 +1507,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
     auto prepare = [&]() {
         for (int i = begin + static_cast<int>(tid()); i < end; i += kThreads)
             residual[i - begin] = input_element(L, layer, step, token, i, sh);
-        poll_input<BF16>(L.exchange + L.xl.attn, d, (L.shape.query_heads / L.shape.kv_heads) * L.shape.head_dim,
+        poll_input<BF16>(L.exchange + L.xl.attn, d, L.group * L.shape.head_dim,
                    L.epoch_of(step, layer, kPhaseAttn), L.exchange, L.xl, sh,
                    [&](int i, uint32_t p) {
                        sh.vec[i] = N::from_payload(p);
@@ -1523,7 +1548,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     constexpr int NV = 3 * VPL;                      // vectors per lane and row: gate, up, down
     constexpr int D = VPL >= 8 ? 1 : (VPL >= 4 ? 2 : 4);
     constexpr int kOut = VPL * PV;                   // outputs a lane owns
-    const int d = L.shape.hidden_size;
+    const int d = hidden_size<BF16, VPL>(L);
     const int layer = static_cast<int>(t.layer);
     const int r0 = static_cast<int>(t.begin), r1 = static_cast<int>(t.end);
     const RowGeometry<BF16> g(d);
@@ -1553,7 +1578,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     if (g.wave == 0) {
         issue(0, w[0]);
         issue_fence();
-        poll_words_one_wave<BF16, kOut * 64>(L.exchange + L.xl.r, d, row_stride(d, L.workers), L.epoch_of(step, layer, kPhaseR),
+        poll_words_one_wave<BF16, kOut * 64>(L.exchange + L.xl.r, d, L.hidden_stride, L.epoch_of(step, layer, kPhaseR),
                                              L.exchange, L.xl, sh,
                                              [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
 #pragma unroll
@@ -1660,11 +1685,12 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
     const int rows = end - begin;
     const uint32_t in_epoch = L.epoch_of(step, layer, kPhaseFfn);
     const uint64_t present = static_cast<uint64_t>(in_epoch) << 32;
-    int tpr = 64;
-    while (tpr > 1 && tpr * rows > kThreads)
-        tpr >>= 1;
-    const int slots = kThreads / tpr;
-    const int slot = tid() / tpr, lane = tid() % tpr;
+    int shift = 6;  // log2 of the lanes per row (shifts, not divisions by a run-time value)
+    while (shift > 0 && (rows << shift) > kThreads)
+        --shift;
+    const int tpr = 1 << shift;
+    const int slots = kThreads >> shift;
+    const int slot = static_cast<int>(tid()) >> shift, lane = static_cast<int>(tid()) & (tpr - 1);
     const uint64_t* base = L.exchange + L.xl.ffn;
     for (int first = 0; first < rows; first += slots) {
         const int row = begin + first + slot;
@@ -1729,20 +1755,20 @@ __device__ inline void keep_better(ti_candidate& best, ti_candidate other)
 // The last layer's output into sh.vec, visible to every wave (the final norm's input,
 // decoder_stack.py:126-132).
 template <bool BF16>
-__device__ __forceinline__ void final_input(const Launch<BF16>& L, int step, Shared& sh)
+__device__ __forceinline__ void final_input(const Launch<BF16>& L, int d, int step, Shared& sh)
 {
-    const int d = L.shape.hidden_size;
     const int layers = L.stack.layers;
-    poll_input<BF16>(L.exchange + L.xl.hidden(layers % 2), d, row_stride(d, L.workers), L.epoch_of(step, layers - 1, kPhaseY),
+    poll_input<BF16>(L.exchange + L.xl.hidden(layers % 2), d, L.hidden_stride, L.epoch_of(step, layers - 1, kPhaseY),
                L.exchange, L.xl, sh, [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
 }
 
-template <bool BF16>
+template <bool BF16, int VPL>
 __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
-    const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), L.shape.hidden_size);
-    final_input(L, step, sh);
-    rms_norm_lds<BF16>(sh.vec, L.shape.hidden_size, scale, L.numeric.rms_norm_eps, sh);
+    const int d = hidden_size<BF16, VPL>(L);
+    const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
+    final_input(L, d, step, sh);
+    rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
     void* hidden = (L.stack.layers + 1) % 2 == 0 ? L.input : L.output;
     for (int i = static_cast<int>(t.begin) + tid(); i < static_cast<int>(t.end); i += kThreads)
         Num<BF16>::store(hidden, i, sh.vec[i]);
@@ -1754,14 +1780,14 @@ __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const t
 template <bool BF16, int VPL>
 __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
-    const int d = L.shape.hidden_size;
+    const int d = hidden_size<BF16, VPL>(L);
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     const int lane = tid() & 63, wave = wave_id();
     ti_candidate best{-INFINITY, 0x7fffffff};
     const uint32_t row_bytes = static_cast<uint32_t>(d) * Num<BF16>::kBytes;
     const NormInput<BF16, VPL> norm(L.stack_weight(L.stack.final_norm_offset), d);
     gemv<BF16, VPL, 1, 4>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
-                       begin, end, d, sh, [&]() { final_input(L, step, sh); },
+                       begin, end, d, sh, [&]() { final_input(L, d, step, sh); },
                        [&]() { return norm(sh, d, L.numeric.rms_norm_eps); },
                        [&](int row, const float* dots) {
                            const float logit = Num<BF16>::round(dots[0]);
@@ -1910,7 +1936,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
                 sh.mark_ready = 0;
             }
             switch (task.opcode) {
-            case TI_OP_QKV: op_qkv<BF16, VPL>(L, task, step, token, sh); break;
+            case TI_OP_QKV: op_qkv<BF16, VPL, LRK>(L, task, step, token, sh); break;
             case TI_OP_ATTENTION_SCORES: op_attention<BF16, LRK>(L, task, step, sh); break;
             case TI_OP_OUTPUT_PROJECTION: op_output_projection<BF16, VPL>(L, task, step, token, sh); break;
             case TI_OP_FFN: op_ffn<BF16, VPL>(L, task, step, sh); break;
@@ -1922,7 +1948,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
                     Num<BF16>::store(L.input, i, Num<BF16>::load(row, i));
                 break;
             }
-            case TI_OP_FINAL_RMS_NORM: op_final_rms_norm(L, task, step, sh); break;
+            case TI_OP_FINAL_RMS_NORM: op_final_rms_norm<BF16, VPL>(L, task, step, sh); break;
             case TI_OP_LOGITS: op_logits<BF16, VPL>(L, task, step, sh); break;
             default: break;  // attention_values: merged inside the scores tasks
             }
@@ -1979,6 +2005,10 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     L.selection = selection;
     L.selection_slots = p.selection_slots;
     L.workers = p.workers;
+    L.group = p.shape.query_heads / p.shape.kv_heads;
+    L.inv_group = 1.0f / static_cast<float>(L.group);
+    L.hidden_stride = row_stride(p.shape.hidden_size, p.workers);
+    L.qkv_stride = row_stride(p.shape.hidden_size + 2 * p.shape.kv_heads * p.shape.head_dim, p.workers);
     void* args[] = {&L};
     const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decoder_worker<BF16, VPL, LRK>),
                                                     dim3(p.workers), dim3(kBlockThreads), args, 0, stream);
