@@ -156,7 +156,7 @@ struct Shared {
     alignas(16) float region[kLdsRegionFloats];  // scores/probabilities, reductions, FFN gate/up/product
     float xsave[kLdsHidden];      // the layer input this worker last read, before the norm
     float rsave[kLdsHidden];      // the attention block output this worker last read
-    float small[kMaxTaskRows];    // reductions over waves, softmax statistics, residual rows
+    alignas(16) float small[kMaxTaskRows];  // reductions over waves, softmax statistics, residual rows
     float rotated[(kMaxGroup + 1) * kMaxHeadDim];
     float vcur[kMaxHeadDim];
     float rope_cs[kMaxHeadDim];  // the position's RoPE cos (first half) and sin (second half)
@@ -509,15 +509,24 @@ __device__ inline void publish_element(uint64_t* region, int index, float rounde
 // (plan_core.py:275-278: every task gets at least n / workers rows).
 __host__ __device__ inline int row_stride(int n, int workers) { return n >= workers ? n / workers : 1; }
 
+// The first half of a block-wide RMSNorm (rms_apply is the second): each wave adds the squares
+// its threads accumulated over the elements they delivered and puts the sum in sh.small[wave].
+__device__ __forceinline__ void rms_partial(float squares, Shared& sh)
+{
+    squares = group_sum<64>(squares);
+    if ((tid() & 63) == 63)
+        sh.small[wave_id()] = squares;
+}
+
 // ---------------------------------------------------------------- layer input and residuals
 
 // The hidden state a layer reads, into dst (FP32): the token's embedding row for a stack's
 // first layer, the host-written input of a block package, or the previous layer's output.
 // A copy stays in sh.xsave for the layer's residual addition.
 template <bool BF16>
-__device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int d, int layer, int step, ti_token_id token, float* dst,
-                                           Shared& sh)
+__device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int d, int layer, int step, ti_token_id token, Shared& sh)
 {
+    float squares = 0.0f;  // the RMSNorm statistic over the elements this thread delivers
     if (layer == 0) {
         // The token is uniform; as a scalar, its row offset (hoisted to the step's start by the
         // compiler) does not hold two VGPRs across the whole step.
@@ -535,14 +544,21 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int d, int la
 #pragma unroll
         for (int k = 0; k < kLdsHidden / kThreads; ++k) {
             const int i = k * kThreads + static_cast<int>(tid());
-            if (i < d)
-                dst[i] = sh.xsave[i] = v[k];
+            if (i < d) {
+                sh.xsave[i] = v[k];
+                squares = fmaf(v[k], v[k], squares);
+            }
         }
-        block_sync(sh);
     } else {
-        poll_input<BF16>(L.exchange + L.xl.hidden(layer % 2), d, L.hidden_stride, L.epoch_of(step, layer - 1, kPhaseY),
-                   L.exchange, L.xl, sh, [&](int i, uint32_t p) { dst[i] = sh.xsave[i] = Num<BF16>::from_payload(p); });
+        poll_words<BF16>(L.exchange + L.xl.hidden(layer % 2), d, L.hidden_stride, L.epoch_of(step, layer - 1, kPhaseY),
+                         L.exchange, L.xl, sh, [&](int i, uint32_t p) {
+                             const float x = Num<BF16>::from_payload(p);
+                             sh.xsave[i] = x;
+                             squares = fmaf(x, x, squares);
+                         });
     }
+    rms_partial(squares, sh);
+    block_sync(sh);
     if (tid() == 0)
         sh.xsave_tag = L.epoch_of(step, layer, kPhaseQKV);
 }
@@ -596,38 +612,34 @@ __device__ __forceinline__ NormScale load_scale(const void* scale, int d)
     return s;
 }
 
-// In place: v[i] = round(round(v[i] * inv_rms) * scale[i]) for bf16, v[i] * inv_rms * scale[i]
-// for fp32 (decoder_reference.py:183-187, decoder_stack.py:126-132), with the bf16 bits in
-// sh.vbits (v is sh.vec).  The statistic is FP32.
+// RMSNorm in two block-wide halves around a barrier of the caller's: rms_partial (above), then
+// rms_apply after the barrier: the statistic is the waves' sums in wave order (FP32); then
+// element i = tid() + k * kThreads of the raw vector x becomes round(round(x[i] * inv_rms) *
+// scale[i]) in bf16, x[i] * inv_rms * scale[i] in fp32 (decoder_reference.py:183-187,
+// decoder_stack.py:126-132): into sh.vbits (bf16 bits, the GEMV input) and, for fp32 or when
+// asked, into sh.vec.  Ends with a barrier.
 template <bool BF16>
-__device__ __forceinline__ void rms_norm_lds(float* v, int d, const NormScale& scale, float eps, Shared& sh)
+__device__ __forceinline__ void rms_apply(const float* x, int d, const NormScale& scale, float eps, Shared& sh,
+                                          bool fp32_copy = false)
 {
-    float x[kLdsHidden / kThreads];  // all reads first (v holds kLdsHidden floats)
+    float xv[kLdsHidden / kThreads];  // all reads first
 #pragma unroll
-    for (int k = 0; k < kLdsHidden / kThreads; ++k)
-        x[k] = v[k * kThreads + tid()];
-    float sum = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kLdsHidden / kThreads; ++k)
-        sum += k * kThreads + static_cast<int>(tid()) < d ? x[k] * x[k] : 0.0f;
-    sum = group_sum<64>(sum);
-    const int lane = tid() & 63, wave = wave_id();
-    block_sync(sh);
-    if (lane == 63)
-        sh.small[wave] = sum;
-    block_sync(sh);
-    float total = 0.0f;
-    for (int w = 0; w < kWaves; ++w)
-        total += sh.small[w];
+    for (int k = 0; k < kLdsHidden / kThreads; ++k) {
+        const int i = k * kThreads + static_cast<int>(tid());
+        xv[k] = x[i < d ? i : 0];
+    }
+    static_assert(kWaves == 8, "wave sums read as two float4");
+    const float4 s0 = reinterpret_cast<const float4*>(sh.small)[0];
+    const float4 s1 = reinterpret_cast<const float4*>(sh.small)[1];
+    const float total = ((((((s0.x + s0.y) + s0.z) + s0.w) + s1.x) + s1.y) + s1.z) + s1.w;
     const float inv = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
-    // x[k] still holds v[i]: nobody writes v between the first read and here, and re-reading it
-    // after the barriers made every element a dependent LDS round trip.
 #pragma unroll
     for (int k = 0; k < kLdsHidden / kThreads; ++k) {
         const int i = k * kThreads + static_cast<int>(tid());
         if (i < d) {
-            const float y = Num<BF16>::round(Num<BF16>::round(x[k] * inv) * scale.v[k]);
-            v[i] = y;
+            const float y = Num<BF16>::round(Num<BF16>::round(xv[k] * inv) * scale.v[k]);
+            if (!BF16 || fp32_copy)
+                sh.vec[i] = y;
             if constexpr (BF16)
                 sh.vbits[i] = static_cast<uint16_t>(float_to_bf16_bits(y));
         }
@@ -697,14 +709,15 @@ struct InputSlice {
     }
 };
 
-// The normalized GEMV input of a lane: rms_norm_lds, then the lane's slice from LDS.
+// The normalized GEMV input of a lane: rms_apply to the raw vector x (its statistic already in
+// sh.small), then the lane's slice from LDS.
 template <bool BF16, int VPL>
 struct NormInput {
     NormScale scale;
     __device__ NormInput(const void* weights, int d) : scale(load_scale<BF16>(weights, d)) {}
-    __device__ InputSlice<VPL> operator()(Shared& sh, int d, float eps) const
+    __device__ InputSlice<VPL> operator()(const float* x, Shared& sh, int d, float eps) const
     {
-        rms_norm_lds<BF16>(sh.vec, d, scale, eps, sh);
+        rms_apply<BF16>(x, d, scale, eps, sh);
         const RowGeometry<BF16> g(d);
         return InputSlice<VPL>(gemv_input<BF16>(sh), g.col, g.lr);
     }
@@ -810,8 +823,8 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
         return (region + (static_cast<uint32_t>(row) - first) * static_cast<uint32_t>(d)) * N::kBytes;
     };
     const NormInput<BF16, VPL> norm(L.layer_weight(layer, L.layout.attn_norm), d);
-    auto prepare = [&]() { load_hidden(L, d, layer, step, token, sh.vec, sh); };
-    auto make_slice = [&]() { return norm(sh, d, L.numeric.rms_norm_eps); };
+    auto prepare = [&]() { load_hidden(L, d, layer, step, token, sh); };
+    auto make_slice = [&]() { return norm(sh.xsave, sh, d, L.numeric.rms_norm_eps); };
     float* staged_v = sh.small;  // this task's V rows, for the cache stores after the GEMV
     // Read once into registers: inside the row loop every field of the LDS launch record would be
     // re-read after each LDS store.
@@ -1573,14 +1586,18 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
         }
     };
     u32x4 w[D][NV];
+    float squares = 0.0f;  // wave 0 delivers every element of r, and the norm statistic with them
     // Waves 1-7 wait for their earlier stores (V cache rows of a QKV task) before their loads, as
     // the block-wide poll does after its reads, so that every later publish follows those stores.
     if (g.wave == 0) {
         issue(0, w[0]);
         issue_fence();
         poll_words_one_wave<BF16, kOut * 64>(L.exchange + L.xl.r, d, L.hidden_stride, L.epoch_of(step, layer, kPhaseR),
-                                             L.exchange, L.xl, sh,
-                                             [&](int i, uint32_t p) { sh.vec[i] = sh.rsave[i] = N::from_payload(p); });
+                                             L.exchange, L.xl, sh, [&](int i, uint32_t p) {
+                                                 const float x = N::from_payload(p);
+                                                 sh.rsave[i] = x;
+                                                 squares = fmaf(x, x, squares);
+                                             });
 #pragma unroll
         for (int s = 1; s < D; ++s)
             issue(s, w[s]);
@@ -1591,10 +1608,11 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
             issue(s, w[s]);
     }
     issue_fence();
+    rms_partial(squares, sh);
     block_sync(sh);
     if (tid() == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
-    const InputSlice<VPL> in = norm(sh, d, L.numeric.rms_norm_eps);
+    const InputSlice<VPL> in = norm(sh.rsave, sh, d, L.numeric.rms_norm_eps);
     float acc[kOut];
 #pragma unroll
     for (int n = 0; n < kOut; ++n)
@@ -1752,14 +1770,21 @@ __device__ inline void keep_better(ti_candidate& best, ti_candidate other)
         best = other;
 }
 
-// The last layer's output into sh.vec, visible to every wave (the final norm's input,
-// decoder_stack.py:126-132).
+// The last layer's output (the final norm's input, decoder_stack.py:126-132), raw into the work
+// region, and its RMSNorm statistic (rms_partial); visible to every wave on return.
 template <bool BF16>
 __device__ __forceinline__ void final_input(const Launch<BF16>& L, int d, int step, Shared& sh)
 {
     const int layers = L.stack.layers;
-    poll_input<BF16>(L.exchange + L.xl.hidden(layers % 2), d, L.hidden_stride, L.epoch_of(step, layers - 1, kPhaseY),
-               L.exchange, L.xl, sh, [&](int i, uint32_t p) { sh.vec[i] = Num<BF16>::from_payload(p); });
+    float squares = 0.0f;
+    poll_words<BF16>(L.exchange + L.xl.hidden(layers % 2), d, L.hidden_stride, L.epoch_of(step, layers - 1, kPhaseY),
+                     L.exchange, L.xl, sh, [&](int i, uint32_t p) {
+                         const float x = Num<BF16>::from_payload(p);
+                         sh.region[i] = x;
+                         squares = fmaf(x, x, squares);
+                     });
+    rms_partial(squares, sh);
+    block_sync(sh);
 }
 
 template <bool BF16, int VPL>
@@ -1768,7 +1793,7 @@ __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const t
     const int d = hidden_size<BF16, VPL>(L);
     const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
     final_input(L, d, step, sh);
-    rms_norm_lds<BF16>(sh.vec, d, scale, L.numeric.rms_norm_eps, sh);
+    rms_apply<BF16>(sh.region, d, scale, L.numeric.rms_norm_eps, sh, true);
     void* hidden = (L.stack.layers + 1) % 2 == 0 ? L.input : L.output;
     for (int i = static_cast<int>(t.begin) + tid(); i < static_cast<int>(t.end); i += kThreads)
         Num<BF16>::store(hidden, i, sh.vec[i]);
@@ -1788,7 +1813,7 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
     const NormInput<BF16, VPL> norm(L.stack_weight(L.stack.final_norm_offset), d);
     gemv<BF16, VPL, 1, 4>(L.stack_weight(L.stack.lm_head_offset), [&](int, int row) { return static_cast<uint32_t>(row) * row_bytes; },
                        begin, end, d, sh, [&]() { final_input(L, d, step, sh); },
-                       [&]() { return norm(sh, d, L.numeric.rms_norm_eps); },
+                       [&]() { return norm(sh.region, sh, d, L.numeric.rms_norm_eps); },
                        [&](int row, const float* dots) {
                            const float logit = Num<BF16>::round(dots[0]);
                            global(L.logits)[row] = logit;
