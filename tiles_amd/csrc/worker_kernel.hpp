@@ -160,6 +160,7 @@ struct Shared {
     float rotated[(kMaxGroup + 1) * kMaxHeadDim];
     float vcur[kMaxHeadDim];
     float rope_cs[kMaxHeadDim];  // the position's RoPE cos (first half) and sin (second half)
+    int rope_position;           // the position rope_cs holds, -1 when none
     ti_candidate candidates[kWaves];
     ti_task_record stream[kLdsStreamRecords];  // this worker's instructions, when they fit
     uint32_t xsave_tag;  // epoch_of(step, layer, kPhaseQKV) of xsave's contents, 0 when empty
@@ -279,10 +280,14 @@ __device__ inline void wait_witness_words(const uint64_t* src, int count, int st
 // re-reads.  Polling the whole vector from every thread of every worker floods the few memory
 // channels that hold it and slows the producers themselves.  Every read issues all its loads
 // before it looks at any of them: a use right after a load waits for it, and a loop of such
-// pairs would pay one round trip per word.
-template <bool kHalves, typename Sink>
+// pairs would pay one round trip per word.  `overlap()` runs while the first read is in flight.
+struct NoOverlap {
+    __device__ void operator()() const {}
+};
+
+template <bool kHalves, typename Sink, typename Overlap = NoOverlap>
 __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
-                                          const ExchangeLayout& xl, Shared& sh, Sink sink)
+                                          const ExchangeLayout& xl, Shared& sh, Sink sink, Overlap overlap = {})
 {
     constexpr int kBatch = ((kHalves ? kLdsHidden / 2 : kLdsHidden) + kThreads - 1) / kThreads;
     const int words = kHalves ? count / 2 : count;
@@ -292,20 +297,29 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
 #pragma unroll
     for (int k = 0; k < kBatch; ++k)
         w[k] = kHalves ? (static_cast<uint64_t>(want) << 48) | (want << 16) : static_cast<uint64_t>(want) << 32;
-    auto read = [&]() {
+    auto issue_reads = [&]() {
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int index = k * kThreads + static_cast<int>(tid());
             if (k * kThreads < words)  // block-uniform; lanes past the end re-read the last word
                 w[k] = coherent_load64(src + (index < words ? index : words - 1));
         }
+    };
+    auto check = [&]() {
         bool ok = true;
 #pragma unroll
         for (int k = 0; k < kBatch; ++k)
             ok &= word_present<kHalves>(w[k], want);
         return ok;
     };
-    const bool all_present = block_sync_and(sh, read());
+    auto read = [&]() {
+        issue_reads();
+        return check();
+    };
+    issue_reads();
+    issue_fence();
+    overlap();
+    const bool all_present = block_sync_and(sh, check());
     if (tid() == 0 && sh.mark_read == 0)
         sh.mark_read = __builtin_amdgcn_s_memrealtime();
     if (!all_present) {
@@ -899,7 +913,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     constexpr int kVtStride = PB + 8;                // bf16 elements per V^T row
     constexpr int kBlockTiles = PB / kTile;
     constexpr int TW = (kBlockTiles + kWaves - 1) / kWaves;  // tiles per wave in a block
-    static_assert(!kMfma || dh * kVtStride <= kVtElements, "V^T block exceeds its LDS area");
+    static_assert(!kMfma || dh * kVtStride + (dh / 8) * 16 <= kVtElements, "V^T block exceeds its LDS area");
     static_assert(!kMfma || dh / 16 <= kWaves, "a wave per 16 output dims");
     constexpr int kRowsPerWave = 64 / LRK;
     constexpr int kBlockRows = kWaves * kRowsPerWave;
@@ -969,44 +983,85 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     }
     issue_fence();
 
-    // cos/sin of the position's RoPE angles, rounded (ops.cuh:125-140).
+    // cos/sin of the position's RoPE angles, rounded (ops.cuh:125-140): the same for every layer
+    // of a step, so computed once per position (the tag is read before the poll's barriers and
+    // written after them), while the first exchange read is in flight.
     constexpr int half = dh / 2;
-    for (int pair = tid(); pair < half; pair += kThreads) {
-        const float angle = static_cast<float>(position) * global(L.rope)[pair];
-        sh.rope_cs[pair] = N::round(cosf(angle));
-        sh.rope_cs[half + pair] = N::round(sinf(angle));
-    }
+    const bool fresh_rope = sh.rope_position != position;
+    auto rope_table = [&]() {
+        if (fresh_rope)
+            for (int pair = tid(); pair < half; pair += kThreads) {
+                const float angle = static_cast<float>(position) * global(L.rope)[pair];
+                sh.rope_cs[pair] = N::round(cosf(angle));
+                sh.rope_cs[half + pair] = N::round(sinf(angle));
+            }
+    };
 
-    // This token's Q heads, K and V of the head group: one packed exchange block.
+    // This token's Q heads, K and V of the head group: one packed exchange block.  With
+    // head_dim <= 64, thread t polls element t and finds its RoPE partner (element t +- dh / 2)
+    // in lane t ^ (dh / 2) of its own wave, so it rotates in registers; wider heads go through
+    // the work region and a pass of their own.
+    constexpr bool kRopeInWave = half <= 32;
     const int block = (group + 2) * dh;
-    float* incoming = sh.region;  // [group][dh] Q, [dh] K, [dh] V
+    const int qk = (group + 1) * dh;
+    float held = 0.0f;  // kRopeInWave: element tid() of the block
     poll_words<false>(L.exchange + L.xl.qkv + static_cast<size_t>(kv_head) * block, block,
                L.qkv_stride, L.epoch_of(step, layer, kPhaseQKV), L.exchange, L.xl, sh,
-               [&](int i, uint32_t p) { incoming[i] = N::from_payload(p); });
-    block_sync(sh);
-    for (int index = tid(); index < (group + 1) * half; index += kThreads) {
-        const int head = index / half, pair = index - head * half;
-        const float c = sh.rope_cs[pair], sn = sh.rope_cs[half + pair];
-        const float a = incoming[head * dh + pair], b = incoming[head * dh + pair + half];
-        sh.rotated[head * dh + pair] = N::round(N::round(a * c) - N::round(b * sn));
-        sh.rotated[head * dh + pair + half] = N::round(N::round(b * c) + N::round(a * sn));
-    }
-    for (int index = tid(); index < dh; index += kThreads)
-        sh.vcur[index] = incoming[(group + 1) * dh + index];
-    block_sync(sh);  // incoming is dead: the scores may overwrite the region
-    if (chunk == 0) {
-        for (int index = tid(); index < (group + 1) * dh; index += kThreads) {
-            const float value = sh.rotated[index];
-            if (index < group * dh) {
-                N::store(L.scratch, L.layout.q_rot + first_head * dh + index, value);
-            } else {
-                const size_t e = static_cast<size_t>(position) * kvw + kv_head * dh + (index - group * dh);
-                if constexpr (BF16)
-                    coherent_store16(static_cast<uint16_t*>(key_cache) + e, static_cast<uint16_t>(float_to_bf16_bits(value)));
-                else
-                    coherent_storef(static_cast<float*>(key_cache) + e, value);
+               [&](int i, uint32_t p) {
+                   const float v = N::from_payload(p);
+                   if (i >= qk)
+                       sh.vcur[i - qk] = v;
+                   if constexpr (kRopeInWave)
+                       held = v;  // i == tid(): block <= kThreads
+                   else if (i < qk)
+                       sh.region[i] = v;
+               }, rope_table);
+    if (tid() == 0)
+        sh.rope_position = position;
+    // Chunk 0 stores the rotated K row into the cache and the rotated Q heads into scratch.  Every
+    // load issued so far has returned (the poll waited for its own, which return after them); an
+    // explicit wait says so to the compiler, which would otherwise make later waits for those loads
+    // wait for these stores too.
+    auto store_rotated = [&](int index, float value) {
+        if (index < group * dh) {
+            N::store(L.scratch, L.layout.q_rot + first_head * dh + index, value);
+        } else {
+            const size_t e = static_cast<size_t>(position) * kvw + kv_head * dh + (index - group * dh);
+            if constexpr (BF16)
+                coherent_store16(static_cast<uint16_t*>(key_cache) + e, static_cast<uint16_t>(float_to_bf16_bits(value)));
+            else
+                coherent_storef(static_cast<float*>(key_cache) + e, value);
+        }
+    };
+    if constexpr (kRopeInWave) {
+        static_assert((kMaxGroup + 2) * dh <= kThreads, "one block element per thread");
+        const int t = static_cast<int>(tid());
+        const float partner = __shfl_xor(held, half);  // a wave holds whole heads: dh divides 64
+        const int d = t % dh, pair = d % half;
+        if (t < qk) {
+            const float c = sh.rope_cs[pair], sn = sh.rope_cs[half + pair];
+            const float value = d < half ? N::round(N::round(held * c) - N::round(partner * sn))
+                                         : N::round(N::round(held * c) + N::round(partner * sn));
+            sh.rotated[t] = value;
+            if (chunk == 0) {
+                wait_stores();
+                store_rotated(t, value);
             }
         }
+        block_sync(sh);
+    } else {
+        block_sync(sh);
+        for (int index = tid(); index < (group + 1) * half; index += kThreads) {
+            const int head = index / half, pair = index - head * half;
+            const float c = sh.rope_cs[pair], sn = sh.rope_cs[half + pair];
+            const float a = sh.region[head * dh + pair], b = sh.region[head * dh + pair + half];
+            sh.rotated[head * dh + pair] = N::round(N::round(a * c) - N::round(b * sn));
+            sh.rotated[head * dh + pair + half] = N::round(N::round(b * c) + N::round(a * sn));
+        }
+        block_sync(sh);  // the region is dead: the scores may overwrite it
+        if (chunk == 0)
+            for (int index = tid(); index < qk; index += kThreads)
+                store_rotated(index, sh.rotated[index]);
     }
 
     const float scale = 1.0f / sqrtf(static_cast<float>(dh));
@@ -1027,6 +1082,10 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     // Matrix path: V^T of the PB positions from tile first_tile of the chunk, one column per
     // position; the wave writes its tile wave + 8 j of the block (vb: that tile's rows).
     uint16_t* vt = sh.vt;
+    // Row `dim` of V^T starts at vt_row(dim): every 8 rows are skewed 16 elements further, so that
+    // the 16-bit stores of one instruction (dims 8 apart across its lane groups) fall in distinct
+    // LDS banks; rows stay 16-byte aligned for the operand reads.
+    auto vt_row = [](int dim) { return dim * kVtStride + (dim >> 3) * 16; };
     auto write_vt = [&](int first_tile, int j, const u32x4* vb) {
         const int tile = wave + j * kWaves;
         const int column = tile * kTile + tr;
@@ -1038,8 +1097,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             for (int q = 0; q < 4; ++q) {
                 const uint32_t pair = current ? now[q] : vb[k][q];
                 const int dim = 32 * k + 8 * tk + 2 * q;
-                vt[dim * kVtStride + column] = static_cast<uint16_t>(pair);
-                vt[(dim + 1) * kVtStride + column] = static_cast<uint16_t>(pair >> 16);
+                vt[vt_row(dim) + column] = static_cast<uint16_t>(pair);
+                vt[vt_row(dim + 1) + column] = static_cast<uint16_t>(pair >> 16);
             }
         }
     };
@@ -1225,6 +1284,10 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             stat_sum[wave] = sum;
         }
     }
+    // One chunk on the matrix path publishes straight from the P V accumulators of waves 0-3:
+    // the K row store (and every earlier store) completes before this barrier.
+    if (kMfma && fused)
+        wait_stores();
     block_sync(sh);
 
     const int outputs = group * dh;
@@ -1343,7 +1406,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 #pragma unroll
                 for (int q = 0; q < PB / 32; ++q) {
                     const int t0 = first + 32 * q + 8 * tk;
-                    const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + (16 * n + tr) * kVtStride + 32 * q + 8 * tk);
+                    const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + vt_row(16 * n + tr) + 32 * q + 8 * tk);
                     const u32x4 pa = tr < group ? *reinterpret_cast<const u32x4*>(pbits + tr * span_pad + t0) : zero;
                     o = mfma_16x16x32_bf16(pa, vb, o);
                 }
@@ -1351,7 +1414,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
 #pragma unroll
                 for (int q = 0; q < PB / 32; ++q) {
                     const int t0 = first + 32 * q + 8 * tk;
-                    const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + (16 * n + tr) * kVtStride + 32 * q + 8 * tk);
+                    const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + vt_row(16 * n + tr) + 32 * q + 8 * tk);
                     float p[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
@@ -1360,7 +1423,18 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 }
             }
         }
-        float* results = sh.rotated;  // [group][dh]: the rotated heads are dead
+        if (fused) {
+            // Lanes 0-15 of wave n hold output dims 16 n + l of every head of the group.
+            const uint32_t out_epoch = L.epoch_of(step, layer, kPhaseAttn);
+            if (n < dh / 16 && tk == 0)
+#pragma unroll
+                for (int g = 0; g < MG; ++g)
+                    if (g < group)
+                        publish_element<BF16>(L.exchange + L.xl.attn, (first_head + g) * dh + 16 * n + tr, N::round(o[g]),
+                                              out_epoch);
+            return;
+        }
+        float* results = sh.rotated;  // [group][dh]: the unrotated heads are dead
         if (n < dh / 16 && tk == 0)
 #pragma unroll
             for (int g = 0; g < MG; ++g)
@@ -1917,6 +1991,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
     if (tid() == 0) {
         record = launch;
         sh.aborted = 0;
+        sh.rope_position = -1;
         sh.flag = 0;
         sh.xsave_tag = 0;
         sh.rsave_tag = 0;
