@@ -138,6 +138,17 @@ __device__ inline void issue_fence() { asm volatile("" ::: "memory"); }
 // Waits until every earlier memory operation of the wave completed (s_waitcnt vmcnt(0)).
 __device__ inline void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
 
+// Waits until at most N vector memory operations of the wave are in flight (s_waitcnt vmcnt(N),
+// the other counters untouched).  The compiler takes explicit waits into its own count: where
+// code paths with different loads in flight merge, it otherwise picks counts that are right for
+// one path and make the other wait for loads it does not need.
+template <int N>
+__device__ inline void wait_vmem()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // Device-coherent accesses: relaxed agent-scope atomics, global_load/store ... sc1.
 __device__ inline uint64_t coherent_load64(const uint64_t* p)
 {

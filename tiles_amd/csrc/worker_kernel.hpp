@@ -632,9 +632,18 @@ __device__ __forceinline__ NormScale load_scale(const void* scale, int d)
 // scale[i]) in bf16, x[i] * inv_rms * scale[i] in fp32 (decoder_reference.py:183-187,
 // decoder_stack.py:126-132): into sh.vbits (bf16 bits, the GEMV input) and, for fp32 or when
 // asked, into sh.vec.  Ends with a barrier.
-template <bool BF16>
-__device__ __forceinline__ void rms_apply(const float* x, int d, const NormScale& scale, float eps, Shared& sh,
-                                          bool fp32_copy = false)
+// Scale element i (slot k of the calling thread) for rms_apply: from registers, or (bf16) from
+// the bits a wave left in sh.vbits, read by the thread that then overwrites them.
+struct RegisterScale {
+    const NormScale& scale;
+    __device__ float operator()(int k, int, const Shared&) const { return scale.v[k]; }
+};
+struct LdsScale {
+    __device__ float operator()(int, int i, const Shared& sh) const { return bf16_bits_to_float(sh.vbits[i]); }
+};
+
+template <bool BF16, typename Scale>
+__device__ __forceinline__ void rms_apply(const float* x, int d, Scale scale, float eps, Shared& sh, bool fp32_copy = false)
 {
     float xv[kLdsHidden / kThreads];  // all reads first
 #pragma unroll
@@ -651,7 +660,7 @@ __device__ __forceinline__ void rms_apply(const float* x, int d, const NormScale
     for (int k = 0; k < kLdsHidden / kThreads; ++k) {
         const int i = k * kThreads + static_cast<int>(tid());
         if (i < d) {
-            const float y = Num<BF16>::round(Num<BF16>::round(xv[k] * inv) * scale.v[k]);
+            const float y = Num<BF16>::round(Num<BF16>::round(xv[k] * inv) * scale(k, i, sh));
             if (!BF16 || fp32_copy)
                 sh.vec[i] = y;
             if constexpr (BF16)
@@ -731,7 +740,7 @@ struct NormInput {
     __device__ NormInput(const void* weights, int d) : scale(load_scale<BF16>(weights, d)) {}
     __device__ InputSlice<VPL> operator()(const float* x, Shared& sh, int d, float eps) const
     {
-        rms_apply<BF16>(x, d, scale, eps, sh);
+        rms_apply<BF16>(x, d, RegisterScale{scale}, eps, sh);
         const RowGeometry<BF16> g(d);
         return InputSlice<VPL>(gemv_input<BF16>(sh), g.col, g.lr);
     }
@@ -739,8 +748,8 @@ struct NormInput {
 
 // Dot products of rows [r0, r1) of NM matrices of hidden width with an input vector: prepare()
 // (block-wide) waits for the task's inputs, make_slice() then gives each lane its slice of the
-// vector (InputSlice).  emit(row, dots) runs in each row group's last lane with one dot per
-// matrix.
+// vector (InputSlice).  emit(row, dots), with one dot per matrix, runs once per row after every
+// row is done, in any thread.
 //
 // row_offset(m, row) is the byte offset from `base` of a row of matrix m (below 2 GiB).  D passes
 // of loads are in flight; all D issue before `prepare`, which runs block-wide, waits for the
@@ -782,12 +791,18 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
     issue_fence();
     prepare();
     const InputSlice<VPL> in = make_slice();
+    // Whole groups of D passes without branches (passes past the task compute values nobody
+    // keeps), an explicit wait for each pass's loads with the D - 1 later passes in flight, and no
+    // global store inside the loop: the row results wait in LDS (the work region, free once the
+    // input slice is read) and are emitted afterwards, one row per thread.  Loads and stores share
+    // vmcnt, so a store, or a branch the compiler's count merges over, made each wait a wait for
+    // every load in flight.
+    float* staged = sh.region;  // [row - r0][NM]
     for (int pass0 = 0; active(pass0); pass0 += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
             const int pass = pass0 + s;
-            if (!active(pass))
-                break;
+            wait_vmem<(D - 1) * K>();
             float dots[NM];
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
@@ -797,9 +812,20 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
             issue(pass + D, w[s]);
             const int row = g.first_row(r0, pass) + g.sub;
             if (row < r1 && g.col == g.lr - 1)
-                emit(row, dots);
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+                    staged[(row - r0) * NM + m] = dots[m];
         }
     }
+    block_sync(sh);
+    for (int row = r0 + static_cast<int>(tid()); row < r1; row += kThreads) {
+        float dots[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+            dots[m] = staged[(row - r0) * NM + m];
+        emit(row, dots);
+    }
+    static_assert(kMaxTaskRows * NM <= kLdsRegionFloats, "staged GEMV rows exceed the work region");
     (void)N::kBytes;
 }
 
@@ -1024,7 +1050,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     // wait for these stores too.
     auto store_rotated = [&](int index, float value) {
         if (index < group * dh) {
-            N::store(L.scratch, L.layout.q_rot + first_head * dh + index, value);
+            if (L.block_trace)  // scratch intermediates only on traced launches
+                N::store(L.scratch, L.layout.q_rot + first_head * dh + index, value);
         } else {
             const size_t e = static_cast<size_t>(position) * kvw + kv_head * dh + (index - group * dh);
             if constexpr (BF16)
@@ -1600,7 +1627,7 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
                        sh.vec[i] = N::from_payload(p);
                        sh.vbits[i] = static_cast<uint16_t>(p);
                    });
-        if (begin == 0)
+        if (begin == 0 && L.block_trace)  // scratch intermediates only on traced launches
             for (int i = tid(); i < d; i += kThreads)
                 N::store(L.scratch, L.layout.attention + i, sh.vec[i]);
     };
@@ -1609,7 +1636,8 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
                        [&]() { return InputSlice<VPL>(gemv_input<BF16>(sh), RowGeometry<BF16>(d).col, RowGeometry<BF16>(d).lr); },
                        [&](int row, const float* dots) {
                            const float r = N::round(N::round(dots[0]) + residual[row - begin]);
-                           N::store(L.scratch, L.layout.r + row, r);
+                           if (L.block_trace)
+                               N::store(L.scratch, L.layout.r + row, r);
                            publish_element<BF16>(L.exchange + L.xl.r, row, r, epoch);
                        });
 }
@@ -1639,7 +1667,27 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     const int layer = static_cast<int>(t.layer);
     const int r0 = static_cast<int>(t.begin), r1 = static_cast<int>(t.end);
     const RowGeometry<BF16> g(d);
-    const NormInput<BF16, VPL> norm(L.layer_weight(layer, L.layout.ffn_norm), d);
+    const bool traced = L.block_trace != nullptr;  // scratch intermediates only on traced launches
+    // Waves 1-7 wait for their earlier stores (V cache rows of a QKV task) before their loads, as
+    // the block-wide poll does after its reads, so that every later publish follows those stores.
+    if (g.wave != 0)
+        wait_stores();
+    // The norm's scale.  fp32: every thread's elements in registers.  bf16: wave 0 alone reads it,
+    // ahead of its weights, and leaves it in sh.vbits for rms_apply (LdsScale), so that waves 1-7
+    // have no reads older than their weights to wait for before the norm.
+    const void* norm_weights = L.layer_weight(layer, L.layout.ffn_norm);
+    const NormScale scale = BF16 ? NormScale{} : load_scale<BF16>(norm_weights, d);
+    constexpr int kScaleVectors = VPL;  // bf16: 16-byte vectors of the scale per lane of wave 0
+    u32x4 scale_bits[kScaleVectors];
+    if (BF16 && g.wave == 0) {
+        const int vectors = d / PV, lane = static_cast<int>(tid() & 63);
+#pragma unroll
+        for (int j = 0; j < kScaleVectors; ++j) {
+            const int v = lane + 64 * j;
+            scale_bits[j] = global(static_cast<const u32x4*>(norm_weights))[v < vectors ? v : 0];
+        }
+    }
+    issue_fence();
     auto row_of = [&](int pass) { return g.first_row(r0, pass) + g.sub; };
     const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
     const char* gate = L.layer_weight(layer, L.layout.Wgate) + g.col * 16;
@@ -1661,8 +1709,6 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     };
     u32x4 w[D][NV];
     float squares = 0.0f;  // wave 0 delivers every element of r, and the norm statistic with them
-    // Waves 1-7 wait for their earlier stores (V cache rows of a QKV task) before their loads, as
-    // the block-wide poll does after its reads, so that every later publish follows those stores.
     if (g.wave == 0) {
         issue(0, w[0]);
         issue_fence();
@@ -1676,17 +1722,28 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
         for (int s = 1; s < D; ++s)
             issue(s, w[s]);
     } else {
-        wait_stores();
 #pragma unroll
         for (int s = 0; s < D; ++s)
             issue(s, w[s]);
     }
     issue_fence();
+    if (BF16 && g.wave == 0) {
+        // The poll's reads returned after the scale's (wave 0 issued it first).
+        const int vectors = d / PV, lane = static_cast<int>(tid() & 63);
+#pragma unroll
+        for (int j = 0; j < kScaleVectors; ++j)
+            if (lane + 64 * j < vectors)
+                reinterpret_cast<u32x4*>(sh.vbits)[lane + 64 * j] = scale_bits[j];
+    }
     rms_partial(squares, sh);
     block_sync(sh);
     if (tid() == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
-    const InputSlice<VPL> in = norm(sh.rsave, sh, d, L.numeric.rms_norm_eps);
+    if constexpr (BF16)
+        rms_apply<BF16>(sh.rsave, d, LdsScale{}, L.numeric.rms_norm_eps, sh);
+    else
+        rms_apply<BF16>(sh.rsave, d, RegisterScale{scale}, L.numeric.rms_norm_eps, sh);
+    const InputSlice<VPL> in(gemv_input<BF16>(sh), g.col, g.lr);
     float acc[kOut];
 #pragma unroll
     for (int n = 0; n < kOut; ++n)
@@ -1708,24 +1765,34 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
         const float gr = N::round(gate_dot);
         const float silu = N::round(gr / (1.0f + expf(-gr)));
         const float p = row < r1 ? N::round(silu * N::round(up_dot)) : 0.0f;
-        if (row < r1 && g.col == g.lr - 1)
-            N::store(L.scratch, L.layout.product + row, p);
+        // The product trace waits in LDS: a global store here would make the compiler wait for
+        // every weight load in flight at each later wait (loads and stores share vmcnt).
+        if (traced && row < r1 && g.col == g.lr - 1)
+            sh.small[row - r0] = p;
 #pragma unroll
         for (int k = 0; k < VPL; ++k)
 #pragma unroll
             for (int j = 0; j < PV; ++j)
                 acc[k * PV + j] += N::elem(wd[k], j) * p;
     };
+    // Whole groups of D passes, without branches (a pass past the chunk weighs 0), and an
+    // explicit wait for each pass's loads, the D - 1 later passes staying in flight: with a branch
+    // in the loop the compiler's count, merged at the loop header, waited for every load in flight.
     for (int base = 0; g.first_row(r0, base) < r1; base += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
             const int pass = base + s;
-            if (g.first_row(r0, pass) >= r1)
-                break;
+            wait_vmem<(D - 1) * NV>();
             product_row(&w[s][0], &w[s][VPL], &w[s][2 * VPL], row_of(pass));
             issue(pass + D, w[s]);
         }
     }
+    if (traced)  // the lanes that staged them, after the last weight load
+        for (int pass = 0; g.first_row(r0, pass) < r1; ++pass) {
+            const int row = row_of(pass);
+            if (row < r1 && g.col == g.lr - 1)
+                N::store(L.scratch, L.layout.product + row, sh.small[row - r0]);
+        }
     // Lanes of one wave that hold the same columns (several rows per pass) add up first.
     if (g.lr < 64)
         residue_sum(acc, g.lr);
@@ -1867,7 +1934,7 @@ __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const t
     const int d = hidden_size<BF16, VPL>(L);
     const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
     final_input(L, d, step, sh);
-    rms_apply<BF16>(sh.region, d, scale, L.numeric.rms_norm_eps, sh, true);
+    rms_apply<BF16>(sh.region, d, RegisterScale{scale}, L.numeric.rms_norm_eps, sh, true);
     void* hidden = (L.stack.layers + 1) % 2 == 0 ? L.input : L.output;
     for (int i = static_cast<int>(t.begin) + tid(); i < static_cast<int>(t.end); i += kThreads)
         Num<BF16>::store(hidden, i, sh.vec[i]);
