@@ -100,10 +100,12 @@ typedef struct {
 typedef struct {
     void* input;
     void* output;
-    void* scratch;
+    void* scratch;      /* the launch's intermediates (q_rot, attention, r, product), written only
+                           when block_trace is set: vectors travel through the exchange area */
     void* kv;
     float* logits;
-    float* block_trace;
+    float* block_trace; /* optional: each layer's output of the last step; scratch intermediates
+                           are written only when it is set */
     void* attention_scores;
     float* attention_partials;
     ti_candidate* selection;
