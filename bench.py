@@ -1,21 +1,24 @@
 """Benchmark: bf16 batch-1 greedy decode of a random-init Llama-3.2-1B on one MI355X.
 
-Prints ONE JSON line.  The workload of the headline metric (ms/token of batch-1 bf16 decode):
+Prints ONE JSON line.  The workloads (ms/token of batch-1 bf16 decode):
 
-* ctx 1 (the headline ``value``): 1-token prompt, 256 new tokens, 64 per launch;
-* ctx 4096: 4096 seeded uniform prompt tokens prefilled, then 64 new tokens in one launch
-  (reported under ``ctx4096``).
+* ctx 1 (the headline ``value``): 1-token prompt, 256 new tokens, 64 per persistent launch;
+* ctx 4096 and ctx 32768: a seeded prompt of that length prefilled, then 64 new tokens in one
+  launch (reported under ``ctx4096`` / ``ctx32768``).
 
 Each runs on a package of the same weights planned for its context: 321 positions with the
 planner's default attention chunking (one fused chunk) for ctx 1, 4160 positions in 130-step
-chunks for ctx 4096.
+chunks for ctx 4096, 32832 positions in 1026-step chunks for ctx 32768.
 
-A "step" is one token of decode (one pass of the hot path); ``ms_per_step`` = ``value``
-= ms/token of the generate launches, timed with HIP events on the context stream (prefill,
-setup and readback excluded, as the reference's ``tile_runtime bench``).  The roofline block
-prices the decoder_worker launches against HBM: algorithmic bytes = every weight byte plus
-32 KiB of K/V per visible position per token.  ``cpu_baseline`` times the PyTorch-eager CPU
-oracle (oracle/decoder.py) on the same bf16 weights, on a bounded sample of the same decode.
+A step is one ctx-1 generation of 256 tokens (``--steps`` / ``--warmup`` count them);
+``value`` is ms/token of the generate launches, timed with HIP events on the context stream
+(prefill, setup and readback excluded, as the reference's ``tile_runtime bench``), and
+``ms_per_step`` the same per 256-token step.  The roofline block prices the decoder_worker
+launches against HBM: algorithmic bytes = every weight byte plus 32 KiB of K/V per visible
+position per token; ``traffic`` comes from rocprofv3 counter passes on the same worker sources
+(tiles_amd/counters.py), null when none match.  ``cpu_baseline`` times the PyTorch-eager CPU
+oracle (oracle/decoder.py) on the same weights, on a bounded sample (bf16 and fp32, ctx 1 and
+4096).
 """
 
 from __future__ import annotations
@@ -32,13 +35,14 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+S_BOS = 128000                        # the prompt token of every configuration (Llama-3 BOS)
 WEIGHT_BYTES = 2_471_628_800          # bf16 weights streamed per token: 1,235,814,400 parameters x 2 bytes
 KV_BYTES_PER_POSITION = 32_768        # 16 layers x (K + V) x 8 heads x 64 x 2 bytes
 LM_HEAD_STEP_BYTES = 525_344_768      # 128256 x 2048 bf16 LM-head rows + the hidden vector and final-norm weight
 PEAK_HBM_GBPS = 8000.0                # MI355X published HBM3E bandwidth
-# HBM bytes a ctx-1 generate token moves, measured with rocprofv3 FETCH_SIZE and WRITE_SIZE
-# (calibrated against a known-size read and fill), profiles/decoder_worker_llama1b_bf16_ctx1_hbm_counters.md.
-MEASURED_TRAFFIC_BYTES_PER_TOKEN = 2_690_412_504
+# HBM bytes per generate launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes (tiles_amd/counters.py),
+# used only while they were measured on the current worker sources.
+TRAFFIC_SUMMARY = ROOT / "profiles" / "decoder_worker_hbm_traffic.json"
 
 
 def log(*args) -> None:
@@ -50,49 +54,90 @@ def bytes_per_token(position: int) -> int:
     return WEIGHT_BYTES + (position + 1) * KV_BYTES_PER_POSITION
 
 
-def cpu_baseline(weights: dict, prompt: list[int], tokens: int) -> dict:
-    """The oracle's eager bf16 decode on the host cores: median ms per decoded token."""
+def cpu_threads() -> int:
+    """The host cores this process may run on: its CPU affinity set, capped by OMP_NUM_THREADS
+    when that is set.  A GPU box gives one GPU's job a share of the host (16 threads), whatever
+    os.cpu_count() reports for the whole machine."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(weights: dict, tokens: int) -> dict:
+    """The oracle's eager decode on the host cores: median ms per decoded
+    token of `tokens` greedy steps, in bf16 and fp32, at ctx 1 (after a 1-token prompt) and ctx
+    4096 (after a deterministic synthetic K/V prefix of 4096 positions, uniform in [-1, 1), as the
+    reference's diagnostic context fills for timing, diagnostic_context.cu:89-118)."""
     import torch
 
     from oracle import decoder as ref
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
-    spec = ref.Spec(hidden_size=2048, intermediate_size=8192, num_attention_heads=32, num_key_value_heads=8,
-                    head_dim=64, max_context=len(prompt) + tokens + 1, layers=16, vocab_size=128256)
-    cache = ref.StackCache.empty(spec, torch.bfloat16)
-    samples = []
-    with torch.inference_mode():
-        out = None
-        for token in prompt:
-            out = ref.decode_token(token, weights, spec, cache)
-        for _ in range(tokens):
-            token = ref.greedy(out["logits"])
-            start = time.perf_counter()
-            out = ref.decode_token(token, weights, spec, cache)
-            samples.append((time.perf_counter() - start) * 1e3)
-    ms = statistics.median(samples[1:] if len(samples) > 2 else samples)
-    return {"value": ms, "unit": "ms/token", "cores": threads, "kind": "port",
-            "sample": f"{tokens} greedy bf16 decode steps at ctx 1-{tokens + 1} of the same random-init "
-                      f"Llama-3.2-1B, PyTorch eager CPU oracle (oracle/decoder.py), median after the first"}
+    results = {}
+    for label, dtype in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+        w = weights if dtype is torch.bfloat16 else {k: v.float() for k, v in weights.items()}
+        for ctx in (1, 4096):
+            spec = ref.Spec(hidden_size=2048, intermediate_size=8192, num_attention_heads=32, num_key_value_heads=8,
+                            head_dim=64, max_context=ctx + tokens + 1, layers=16, vocab_size=128256)
+            cache = ref.StackCache.empty(spec, dtype)
+            samples = []
+            with torch.inference_mode():
+                if ctx == 1:
+                    out = ref.decode_token(S_BOS, w, spec, cache)
+                else:
+                    generator = torch.Generator().manual_seed(ctx)
+                    for layer in cache.layers:
+                        for table in (layer.k, layer.v):
+                            table[:ctx] = (torch.rand(table[:ctx].shape, generator=generator) * 2 - 1).to(dtype)
+                        layer.position = ctx
+                    out = ref.decode_token(S_BOS, w, spec, cache)
+                for _ in range(tokens):
+                    token = ref.greedy(out["logits"])
+                    start = time.perf_counter()
+                    out = ref.decode_token(token, w, spec, cache)
+                    samples.append((time.perf_counter() - start) * 1e3)
+            results[f"{label}_ctx{ctx}"] = statistics.median(samples)
+            log(f"cpu baseline {label} ctx {ctx}: {results[f'{label}_ctx{ctx}']:.1f} ms/token")
+        del w
+        gc.collect()
+    return {"value": results["bf16_ctx1"], "unit": "ms/token", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "by_config": results,
+            "sample": f"{tokens} greedy decode steps per configuration (bf16 and fp32; ctx 1 after a 1-token "
+                      f"prompt, ctx 4096 after a synthetic 4096-position K/V prefix) of the same random-init "
+                      f"Llama-3.2-1B, PyTorch eager CPU oracle (oracle/decoder.py), median step time; value is "
+                      f"bf16 at ctx 1"}
 
 
 def main() -> int:
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=4, help="timed 256-token ctx-1 generations")
-    parser.add_argument("--warmup", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=4,
+                        help="timed steps; a step is one ctx-1 generation of 256 tokens (4 persistent launches)")
+    parser.add_argument("--warmup", type=int, default=1, help="untimed steps before them")
     parser.add_argument("--no-ctx4096", action="store_true")
-    parser.add_argument("--cpu-tokens", type=int, default=24)
+    parser.add_argument("--cpu-tokens", type=int, default=24, help="decode steps per CPU-baseline configuration")
     # Each configuration runs on a package planned for its context.  ctx 1 (positions 1-256): a
     # 321-position package with the planner's default chunking, one fused chunk (the planner fuses
     # contexts up to 384 positions).  ctx 4096: 130-step chunks split the 4160-position context
     # into 32 chunks per K/V head, 256 attention tasks for 256 workers (128 would give 33 chunks and
     # two tasks to 8 workers).
     parser.add_argument("--chunk-steps", type=int, default=130, help="attention chunk steps of the ctx-4096 package")
-    parser.add_argument("--ctx32768", action="store_true",
-                        help="also decode 64 tokens at context 32768 (BASELINE config 5: a second package with "
-                             "max_context 32832 and 1026-step attention chunks: 32 per K/V head, one attention task per worker)")
+    parser.add_argument("--no-ctx32768", action="store_true",
+                        help="skip the 64 tokens at context 32768 (BASELINE config 5: a package with max_context 32832 "
+                             "and 1026-step attention chunks: 32 per K/V head, one attention task per worker)")
     parser.add_argument("--write-package", type=Path, default=None,
                         help="only write the ctx-1 package to this directory and its prompt to DIR.ctx1.json "
                              "(for `tiles_amd/tile_runtime bench` under a profiler), then exit")
@@ -157,20 +202,22 @@ def main() -> int:
     log(f"ctx1: {ms_per_token * 1e3:.1f} us/token, floor {floor_ms * 1e3:.1f} us")
 
     # The LM-head step (BASELINE config 2's GEMV: final RMSNorm, 128256 x 2048 bf16 rows, argmax)
-    # inside one decode step: the logits phase of a timeline launch, from the end of the final
-    # norm to the last candidate, against its 525,344,768 bytes.
+    # inside one decode step: the logits wave of a timeline launch, from the first logits task's
+    # start (before it issues its first weight loads) to the last task's end, against its
+    # 525,344,768 bytes.  The span counts the loads issued while the final layer still ran.
     from tiles_amd import timeline as T
     ctx.set_timeline(True)
     ctx.wait(ctx.enqueue_reset())
     ctx.wait(ctx.enqueue_prefill(prompt))
     ctx.wait(ctx.enqueue_generate(64))
     plan_dict = json.loads((work / "llama" / "plan.json").read_text())
-    phases = T.budget(plan_dict, ctx.timeline().reshape(-1, 4), len(prompt) + 63, stream_gbps)["by_opcode"]
+    waves = T.budget(plan_dict, ctx.timeline().reshape(-1, 4), len(prompt) + 63, stream_gbps)["waves"]
     ctx.set_timeline(False)
-    head_us = phases["logits"]["us"]
+    head_us = [w for w in waves if w["opcode"] == "logits"][-1]["span_us"]
     lm_head_step = {"us": head_us, "bytes": LM_HEAD_STEP_BYTES, "GBps": LM_HEAD_STEP_BYTES / (head_us * 1e-6) / 1e9,
                     "fraction_of_stream_read": LM_HEAD_STEP_BYTES / (head_us * 1e-6) / 1e9 / stream_gbps,
-                    "measured": "logits phase of the last step of a 64-token ctx-1 launch (timeline)"}
+                    "measured": "logits wave of the last step of a 64-token ctx-1 launch (timeline): first task "
+                                "start to last task end"}
     log(f"LM-head step: {head_us:.1f} us, {lm_head_step['GBps']:.0f} GB/s")
 
     del ctx, model, plan
@@ -200,7 +247,7 @@ def main() -> int:
         del ctx, model
         gc.collect()
     ctx32768 = None
-    if args.ctx32768:
+    if not args.no_ctx32768:
         long_context = 32768 + 64
         start = time.time()
         S.llama_package(work / "llama32k", long_context, "bfloat16", seed=0, chunk_steps=1026, target=target,
@@ -224,23 +271,26 @@ def main() -> int:
         gc.collect()
     baseline = None
     if args.cpu_tokens > 0:
-        baseline = cpu_baseline(weights, prompt, args.cpu_tokens)
-        log(f"cpu baseline {baseline['value']:.1f} ms/token on {baseline['cores']} threads")
+        baseline = cpu_baseline(weights, args.cpu_tokens)
+    from tiles_amd import counters
+    traffic = counters.load(TRAFFIC_SUMMARY, "ctx1")
     line = {
         "metric": "ms/token bf16 batch-1 decode at ctx 1 & 4096; % of HBM byte floor",
         "value": ms_per_token,
         "unit": "ms/token",
         "n_gpus": 1,
-        "steps": steps * new_tokens,
-        "warmup": args.warmup * new_tokens,
-        "ms_per_step": ms_per_token,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_token * new_tokens,
+        "tokens_per_step": new_tokens,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init N(0,0.02) weights, norm weights 1.0, seed 0)",
         "config": {"workload": "Llama-3.2-1B bf16 batch-1 greedy decode, ctx 1: 1-token prompt, 256 new tokens, "
-                               "64 per persistent launch; ctx 4096 (4096-token prompt, 64 new tokens) under ctx4096",
+                               "64 per persistent launch (one step = one such generation); ctx 4096 and ctx 32768 "
+                               "(prompt of that length, 64 new tokens) under ctx4096 / ctx32768",
                    "global_batch": 1, "seq_len": len(prompt) + new_tokens, "parallelism": "none",
                    "packages": {"ctx1": f"max_context {ctx1_context}, planner default attention chunking "
                                         "(one fused chunk)",
@@ -252,7 +302,7 @@ def main() -> int:
         "fraction_of_floor": floor_ms / ms_per_token,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBPS,
-                     "traffic": MEASURED_TRAFFIC_BYTES_PER_TOKEN * min(new_tokens, 64),
+                     "traffic": traffic["traffic_bytes_per_launch"] if traffic else None,
                      "kernel": "decoder_worker", "launches": launches * steps,
                      "bytes_per_launch": total_bytes / launches, "avg_launch_us": mean_us / launches},
         "ctx4096": ctx4096,
