@@ -192,10 +192,6 @@ __device__ inline u32x4 coherent_load128(__amdgpu_buffer_rsrc_t rsrc, uint32_t o
 {
     return __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 16);
 }
-__device__ inline void coherent_store128(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset, u32x4 v)
-{
-    __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, offset, 0, 16);
-}
 
 // ---------------------------------------------------------------- cross-lane reductions
 //
