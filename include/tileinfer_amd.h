@@ -155,9 +155,18 @@ uint32_t ti_epochs_per_launch(int32_t layers);
 uint32_t ti_epoch_after_generation(uint32_t current, const uint32_t* launch_epochs, int32_t launches,
                                    int32_t generated, int32_t layers);
 
-/* detail::enqueue_worker (launch.cuh:87-88, worker_kernel.cu:240-249): one cooperative launch
- * decoding token.steps ∈ [1, 64] consecutive positions from `position`.  `stream` is a
- * hipStream_t (NULL = default stream).  Stream-ordered, never allocates. */
+/* detail::enqueue_worker (launch.cuh:87-88, worker_kernel.cu:240-249): one persistent launch
+ * decoding token.steps ∈ [1, 64] consecutive positions from `position`, with all
+ * program->workers blocks resident at once (TI_ERR_INVALID_ARGUMENT if the device cannot hold
+ * them).  The reference launches cooperatively; this is an ordinary launch, because on ROCm a
+ * cooperative launch binds a device-wide resource that fails every other process's cooperative
+ * launch while it is held.  `stream` is a hipStream_t (NULL = default stream).  Stream-ordered,
+ * never allocates device memory.  A launch occupies the whole device, so launches from
+ * different streams are ordered: when the device's previous launch came from another stream,
+ * this launch waits on the device for it to complete (one event per device, created on first
+ * use).  Launches made under graph capture are not ordered; the graph's owner orders its
+ * replays.  Blocks held off the device by another process's kernels end the launch with
+ * TI_DEVICE_SYNC_TIMEOUT after the worker's bounded waits, never a hang. */
 int ti_enqueue_worker(void* stream, const ti_worker_program_view* program, const ti_worker_buffers* buffers,
                       int32_t position, ti_token_input token, ti_selection selection);
 

@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -363,19 +364,79 @@ extern "C" int ti_measure_stream_read(size_t bytes, int32_t repeats, double* bes
     return TI_OK;
 }
 
+namespace tiles {
+namespace {
+
+// A worker launch occupies every CU with blocks that wait on each other, so two launches must
+// never be on the device together: dispatched side by side from two queues, each could hold CUs
+// that the other's remaining blocks need, and both would wait out the spin limit.  Launches from
+// different streams of this process (two sequence contexts, say) are therefore ordered here:
+// a launch on stream s waits, on the device, for the last launch of another stream on the same
+// device to complete.  Launches on one stream are ordered by the stream itself.
+struct LaunchOrder {
+    std::mutex mutex;
+    hipEvent_t last = nullptr;      // recorded after the device's latest ordered launch
+    hipStream_t stream = nullptr;   // the stream it was launched on
+};
+constexpr int kOrderedDevices = 64;
+LaunchOrder g_order[kOrderedDevices];
+
+int launch_typed_worker(hipStream_t s, const ti_worker_program_view& program, const ti_worker_buffers& buffers,
+                        int32_t position, ti_token_input token, ti_selection selection)
+{
+    if (program.weight_dtype != TI_DTYPE_BFLOAT16)
+        return launch_worker_f32(s, program, buffers, position, token, selection);
+    return launch_worker_bf16(s, program, buffers, position, token, selection);
+}
+
+} // namespace
+
+int enqueue_worker(hipStream_t s, const ti_worker_program_view& program, const ti_worker_buffers& buffers, int32_t position,
+                   ti_token_input token, ti_selection selection, bool order_streams)
+{
+    if (token.steps < 1 || token.steps > TI_MAX_LAUNCH_STEPS)
+        return fail(TI_ERR_INVALID_ARGUMENT, "invalid worker launch step count");
+    const std::string problem = check_launch_shape(program, buffers, position, token.steps);
+    if (!problem.empty())
+        return fail(TI_ERR_INVALID_ARGUMENT, problem.c_str());
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s, &capture);
+    if (e != hipSuccess)
+        return hip_fail(e, "stream capture status");
+    // A captured launch runs when its graph is replayed; the graph's owner orders it.
+    if (!order_streams || capture != hipStreamCaptureStatusNone)
+        return launch_typed_worker(s, program, buffers, position, token, selection);
+    int device = 0;
+    if ((e = hipGetDevice(&device)) != hipSuccess)
+        return hip_fail(e, "current device");
+    if (device < 0 || device >= kOrderedDevices)
+        return fail(TI_ERR_INVALID_ARGUMENT, "device index beyond the launch-order table");
+    LaunchOrder& order = g_order[device];
+    std::lock_guard<std::mutex> lock(order.mutex);
+    if (!order.last) {
+        if ((e = hipEventCreateWithFlags(&order.last, hipEventDisableTiming)) != hipSuccess) {
+            order.last = nullptr;
+            return hip_fail(e, "launch-order event");
+        }
+    } else if (order.stream != s && (e = hipStreamWaitEvent(s, order.last, 0)) != hipSuccess) {
+        return hip_fail(e, "order after the previous worker launch");
+    }
+    const int code = launch_typed_worker(s, program, buffers, position, token, selection);
+    if (code != TI_OK)
+        return code;
+    if ((e = hipEventRecord(order.last, s)) != hipSuccess)
+        return hip_fail(e, "record worker launch");
+    order.stream = s;
+    return TI_OK;
+}
+
+} // namespace tiles
+
 extern "C" int ti_enqueue_worker(void* stream, const ti_worker_program_view* program, const ti_worker_buffers* buffers,
                                  int32_t position, ti_token_input token, ti_selection selection)
 {
     using namespace tiles;
     if (!program || !buffers)
         return fail(TI_ERR_INVALID_ARGUMENT, "null program or buffers");
-    if (token.steps < 1 || token.steps > TI_MAX_LAUNCH_STEPS)
-        return fail(TI_ERR_INVALID_ARGUMENT, "invalid worker launch step count");
-    const std::string problem = check_launch_shape(*program, *buffers, position, token.steps);
-    if (!problem.empty())
-        return fail(TI_ERR_INVALID_ARGUMENT, problem.c_str());
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (program->weight_dtype != TI_DTYPE_BFLOAT16)
-        return launch_worker_f32(s, *program, *buffers, position, token, selection);
-    return launch_worker_bf16(s, *program, *buffers, position, token, selection);
+    return enqueue_worker(static_cast<hipStream_t>(stream), *program, *buffers, position, token, selection, true);
 }

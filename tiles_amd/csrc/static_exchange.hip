@@ -97,7 +97,8 @@ extern "C" int ti_enqueue_worker_static(void* stream, const ti_worker_program_vi
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return hip_fail(e, "clear static exchange");
-    code = ti_enqueue_worker(stream, program, &b, position, token, selection);
+    // Callers of this entry order their launches themselves (and it creates no event to do so).
+    code = enqueue_worker(s, *program, b, position, token, selection, false);
     if (code != TI_OK)
         return code;
     if (sync_timeout) {

@@ -186,6 +186,10 @@ int launch_worker_bf16(hipStream_t stream, const ti_worker_program_view& p, cons
                        ti_token_input token, ti_selection selection);
 int launch_worker_f32(hipStream_t stream, const ti_worker_program_view& p, const ti_worker_buffers& b, int position,
                       ti_token_input token, ti_selection selection);
+// Checked worker launch.  With order_streams, a launch waits on the device for the device's last
+// launch from another stream to complete (two launches cannot share the device).
+int enqueue_worker(hipStream_t s, const ti_worker_program_view& program, const ti_worker_buffers& buffers, int32_t position,
+                   ti_token_input token, ti_selection selection, bool order_streams);
 std::vector<const void*> worker_functions_bf16();
 std::vector<const void*> worker_functions_f32();
 

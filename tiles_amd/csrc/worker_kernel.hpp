@@ -1,4 +1,4 @@
-// MI355X (gfx950) decode worker: one persistent cooperative kernel per launch that runs
+// MI355X (gfx950) decode worker: one persistent kernel per launch, all of whose blocks are resident, that runs
 // every worker's instruction stream once per token for up to 64 tokens, with on-GPU greedy
 // selection (replaces tileinfer/src/runtime/worker_kernel.cu and ops.cuh).
 //
@@ -24,6 +24,7 @@
 // (docs/architecture.md:284-312; ops.cuh sites cited per function).
 #pragma once
 
+#include <atomic>
 #include <string>
 #include <vector>
 
@@ -35,6 +36,7 @@ namespace tiles {
 namespace {
 
 constexpr int kWaves = kThreads / 64;
+constexpr int kResidencyDevices = 64;
 constexpr int kBlockThreads = kThreads;
 constexpr int kLdsHidden = kMaxHidden;
 constexpr int kLdsRegionFloats = kRegionFloats;
@@ -2176,11 +2178,36 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     L.inv_group = 1.0f / static_cast<float>(L.group);
     L.hidden_stride = row_stride(p.shape.hidden_size, p.workers);
     L.qkv_stride = row_stride(p.shape.hidden_size + 2 * p.shape.kv_heads * p.shape.head_dim, p.workers);
-    void* args[] = {&L};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decoder_worker<BF16, VPL, LRK>),
-                                                    dim3(p.workers), dim3(kBlockThreads), args, 0, stream);
+    // Every worker waits on the others, so all p.workers blocks must be resident at once: at most
+    // CUs x resident blocks per CU, found once per device.  The launch is an ordinary one.  A
+    // cooperative launch would check the same bound, but on this runtime it also binds a
+    // device-wide resource to the process's queue, and while one process holds it every other
+    // process's cooperative launch fails (hipErrorIllegalState): a host running the tile_runtime
+    // CLI beside its own context could not decode.  Nothing in the worker needs that resource;
+    // its waits are the exchange polls, bounded by kSpinLimit, so blocks held off the device by
+    // another process's kernels end the launch with TI_DEVICE_SYNC_TIMEOUT instead of a hang.
+    const void* function = reinterpret_cast<const void*>(&decoder_worker<BF16, VPL, LRK>);
+    static std::atomic<int> resident[kResidencyDevices] = {};
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess)
-        return hip_fail(e, "cooperative worker launch");
+        return hip_fail(e, "current device");
+    if (device < 0 || device >= kResidencyDevices)
+        return fail(TI_ERR_INVALID_ARGUMENT, "device index beyond the worker residency table");
+    if (resident[device].load(std::memory_order_relaxed) == 0) {
+        int cus = 0, per_cu = 0;
+        if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess)
+            return hip_fail(e, "CU count");
+        if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, function, kBlockThreads, 0)) != hipSuccess)
+            return hip_fail(e, "worker occupancy");
+        resident[device].store(cus * per_cu, std::memory_order_relaxed);
+    }
+    if (p.workers > resident[device].load(std::memory_order_relaxed))
+        return fail(TI_ERR_INVALID_ARGUMENT, "more workers than the device holds resident at once");
+    void* args[] = {&L};
+    e = hipLaunchKernel(function, dim3(p.workers), dim3(kBlockThreads), args, 0, stream);
+    if (e != hipSuccess)
+        return hip_fail(e, "worker launch");
     return TI_OK;
 }
 } // namespace
