@@ -149,6 +149,17 @@ __device__ inline void wait_vmem()
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// f(std::integral_constant<int, I>{}) for I = 0 .. N - 1, in order: an unrolled loop whose index
+// is a constant expression in the body (a template argument of wait_vmem, say).
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void unroll(const F& f)
+{
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        unroll<N, I + 1>(f);
+    }
+}
+
 // Device-coherent accesses: relaxed agent-scope atomics, global_load/store ... sc1.
 __device__ inline uint64_t coherent_load64(const uint64_t* p)
 {

@@ -794,31 +794,41 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
     prepare();
     const InputSlice<VPL> in = make_slice();
     // Whole groups of D passes without branches (passes past the task compute values nobody
-    // keeps), an explicit wait for each pass's loads with the D - 1 later passes in flight, and no
+    // keeps), an explicit wait for each pass's loads with the later passes in flight, and no
     // global store inside the loop: the row results wait in LDS (the work region, free once the
     // input slice is read) and are emitted afterwards, one row per thread.  Loads and stores share
     // vmcnt, so a store, or a branch the compiler's count merges over, made each wait a wait for
-    // every load in flight.
+    // every load in flight.  Every group but the last issues the next group's passes; the last
+    // issues nothing, so that no load is in flight when the rows are emitted (loads past the task
+    // issued at its end made the first publish wait a whole memory round trip for them).
     float* staged = sh.region;  // [row - r0][NM]
-    for (int pass0 = 0; active(pass0); pass0 += D) {
+    auto compute = [&](int s, int pass) {
+        float dots[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const float part = in.template dot<BF16>(&w[s][m * VPL]);
+            dots[m] = VPL > 1 ? group_sum<64>(part) : group_sum(part, g.lr);
+        }
+        const int row = g.first_row(r0, pass) + g.sub;
+        if (row < r1 && g.col == g.lr - 1)
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+                staged[(row - r0) * NM + m] = dots[m];
+    };
+    int pass0 = 0;
+    for (; active(pass0 + D); pass0 += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
-            const int pass = pass0 + s;
             wait_vmem<(D - 1) * K>();
-            float dots[NM];
-#pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                const float part = in.template dot<BF16>(&w[s][m * VPL]);
-                dots[m] = VPL > 1 ? group_sum<64>(part) : group_sum(part, g.lr);
-            }
-            issue(pass + D, w[s]);
-            const int row = g.first_row(r0, pass) + g.sub;
-            if (row < r1 && g.col == g.lr - 1)
-#pragma unroll
-                for (int m = 0; m < NM; ++m)
-                    staged[(row - r0) * NM + m] = dots[m];
+            compute(s, pass0 + s);
+            issue(pass0 + s + D, w[s]);
         }
     }
+    unroll<D>([&](auto step) {
+        constexpr int s = decltype(step)::value;
+        wait_vmem<(D - 1 - s) * K>();
+        compute(s, pass0 + s);
+    });
     block_sync(sh);
     for (int row = r0 + static_cast<int>(tid()); row < r1; row += kThreads) {
         float dots[NM];
@@ -1453,7 +1463,11 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             }
         }
         if (fused) {
-            // Lanes 0-15 of wave n hold output dims 16 n + l of every head of the group.
+            // Lanes 0-15 of wave n hold output dims 16 n + l of every head of the group.  The
+            // last block loaded no next V tiles, so nothing is in flight; saying so lets the
+            // stores issue back to back (the compiler otherwise made each wait for the store
+            // before the previous one, assuming a V tile load might still be pending).
+            wait_vmem<0>();
             const uint32_t out_epoch = L.epoch_of(step, layer, kPhaseAttn);
             if (n < dh / 16 && tk == 0)
 #pragma unroll
@@ -1778,9 +1792,11 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
                 acc[k * PV + j] += N::elem(wd[k], j) * p;
     };
     // Whole groups of D passes, without branches (a pass past the chunk weighs 0), and an
-    // explicit wait for each pass's loads, the D - 1 later passes staying in flight: with a branch
-    // in the loop the compiler's count, merged at the loop header, waited for every load in flight.
-    for (int base = 0; g.first_row(r0, base) < r1; base += D) {
+    // explicit wait for each pass's loads, the later passes staying in flight: with a branch in
+    // the loop the compiler's count, merged at the loop header, waited for every load in flight.
+    // The last group issues nothing, so no load past the chunk delays the publication.
+    int base = 0;
+    for (; g.first_row(r0, base + D) < r1; base += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
             const int pass = base + s;
@@ -1789,6 +1805,11 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
             issue(pass + D, w[s]);
         }
     }
+    unroll<D>([&](auto step) {
+        constexpr int s = decltype(step)::value;
+        wait_vmem<(D - 1 - s) * NV>();
+        product_row(&w[s][0], &w[s][VPL], &w[s][2 * VPL], row_of(base + s));
+    });
     if (traced)  // the lanes that staged them, after the last weight load
         for (int pass = 0; g.first_row(r0, pass) < r1; ++pass) {
             const int row = row_of(pass);
