@@ -1145,11 +1145,15 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     if constexpr (kMfma) {
         // A: query head tr (zero past the group); the current K row stands in for the
         // position's own tile row.
+        // Rows past the group read head 0 (one address per tk, a broadcast) and take zeros:
+        // reading row tr put the 16 rows, 256 bytes apart, on the same LDS banks.
         u32x4 qa[KS], kc[KS];
         const u32x4 zero = {0u, 0u, 0u, 0u};
+        const int qrow = tr < group ? tr : 0;
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
-            qa[k] = tr < group ? pack8(sh.rotated + tr * dh + 32 * k + 8 * tk) : zero;
+            const u32x4 q = pack8(sh.rotated + qrow * dh + 32 * k + 8 * tk);
+            qa[k] = tr < group ? q : zero;
             kc[k] = pack8(sh.rotated + group * dh + 32 * k + 8 * tk);
         }
         auto tile_scores = [&](int tile, const u32x4* kb) {
@@ -1446,7 +1450,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 for (int q = 0; q < PB / 32; ++q) {
                     const int t0 = first + 32 * q + 8 * tk;
                     const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + vt_row(16 * n + tr) + 32 * q + 8 * tk);
-                    const u32x4 pa = tr < group ? *reinterpret_cast<const u32x4*>(pbits + tr * span_pad + t0) : zero;
+                    const u32x4 p = *reinterpret_cast<const u32x4*>(pbits + (tr < group ? tr : 0) * span_pad + t0);
+                    const u32x4 pa = tr < group ? p : zero;
                     o = mfma_16x16x32_bf16(pa, vb, o);
                 }
             } else if (n < dh / 16) {
