@@ -130,6 +130,15 @@ __device__ __forceinline__ int hidden_size(const Launch<BF16>& L)
     return VPL > 1 ? VPL * 64 * Num<BF16>::kPerVec : L.shape.hidden_size;
 }
 
+// Elements of a hidden-size vector per thread (an upper bound, exact when VPL > 1): the launcher
+// admits at most VPL 16-byte vectors per lane of a row.  Per-element loops over the vector run
+// this many times, not kMaxHidden / kThreads.
+template <bool BF16, int VPL>
+constexpr int hidden_slots()
+{
+    return (VPL * 64 * Num<BF16>::kPerVec + kThreads - 1) / kThreads;
+}
+
 // bf16 elements of the attention's V^T block: head_dim rows of (block positions + 8).  It
 // shares LDS with the input vector.  A block holds the most positions (a multiple of 32, at most
 // 160) whose rows fit.
@@ -539,7 +548,7 @@ __device__ __forceinline__ void rms_partial(float squares, Shared& sh)
 // The hidden state a layer reads, into dst (FP32): the token's embedding row for a stack's
 // first layer, the host-written input of a block package, or the previous layer's output.
 // A copy stays in sh.xsave for the layer's residual addition.
-template <bool BF16>
+template <bool BF16, int kSlots>
 __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int d, int layer, int step, ti_token_id token, Shared& sh)
 {
     float squares = 0.0f;  // the RMSNorm statistic over the elements this thread delivers
@@ -551,14 +560,14 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int d, int la
                               ? static_cast<const void*>(L.stack_weight(static_cast<size_t>(L.stack.embedding_offset) +
                                                                         static_cast<size_t>(id) * d))
                               : L.input;
-        float v[kLdsHidden / kThreads];
+        float v[kSlots];
 #pragma unroll
-        for (int k = 0; k < kLdsHidden / kThreads; ++k) {  // all loads in flight together
+        for (int k = 0; k < kSlots; ++k) {  // all loads in flight together
             const int i = k * kThreads + static_cast<int>(tid());
             v[k] = Num<BF16>::load(row, i < d ? i : 0);
         }
 #pragma unroll
-        for (int k = 0; k < kLdsHidden / kThreads; ++k) {
+        for (int k = 0; k < kSlots; ++k) {
             const int i = k * kThreads + static_cast<int>(tid());
             if (i < d) {
                 sh.xsave[i] = v[k];
@@ -610,18 +619,19 @@ __device__ __forceinline__ float attention_output_element(const Launch<BF16>& L,
 
 // A norm's scale elements tid() + k * kThreads, loaded into registers before the task
 // waits for its input (a load issued after the wait would add a full memory latency).
+template <int kSlots>
 struct NormScale {
-    float v[kLdsHidden / kThreads];
+    float v[kSlots];
 };
 
-template <bool BF16>
-__device__ __forceinline__ NormScale load_scale(const void* scale, int d)
+template <bool BF16, int kSlots>
+__device__ __forceinline__ NormScale<kSlots> load_scale(const void* scale, int d)
 {
     // Unconditional loads (lanes past d re-read element d - 1, never used): a select on a
     // loaded value would make the load's wait immediate.
-    NormScale s;
+    NormScale<kSlots> s;
 #pragma unroll
-    for (int k = 0; k < kLdsHidden / kThreads; ++k) {
+    for (int k = 0; k < kSlots; ++k) {
         const int i = k * kThreads + static_cast<int>(tid());
         s.v[k] = Num<BF16>::load(scale, i < d ? i : d - 1);
     }
@@ -636,20 +646,21 @@ __device__ __forceinline__ NormScale load_scale(const void* scale, int d)
 // asked, into sh.vec.  Ends with a barrier.
 // Scale element i (slot k of the calling thread) for rms_apply: from registers, or (bf16) from
 // the bits a wave left in sh.vbits, read by the thread that then overwrites them.
+template <int kSlots>
 struct RegisterScale {
-    const NormScale& scale;
+    const NormScale<kSlots>& scale;
     __device__ float operator()(int k, int, const Shared&) const { return scale.v[k]; }
 };
 struct LdsScale {
     __device__ float operator()(int, int i, const Shared& sh) const { return bf16_bits_to_float(sh.vbits[i]); }
 };
 
-template <bool BF16, typename Scale>
+template <bool BF16, int kSlots, typename Scale>
 __device__ __forceinline__ void rms_apply(const float* x, int d, Scale scale, float eps, Shared& sh, bool fp32_copy = false)
 {
-    float xv[kLdsHidden / kThreads];  // all reads first
+    float xv[kSlots];  // all reads first
 #pragma unroll
-    for (int k = 0; k < kLdsHidden / kThreads; ++k) {
+    for (int k = 0; k < kSlots; ++k) {
         const int i = k * kThreads + static_cast<int>(tid());
         xv[k] = x[i < d ? i : 0];
     }
@@ -659,7 +670,7 @@ __device__ __forceinline__ void rms_apply(const float* x, int d, Scale scale, fl
     const float total = ((((((s0.x + s0.y) + s0.z) + s0.w) + s1.x) + s1.y) + s1.z) + s1.w;
     const float inv = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
 #pragma unroll
-    for (int k = 0; k < kLdsHidden / kThreads; ++k) {
+    for (int k = 0; k < kSlots; ++k) {
         const int i = k * kThreads + static_cast<int>(tid());
         if (i < d) {
             const float y = Num<BF16>::round(Num<BF16>::round(xv[k] * inv) * scale(k, i, sh));
@@ -738,11 +749,12 @@ struct InputSlice {
 // sh.small), then the lane's slice from LDS.
 template <bool BF16, int VPL>
 struct NormInput {
-    NormScale scale;
-    __device__ NormInput(const void* weights, int d) : scale(load_scale<BF16>(weights, d)) {}
+    static constexpr int kSlots = hidden_slots<BF16, VPL>();
+    NormScale<kSlots> scale;
+    __device__ NormInput(const void* weights, int d) : scale(load_scale<BF16, kSlots>(weights, d)) {}
     __device__ InputSlice<VPL> operator()(const float* x, Shared& sh, int d, float eps) const
     {
-        rms_apply<BF16>(x, d, RegisterScale{scale}, eps, sh);
+        rms_apply<BF16, kSlots>(x, d, RegisterScale<kSlots>{scale}, eps, sh);
         const RowGeometry<BF16> g(d);
         return InputSlice<VPL>(gemv_input<BF16>(sh), g.col, g.lr);
     }
@@ -875,7 +887,7 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
         return (region + (static_cast<uint32_t>(row) - first) * static_cast<uint32_t>(d)) * N::kBytes;
     };
     const NormInput<BF16, VPL> norm(L.layer_weight(layer, L.layout.attn_norm), d);
-    auto prepare = [&]() { load_hidden(L, d, layer, step, token, sh); };
+    auto prepare = [&]() { load_hidden<BF16, hidden_slots<BF16, VPL>()>(L, d, layer, step, token, sh); };
     auto make_slice = [&]() { return norm(sh.xsave, sh, d, L.numeric.rms_norm_eps); };
     float* staged_v = sh.small;  // this task's V rows, for the cache stores after the GEMV
     // Read once into registers: inside the row loop every field of the LDS launch record would be
@@ -1697,7 +1709,8 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     // ahead of its weights, and leaves it in sh.vbits for rms_apply (LdsScale), so that waves 1-7
     // have no reads older than their weights to wait for before the norm.
     const void* norm_weights = L.layer_weight(layer, L.layout.ffn_norm);
-    const NormScale scale = BF16 ? NormScale{} : load_scale<BF16>(norm_weights, d);
+    constexpr int kSlots = hidden_slots<BF16, VPL>();
+    const NormScale<kSlots> scale = BF16 ? NormScale<kSlots>{} : load_scale<BF16, kSlots>(norm_weights, d);
     constexpr int kScaleVectors = VPL;  // bf16: 16-byte vectors of the scale per lane of wave 0
     u32x4 scale_bits[kScaleVectors];
     if (BF16 && g.wave == 0) {
@@ -1761,9 +1774,9 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     if (tid() == 0)
         sh.rsave_tag = L.epoch_of(step, layer, kPhaseR);
     if constexpr (BF16)
-        rms_apply<BF16>(sh.rsave, d, LdsScale{}, L.numeric.rms_norm_eps, sh);
+        rms_apply<BF16, kSlots>(sh.rsave, d, LdsScale{}, L.numeric.rms_norm_eps, sh);
     else
-        rms_apply<BF16>(sh.rsave, d, RegisterScale{scale}, L.numeric.rms_norm_eps, sh);
+        rms_apply<BF16, kSlots>(sh.rsave, d, RegisterScale<kSlots>{scale}, L.numeric.rms_norm_eps, sh);
     const InputSlice<VPL> in(gemv_input<BF16>(sh), g.col, g.lr);
     float acc[kOut];
 #pragma unroll
@@ -1960,9 +1973,10 @@ template <bool BF16, int VPL>
 __device__ __forceinline__ void op_final_rms_norm(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     const int d = hidden_size<BF16, VPL>(L);
-    const NormScale scale = load_scale<BF16>(L.stack_weight(L.stack.final_norm_offset), d);
+    constexpr int kSlots = hidden_slots<BF16, VPL>();
+    const NormScale<kSlots> scale = load_scale<BF16, kSlots>(L.stack_weight(L.stack.final_norm_offset), d);
     final_input(L, d, step, sh);
-    rms_apply<BF16>(sh.region, d, RegisterScale{scale}, L.numeric.rms_norm_eps, sh, true);
+    rms_apply<BF16, kSlots>(sh.region, d, RegisterScale<kSlots>{scale}, L.numeric.rms_norm_eps, sh, true);
     void* hidden = (L.stack.layers + 1) % 2 == 0 ? L.input : L.output;
     for (int i = static_cast<int>(t.begin) + tid(); i < static_cast<int>(t.end); i += kThreads)
         Num<BF16>::store(hidden, i, sh.vec[i]);
