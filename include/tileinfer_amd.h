@@ -255,6 +255,12 @@ int ti_context_collect_intermediates(ti_context* context, const ti_ticket* ticke
  * instruction order) after waiting for the context's queued work; `count` receives the number
  * of instructions. */
 int ti_context_set_timeline(ti_context* context, int32_t enabled);
+/* No counterpart in the reference, which prefills one position per worker step and lists a
+ * matrix prefill as an open question (docs/development.md:331).  With it on (the default), a
+ * prefill of more than 64 tokens on a bf16 decoder stack runs all but its last token through
+ * each layer as matrices (rocBLAS GEMMs and row kernels following the same rounding points),
+ * then the worker decodes the last token.  Off: every token goes through the worker. */
+int ti_context_set_matrix_prefill(ti_context* context, int32_t enabled);
 int ti_context_timeline(ti_context* context, uint64_t* words, size_t capacity, size_t* count);
 void ti_ticket_free(ti_ticket* ticket);
 

@@ -20,8 +20,8 @@ LIBRARY = PACKAGE / "libtileinfer_amd.so"
 CLI = PACKAGE / "tile_runtime"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["worker_bf16.hip", "worker_f32.hip", "launch.hip", "static_exchange.hip", "plan.cpp", "runtime.cpp",
-           "json.cpp", "sha256.cpp"]
+SOURCES = ["worker_bf16.hip", "worker_f32.hip", "launch.hip", "static_exchange.hip", "prefill.hip", "plan.cpp",
+           "runtime.cpp", "json.cpp", "sha256.cpp"]
 # Packed-FP32 instructions are kept out of every GPU code object (a known-bad form on this pool).
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", f"-I{ROOT / 'include'}", f"-I{CSRC}",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument"]
@@ -46,7 +46,9 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as pool:
         objects = list(pool.map(_object, SOURCES))
     temporary = LIBRARY.with_suffix(".so.tmp")
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(temporary), *map(str, objects)])
+    # rocBLAS supplies the matrix prefill's plain GEMMs (prefill.hip).
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(temporary), *map(str, objects), "-L/opt/rocm/lib",
+          "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"])
     os.replace(temporary, LIBRARY)
     cli_object = _object("main.cpp")
     _run([HIPCC, "--offload-arch=gfx950", "-o", str(CLI), str(cli_object), f"-L{PACKAGE}", "-ltileinfer_amd",

@@ -1,0 +1,387 @@
+// Matrix prefill of a bf16 decoder stack.  The reference prefills a prompt one position per
+// worker step and leaves a matrix prefill as an open question (docs/development.md:331); this
+// one runs up to kChunkRows positions through each layer at once.  Its arithmetic is the
+// reference's full causal block (decoder_reference.py:273-312, recompute_prefix) with every
+// rounding point of the decode path (docs/architecture.md:284-312), so that the cache rows it
+// writes are the ones a position-by-position prefill writes, up to the FP32 summation order of
+// the dot products:
+//
+//   u = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * attn_norm)      rms_rows
+//   q, k, v = bf16(W u)                                          rocBLAS GEMM (bf16 in/out, FP32 sums)
+//   q, k rotated as the worker rotates them; K, V rows -> cache  rope_rows
+//   s = bf16(bf16(q . k) / sqrt(dh)); P = bf16(exp(s - M) / S)   attention_rows (causal, exact
+//   attention = bf16(sum P v)                                    softmax statistics per row)
+//   r = bf16(bf16(Wo attention) + x)                             GEMM, add_rows
+//   z = RMSNorm(r) with ffn_norm                                 rms_rows
+//   p = bf16(bf16(silu(bf16(Wgate z))) * bf16(Wup z))            GEMMs, silu_rows
+//   y = bf16(bf16(Wdown p) + r)                                  GEMM, add_rows
+//
+// The GEMMs are plain library GEMMs (rocBLAS, bf16 inputs and outputs, FP32 accumulation);
+// everything around them is these kernels.
+#include "prefill.hpp"
+
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <string>
+
+#include "device_common.hpp"
+#include "worker_config.hpp"
+
+namespace tiles {
+namespace {
+
+using Bf = Num<true>;
+constexpr int kRowThreads = 256;
+constexpr int kTile = 64;  // key positions per attention tile
+
+__device__ inline float bf(uint16_t bits) { return bf16_bits_to_float(bits); }
+__device__ inline uint16_t bits16(float v) { return static_cast<uint16_t>(float_to_bf16_bits(v)); }
+
+// Sum over the block's threads (kRowThreads), in a fixed order.
+__device__ float block_sum(float v, float* partial)
+{
+    for (int offset = 32; offset > 0; offset >>= 1)
+        v += __shfl_xor(v, offset);
+    if ((threadIdx.x & 63) == 0)
+        partial[threadIdx.x / 64] = v;
+    __syncthreads();
+    float total = 0.0f;
+    for (int w = 0; w < kRowThreads / 64; ++w)
+        total += partial[w];
+    __syncthreads();
+    return total;
+}
+
+// x[r] = the embedding row of tokens[r].
+__global__ void __launch_bounds__(kRowThreads) gather_rows(const uint16_t* embedding, const ti_token_id* tokens, int d,
+                                                           uint16_t* x)
+{
+    const uint16_t* src = embedding + static_cast<size_t>(tokens[blockIdx.x]) * d;
+    uint16_t* dst = x + static_cast<size_t>(blockIdx.x) * d;
+    for (int i = threadIdx.x; i < d; i += kRowThreads)
+        dst[i] = src[i];
+}
+
+// out[r] = bf16(bf16(x[r] * inv_rms) * scale), inv_rms = 1 / sqrt(mean(x[r]^2) + eps) in FP32,
+// as the worker's rms_apply computes it.
+__global__ void __launch_bounds__(kRowThreads) rms_rows(const uint16_t* x, const uint16_t* scale, int d, float eps,
+                                                        uint16_t* out)
+{
+    __shared__ float partial[kRowThreads / 64];
+    const uint16_t* row = x + static_cast<size_t>(blockIdx.x) * d;
+    float squares = 0.0f;
+    for (int i = threadIdx.x; i < d; i += kRowThreads) {
+        const float v = bf(row[i]);
+        squares = fmaf(v, v, squares);
+    }
+    const float total = block_sum(squares, partial);
+    const float inv = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
+    uint16_t* dst = out + static_cast<size_t>(blockIdx.x) * d;
+    for (int i = threadIdx.x; i < d; i += kRowThreads)
+        dst[i] = bits16(Bf::round(Bf::round(bf(row[i]) * inv) * bf(scale[i])));
+}
+
+// Row r of qkv ([q heads | k heads | v heads], bf16) at position `position + r`: the query and
+// key heads rotated (split halves; cos and sin of position * frequency rounded to bf16, each
+// product rounded, then the difference or sum), the query heads to q_rot, the key and value
+// heads to the cache row of the position.
+__global__ void __launch_bounds__(kRowThreads) rope_rows(const uint16_t* qkv, int position, const float* frequencies, int nq,
+                                                         int nkv, int dh, uint16_t* q_rot, uint16_t* key_cache,
+                                                         uint16_t* value_cache)
+{
+    const int r = blockIdx.x;
+    const int pos = position + r;
+    const int half = dh / 2;
+    const uint16_t* src = qkv + static_cast<size_t>(r) * (nq + 2 * nkv) * dh;
+    for (int index = threadIdx.x; index < (nq + nkv) * half; index += kRowThreads) {
+        const int head = index / half, pair = index - head * half;
+        const float angle = static_cast<float>(pos) * frequencies[pair];
+        const float c = Bf::round(cosf(angle)), s = Bf::round(sinf(angle));
+        const float a = bf(src[head * dh + pair]), b = bf(src[head * dh + pair + half]);
+        const uint16_t lo = bits16(Bf::round(Bf::round(a * c) - Bf::round(b * s)));
+        const uint16_t hi = bits16(Bf::round(Bf::round(b * c) + Bf::round(a * s)));
+        uint16_t* dst = head < nq ? q_rot + (static_cast<size_t>(r) * nq + head) * dh
+                                  : key_cache + (static_cast<size_t>(pos) * nkv + head - nq) * dh;
+        dst[pair] = lo;
+        dst[pair + half] = hi;
+    }
+    for (int index = threadIdx.x; index < nkv * dh; index += kRowThreads)
+        value_cache[static_cast<size_t>(pos) * nkv * dh + index] = src[(nq + nkv) * dh + index];
+}
+
+// Causal attention of row r (position `position + r`) for the query heads of K/V head h: one
+// wave per query head of the group.  Pass 1 finds each head's maximum score M and
+// S = sum exp(s - M) over positions 0..pos, a tile of 64 positions (one per lane) at a time,
+// rescaling S when M grows; pass 2 recomputes the scores, rounds P = exp(s - M) / S to bf16 and
+// adds P V in FP32 through LDS, and the result is rounded once.
+template <int DH>
+__global__ void __launch_bounds__(kRowThreads) attention_rows(const uint16_t* q_rot, int position, int nq, int nkv,
+                                                              const uint16_t* key_cache, const uint16_t* value_cache,
+                                                              float scale, uint16_t* out)
+{
+    constexpr int kPairs = DH / 2;
+    constexpr int kVectors = DH / 8;  // 16-byte vectors of a K or V row
+    __shared__ float probability[kMaxGroup][kTile];
+    __shared__ uint16_t values[kTile][DH];
+    const int r = blockIdx.x / nkv, h = blockIdx.x - r * nkv;
+    const int group = nq / nkv;
+    const int pos = position + r;
+    const int length = pos + 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x / 64;
+    const int head = h * group + (wave < group ? wave : 0);
+    // The lane's copy of its head's query as packed bf16 pairs.
+    uint32_t q[kPairs];
+    const uint32_t* qsrc = reinterpret_cast<const uint32_t*>(q_rot + (static_cast<size_t>(r) * nq + head) * DH);
+#pragma unroll
+    for (int j = 0; j < kPairs; ++j)
+        q[j] = qsrc[j];
+    auto score = [&](int t) {
+        const u32x4* krow = reinterpret_cast<const u32x4*>(key_cache + (static_cast<size_t>(t) * nkv + h) * DH);
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kVectors; ++v) {
+            const u32x4 k = krow[v];
+            a = dot2_bf16(k[0], q[4 * v], a);
+            b = dot2_bf16(k[1], q[4 * v + 1], b);
+            a = dot2_bf16(k[2], q[4 * v + 2], a);
+            b = dot2_bf16(k[3], q[4 * v + 3], b);
+        }
+        return Bf::round(Bf::round(a + b) * scale);
+    };
+    float m = -INFINITY, total = 0.0f;
+    if (wave < group)
+        for (int base = 0; base < length; base += kTile) {
+            const int t = base + lane;
+            const float s = t < length ? score(t) : -INFINITY;
+            float tile_max = s;
+            for (int offset = 32; offset > 0; offset >>= 1)
+                tile_max = fmaxf(tile_max, __shfl_xor(tile_max, offset));
+            const float grown = fmaxf(m, tile_max);
+            float e = t < length ? expf(s - grown) : 0.0f;
+            for (int offset = 32; offset > 0; offset >>= 1)
+                e += __shfl_xor(e, offset);
+            total = total * expf(m - grown) + e;
+            m = grown;
+        }
+    constexpr int kOutputs = (kMaxGroup * DH + kRowThreads - 1) / kRowThreads;
+    float acc[kOutputs] = {};
+    for (int base = 0; base < length; base += kTile) {
+        if (wave < group) {
+            const int t = base + lane;
+            probability[wave][lane] = t < length ? Bf::round(expf(score(t) - m) / total) : 0.0f;
+        }
+        for (int index = threadIdx.x; index < kTile * kVectors; index += kRowThreads) {
+            const int t = index / kVectors, v = index - t * kVectors;
+            const u32x4 row = base + t < length
+                                  ? reinterpret_cast<const u32x4*>(value_cache + (static_cast<size_t>(base + t) * nkv + h) * DH)[v]
+                                  : u32x4{0u, 0u, 0u, 0u};
+            reinterpret_cast<u32x4*>(values[t])[v] = row;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kOutputs; ++k) {
+            const int o = threadIdx.x + k * kRowThreads;
+            if (o < group * DH) {
+                const int g = o / DH, j = o - g * DH;
+                float sum = acc[k];
+                for (int t = 0; t < kTile; ++t)
+                    sum = fmaf(probability[g][t], bf(values[t][j]), sum);
+                acc[k] = sum;
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < kOutputs; ++k) {
+        const int o = threadIdx.x + k * kRowThreads;
+        if (o < group * DH)
+            out[static_cast<size_t>(r) * nq * DH + h * group * DH + o] = bits16(Bf::round(acc[k]));
+    }
+}
+
+// out = bf16(a + b) elementwise (a and b bf16).
+__global__ void __launch_bounds__(kRowThreads) add_rows(const uint16_t* a, const uint16_t* b, size_t count, uint16_t* out)
+{
+    for (size_t i = blockIdx.x * static_cast<size_t>(kRowThreads) + threadIdx.x; i < count;
+         i += static_cast<size_t>(gridDim.x) * kRowThreads)
+        out[i] = bits16(Bf::round(bf(a[i]) + bf(b[i])));
+}
+
+// out = bf16(bf16(silu(gate)) * up), silu(g) = g / (1 + exp(-g)) in FP32 (gate and up bf16).
+__global__ void __launch_bounds__(kRowThreads) silu_rows(const uint16_t* gate, const uint16_t* up, size_t count, uint16_t* out)
+{
+    for (size_t i = blockIdx.x * static_cast<size_t>(kRowThreads) + threadIdx.x; i < count;
+         i += static_cast<size_t>(gridDim.x) * kRowThreads) {
+        const float g = bf(gate[i]);
+        out[i] = bits16(Bf::round(Bf::round(g / (1.0f + expf(-g))) * bf(up[i])));
+    }
+}
+
+} // namespace
+
+bool MatrixPrefill::supports(const ti_worker_program_view& p)
+{
+    const int dh = p.shape.head_dim;
+    return p.weight_dtype == TI_DTYPE_BFLOAT16 && p.stack.full_stack && (dh == 64 || dh == 128) &&
+           p.shape.kv_heads > 0 && p.shape.query_heads % p.shape.kv_heads == 0 &&
+           p.shape.query_heads / p.shape.kv_heads <= kMaxGroup;
+}
+
+MatrixPrefill::MatrixPrefill(const ti_worker_program_view& program) : p_(program) {}
+
+MatrixPrefill::~MatrixPrefill()
+{
+    if (handle_)
+        (void)rocblas_destroy_handle(static_cast<rocblas_handle>(handle_));
+    if (buffer_)
+        (void)hipFree(buffer_);
+}
+
+namespace {
+struct Views {
+    uint16_t *x, *u, *qkv, *q, *attention, *projected, *r, *gate, *up;
+};
+size_t row_elements(const ti_model_shape& s)
+{
+    const size_t d = s.hidden_size, f = s.intermediate_size;
+    const size_t qkv = static_cast<size_t>(s.query_heads + 2 * s.kv_heads) * s.head_dim;
+    const size_t q = static_cast<size_t>(s.query_heads) * s.head_dim;
+    return 5 * d + qkv + q + 2 * f;  // x, u, attention, projected, r | qkv | q | gate, up
+}
+Views views(void* buffer, const ti_model_shape& s, size_t rows)
+{
+    const size_t d = s.hidden_size, f = s.intermediate_size;
+    uint16_t* at = static_cast<uint16_t*>(buffer);
+    auto take = [&](size_t per_row) {
+        uint16_t* v = at;
+        at += rows * per_row;
+        return v;
+    };
+    Views v{};
+    v.x = take(d);
+    v.u = take(d);
+    v.attention = take(d);
+    v.projected = take(d);
+    v.r = take(d);
+    v.qkv = take(static_cast<size_t>(s.query_heads + 2 * s.kv_heads) * s.head_dim);
+    v.q = take(static_cast<size_t>(s.query_heads) * s.head_dim);
+    v.gate = take(f);
+    v.up = take(f);
+    return v;
+}
+
+// C (rows x n, row-major) = X (rows x k, row-major) W^T with W (n x k, row-major): in rocBLAS's
+// column-major terms C^T = op(W_cm) X^T, W_cm being the k x n matrix W's bytes form.
+rocblas_status gemm_xwt(rocblas_handle h, const uint16_t* x, int rows, int k, const uint16_t* w, int n, uint16_t* c, int ldc)
+{
+    const float one = 1.0f, zero = 0.0f;
+    return rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, n, rows, k, &one, w, rocblas_datatype_bf16_r, k,
+                           x, rocblas_datatype_bf16_r, k, &zero, c, rocblas_datatype_bf16_r, ldc, c, rocblas_datatype_bf16_r, ldc,
+                           rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+}
+
+// C (rows x n) = X (rows x k) W with W (k x n, row-major): Wdown as stored (transposed).
+rocblas_status gemm_xw(rocblas_handle h, const uint16_t* x, int rows, int k, const uint16_t* w, int n, uint16_t* c)
+{
+    const float one = 1.0f, zero = 0.0f;
+    return rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_none, n, rows, k, &one, w, rocblas_datatype_bf16_r, n, x,
+                           rocblas_datatype_bf16_r, k, &zero, c, rocblas_datatype_bf16_r, n, c, rocblas_datatype_bf16_r, n,
+                           rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+}
+} // namespace
+
+int MatrixPrefill::layer(hipStream_t stream, void* kv, int layer, int position, int rows)
+{
+    const ti_model_shape& s = p_.shape;
+    const int d = s.hidden_size, f = s.intermediate_size, dh = s.head_dim, nq = s.query_heads, nkv = s.kv_heads;
+    const int qw = nq * dh, kvw = nkv * dh, qkvw = qw + 2 * kvw;
+    const Views v = views(buffer_, s, kChunkRows);
+    const uint16_t* base = static_cast<const uint16_t*>(p_.weights) + p_.stack.layer_weights_offset +
+                           static_cast<size_t>(layer) * p_.stack.layer_weight_stride;
+    const ti_layer_layout& w = p_.layout;
+    uint16_t* cache = static_cast<uint16_t*>(kv) + static_cast<size_t>(layer) * p_.stack.layer_kv_stride;
+    auto h = static_cast<rocblas_handle>(handle_);
+    const float eps = p_.numeric.rms_norm_eps;
+    const size_t hidden_count = static_cast<size_t>(rows) * d, ffn_count = static_cast<size_t>(rows) * f;
+    const dim3 elementwise(static_cast<unsigned>(std::min<size_t>(4096, (ffn_count + kRowThreads - 1) / kRowThreads)));
+    rocblas_status st = rocblas_status_success;
+    auto gemm_ok = [&](rocblas_status status) {
+        st = status;
+        return status == rocblas_status_success;
+    };
+
+    hipLaunchKernelGGL(rms_rows, dim3(rows), dim3(kRowThreads), 0, stream, v.x, base + w.attn_norm, d, eps, v.u);
+    if (!gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wq, qw, v.qkv, qkvw)) ||
+        !gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wk, kvw, v.qkv + qw, qkvw)) ||
+        !gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wv, kvw, v.qkv + qw + kvw, qkvw)))
+        return fail(TI_ERR_RUNTIME, (std::string("prefill QKV GEMM: ") + rocblas_status_to_string(st)).c_str());
+    hipLaunchKernelGGL(rope_rows, dim3(rows), dim3(kRowThreads), 0, stream, v.qkv, position, p_.rotary_frequencies, nq, nkv, dh,
+                       v.q, cache + w.key, cache + w.value);
+    const float scale = 1.0f / sqrtf(static_cast<float>(dh));
+    if (dh == 64)
+        hipLaunchKernelGGL(attention_rows<64>, dim3(rows * nkv), dim3(kRowThreads), 0, stream, v.q, position, nq, nkv,
+                           cache + w.key, cache + w.value, scale, v.attention);
+    else
+        hipLaunchKernelGGL(attention_rows<128>, dim3(rows * nkv), dim3(kRowThreads), 0, stream, v.q, position, nq, nkv,
+                           cache + w.key, cache + w.value, scale, v.attention);
+    if (!gemm_ok(gemm_xwt(h, v.attention, rows, qw, base + w.Wo, d, v.projected, d)))
+        return fail(TI_ERR_RUNTIME, (std::string("prefill output projection GEMM: ") + rocblas_status_to_string(st)).c_str());
+    hipLaunchKernelGGL(add_rows, elementwise, dim3(kRowThreads), 0, stream, v.projected, v.x, hidden_count, v.r);
+    hipLaunchKernelGGL(rms_rows, dim3(rows), dim3(kRowThreads), 0, stream, v.r, base + w.ffn_norm, d, eps, v.u);
+    if (!gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wgate, f, v.gate, f)) ||
+        !gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wup, f, v.up, f)))
+        return fail(TI_ERR_RUNTIME, (std::string("prefill gate/up GEMM: ") + rocblas_status_to_string(st)).c_str());
+    hipLaunchKernelGGL(silu_rows, elementwise, dim3(kRowThreads), 0, stream, v.gate, v.up, ffn_count, v.gate);
+    if (!gemm_ok(gemm_xw(h, v.gate, rows, f, base + w.Wdown, d, v.projected)))
+        return fail(TI_ERR_RUNTIME, (std::string("prefill down GEMM: ") + rocblas_status_to_string(st)).c_str());
+    hipLaunchKernelGGL(add_rows, elementwise, dim3(kRowThreads), 0, stream, v.projected, v.r, hidden_count, v.x);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return hip_fail(e, "prefill kernel launch");
+    return TI_OK;
+}
+
+int MatrixPrefill::enqueue(hipStream_t stream, void* kv, const ti_token_id* tokens, int position, int count)
+{
+    if (!supports(p_))
+        return fail(TI_ERR_INVALID_ARGUMENT, "matrix prefill needs a bf16 decoder stack with head_dim 64 or 128");
+    if (count <= 0)
+        return TI_OK;
+    if (position < 0 || position + count > p_.shape.max_context)
+        return fail(TI_ERR_INVALID_ARGUMENT, "sequence context capacity reached");
+    if (!buffer_) {
+        buffer_bytes_ = row_elements(p_.shape) * kChunkRows * sizeof(uint16_t);
+        const hipError_t e = hipMalloc(&buffer_, buffer_bytes_);
+        if (e != hipSuccess) {
+            buffer_ = nullptr;
+            return hip_fail(e, "prefill buffers");
+        }
+    }
+    if (!handle_) {
+        rocblas_handle h = nullptr;
+        if (rocblas_create_handle(&h) != rocblas_status_success)
+            return fail(TI_ERR_RUNTIME, "rocBLAS handle");
+        handle_ = h;
+    }
+    if (rocblas_set_stream(static_cast<rocblas_handle>(handle_), stream) != rocblas_status_success)
+        return fail(TI_ERR_RUNTIME, "rocBLAS stream");
+    const Views v = views(buffer_, p_.shape, kChunkRows);
+    const uint16_t* embedding = static_cast<const uint16_t*>(p_.weights) + p_.stack.embedding_offset;
+    for (int first = 0; first < count; first += kChunkRows) {
+        const int rows = std::min(kChunkRows, count - first);
+        hipLaunchKernelGGL(gather_rows, dim3(rows), dim3(kRowThreads), 0, stream, embedding, tokens + first, p_.shape.hidden_size,
+                           v.x);
+        for (int layer = 0; layer < p_.stack.layers; ++layer) {
+            const int code = this->layer(stream, kv, layer, position + first, rows);
+            if (code != TI_OK)
+                return code;
+        }
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return hip_fail(e, "prefill kernel launch");
+    return TI_OK;
+}
+
+} // namespace tiles

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "plan.hpp"
+#include "prefill.hpp"
 #include "tileinfer_amd.h"
 #include "worker_config.hpp"
 
@@ -167,6 +168,10 @@ struct Context {
     DeviceBuffer block_trace, ffn_trace;
     DeviceBuffer timeline;
     bool timeline_enabled = false;
+    // Prompts longer than one worker launch prefill all but their last token with matrices
+    // (bf16 decoder stacks; the rest go through the worker one position per step).
+    bool matrix_prefill = true;
+    std::unique_ptr<MatrixPrefill> matrix;
     size_t instruction_count = 0;
     PinnedBuffer ring;
     size_t ring_cursor = 0;
@@ -433,7 +438,17 @@ struct Context {
         t->end_position = start + static_cast<int>(count);
         try {
             stage_input(ids, count);
-            launch(start, tokens.as<ti_token_id>(), static_cast<int>(count), diag.block_outputs != 0, ti_selection{});
+            const int n = static_cast<int>(count);
+            if (matrix_prefill && n > TI_MAX_LAUNCH_STEPS && MatrixPrefill::supports(model->view)) {
+                // The worker decodes the last token: its step leaves the greedy candidates and
+                // diagnostics a generation or collect() continues from.
+                if (!matrix)
+                    matrix = std::make_unique<MatrixPrefill>(model->view);
+                check_ti(matrix->enqueue(stream, kv.ptr, tokens.as<ti_token_id>(), start, n - 1));
+                launch(start + n - 1, tokens.as<ti_token_id>() + n - 1, 1, diag.block_outputs != 0, ti_selection{});
+            } else {
+                launch(start, tokens.as<ti_token_id>(), n, diag.block_outputs != 0, ti_selection{});
+            }
             finish_ticket(t, diag);
             queued_position = t->end_position;
         } catch (...) {
@@ -777,6 +792,13 @@ extern "C" int ti_context_collect_intermediates(ti_context* context, const ti_ti
 }
 
 extern "C" void ti_ticket_free(ti_ticket* ticket) { delete ticket; }
+
+extern "C" int ti_context_set_matrix_prefill(ti_context* context, int32_t enabled)
+{
+    if (!context)
+        return TI_ERR_INVALID_ARGUMENT;
+    return guarded(TI_ERR_HIP, [&] { context->context->matrix_prefill = enabled != 0; });
+}
 
 extern "C" int ti_context_set_timeline(ti_context* context, int32_t enabled)
 {

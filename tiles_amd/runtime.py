@@ -103,7 +103,7 @@ EXPORTS = ("ti_error_string", "ti_last_error_message", "ti_abi", "ti_fingerprint
            "ti_context_decode", "ti_context_generate", "ti_context_reset", "ti_context_ready", "ti_context_wait",
            "ti_context_diagnostic_sizes", "ti_context_collect", "ti_context_intermediate_sizes",
            "ti_context_collect_intermediates", "ti_ticket_free", "ti_context_set_timeline",
-           "ti_context_timeline")
+           "ti_context_timeline", "ti_context_set_matrix_prefill")
 
 _lib = None
 
@@ -159,6 +159,7 @@ def library() -> C.CDLL:
         lib.ti_ticket_free.argtypes = [P]
         lib.ti_ticket_free.restype = None
         lib.ti_context_set_timeline.argtypes = [P, C.c_int32]
+        lib.ti_context_set_matrix_prefill.argtypes = [P, C.c_int32]
         lib.ti_context_timeline.argtypes = [P, C.POINTER(C.c_uint64), C.c_size_t, C.POINTER(C.c_size_t)]
         _lib = lib
     return _lib
@@ -325,6 +326,11 @@ class SequenceContext:
         _check(library().ti_context_wait(self._handle, ticket._handle, C.byref(done), ids, ticket.requested))
         return Result(list(ids[: done.count]) if ticket.requested else [], done.position,
                       STOP_REASONS.get(done.stop_reason, "none"), done.compute_us)
+
+    def set_matrix_prefill(self, enabled: bool) -> None:
+        """Prefills of more than 64 tokens on bf16 stacks run all but the last token as matrices
+        (on by default); off, every token goes through the worker."""
+        _check(library().ti_context_set_matrix_prefill(self._handle, int(enabled)))
 
     def set_timeline(self, enabled: bool) -> None:
         _check(library().ti_context_set_timeline(self._handle, int(enabled)))
