@@ -258,7 +258,7 @@ int ti_context_set_timeline(ti_context* context, int32_t enabled);
 /* No counterpart in the reference, which prefills one position per worker step and lists a
  * matrix prefill as an open question (docs/development.md:331).  With it on (the default), a
  * prefill of more than 64 tokens on a bf16 decoder stack runs all but its last token through
- * each layer as matrices (rocBLAS GEMMs and row kernels following the same rounding points),
+ * each layer as matrices (MFMA GEMMs and row kernels following the same rounding points),
  * then the worker decodes the last token.  Off: every token goes through the worker. */
 int ti_context_set_matrix_prefill(ti_context* context, int32_t enabled);
 int ti_context_timeline(ti_context* context, uint64_t* words, size_t capacity, size_t* count);

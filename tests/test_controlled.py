@@ -1,0 +1,31 @@
+"""Statistics and telemetry parsing of the controlled timing protocol (tiles_amd/controlled.py),
+on the CPU: the paired bootstrap recovers a known shift, and amd-smi JSON flattens to numeric
+leaves keyed by path."""
+
+import numpy as np
+
+from tiles_amd import controlled as C
+
+
+def test_paired_bootstrap_recovers_a_constant_shift():
+    reference = [640.0, 641.5, 639.8, 640.7, 641.1, 640.2]
+    p = C.paired(reference, [r + 2.5 for r in reference], seed=1)
+    assert abs(p["mean_us"] - 2.5) < 1e-9 and p["ci95_us"] == [2.5, 2.5] and p["pairs"] == 6
+    assert abs(p["mean_percent"] - 100 * 2.5 / np.mean(reference)) < 1e-9
+
+
+def test_paired_bootstrap_interval_covers_zero_for_noise():
+    rng = np.random.default_rng(3)
+    reference = list(640 + rng.normal(0, 0.5, 12))
+    other = list(np.asarray(reference) + rng.normal(0, 0.5, 12))
+    p = C.paired(reference, other, seed=2)
+    assert p["ci95_us"][0] < 0 < p["ci95_us"][1]
+
+
+def test_amd_smi_records_flatten_to_numeric_leaves():
+    record = {"gpu": 0, "power": {"socket_power": {"value": 312, "unit": "W"}},
+              "clock": {"gfx_0": {"clk": {"value": 2100, "unit": "MHz"}, "max_clk": {"value": 2400, "unit": "MHz"}}},
+              "temperature": {"hotspot": {"value": 55, "unit": "C"}, "mem": "N/A"}}
+    flat = C.flatten(record)
+    assert flat == {"gpu": 0.0, "power.socket_power": 312.0, "clock.gfx_0.clk": 2100.0, "clock.gfx_0.max_clk": 2400.0,
+                    "temperature.hotspot": 55.0}

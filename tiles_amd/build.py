@@ -46,9 +46,7 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as pool:
         objects = list(pool.map(_object, SOURCES))
     temporary = LIBRARY.with_suffix(".so.tmp")
-    # rocBLAS supplies the matrix prefill's plain GEMMs (prefill.hip).
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(temporary), *map(str, objects), "-L/opt/rocm/lib",
-          "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(temporary), *map(str, objects)])
     os.replace(temporary, LIBRARY)
     cli_object = _object("main.cpp")
     _run([HIPCC, "--offload-arch=gfx950", "-o", str(CLI), str(cli_object), f"-L{PACKAGE}", "-ltileinfer_amd",

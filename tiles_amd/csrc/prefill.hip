@@ -7,7 +7,7 @@
 // the dot products:
 //
 //   u = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * attn_norm)      rms_rows
-//   q, k, v = bf16(W u)                                          rocBLAS GEMM (bf16 in/out, FP32 sums)
+//   q, k, v = bf16(W u)                                          gemm_bf16 (MFMA, FP32 sums)
 //   q, k rotated as the worker rotates them; K, V rows -> cache  rope_rows
 //   s = bf16(bf16(q . k) / sqrt(dh)); P = bf16(exp(s - M) / S)   attention_rows (causal, exact
 //   attention = bf16(sum P v)                                    softmax statistics per row)
@@ -16,11 +16,10 @@
 //   p = bf16(bf16(silu(bf16(Wgate z))) * bf16(Wup z))            GEMMs, silu_rows
 //   y = bf16(bf16(Wdown p) + r)                                  GEMM, add_rows
 //
-// The GEMMs are plain library GEMMs (rocBLAS, bf16 inputs and outputs, FP32 accumulation);
-// everything around them is these kernels.
+// The GEMMs are this file's MFMA kernel rather than a library's: rocBLAS, linked into this
+// library, conflicted with the different rocBLAS build PyTorch ships, and a process that loaded
+// this library before importing torch crashed.
 #include "prefill.hpp"
-
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <string>
@@ -218,6 +217,97 @@ __global__ void __launch_bounds__(kRowThreads) silu_rows(const uint16_t* gate, c
     }
 }
 
+// C = A B^T (kBRows: B is [N][K], a weight matrix whose rows are output features) or C = A B
+// (!kBRows: B is [K][N], Wdown as stored), all bf16 and row-major, A [M][K]; C rounded to bf16
+// from FP32 sums (ldc: C's row stride).  Tiles of 128 x 128 per block of 4 waves, each wave
+// 64 x 64 as 4 x 4 v_mfma_f32_16x16x32_bf16 tiles, K in steps of 32 through LDS (rows padded to
+// 40 elements: 16-byte operand reads of 16 rows 80 bytes apart fall on distinct bank groups), the
+// next step's tile loaded into registers while this one's MFMAs run.  K % 32 == 0 and N % 16 == 0
+// (the launcher checks); rows and columns past M and N are clamped on load and not stored.
+constexpr int kGemmTile = 128, kGemmK = 32, kGemmStride = kGemmK + 8;
+
+template <bool kBRows>
+__global__ void __launch_bounds__(256) gemm_bf16(const uint16_t* a, const uint16_t* b, uint16_t* c, int m, int n, int k, int ldc)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t as[kGemmTile * kGemmStride];
+    __shared__ __attribute__((aligned(16))) uint16_t bs[kGemmTile * kGemmStride];  // [n][k] either way
+    const int t = threadIdx.x, lane = t & 63, wave = t / 64;
+    const int m0 = blockIdx.y * kGemmTile, n0 = blockIdx.x * kGemmTile;
+    const int wm = (wave / 2) * 64, wn = (wave % 2) * 64;
+    // Loads of one K step: A rows t / 2 (16 elements each half), B likewise (kBRows) or B rows
+    // k = t / 8 of 16 columns each (!kBRows).
+    const int arow = min(m0 + t / 2, m - 1), acol = (t % 2) * 16;
+    const int brow = kBRows ? min(n0 + t / 2, n - 1) : t / 8;
+    const int bcol = kBRows ? (t % 2) * 16 : min(n0 + (t % 8) * 16, n - 16);
+    u32x4 ra[2], rb[2];
+    auto load = [&](int k0) {
+        const u32x4* pa = reinterpret_cast<const u32x4*>(a + static_cast<size_t>(arow) * k + k0 + acol);
+        ra[0] = pa[0];
+        ra[1] = pa[1];
+        const u32x4* pb = kBRows ? reinterpret_cast<const u32x4*>(b + static_cast<size_t>(brow) * k + k0 + bcol)
+                                 : reinterpret_cast<const u32x4*>(b + static_cast<size_t>(k0 + brow) * n + bcol);
+        rb[0] = pb[0];
+        rb[1] = pb[1];
+    };
+    auto store = [&]() {
+        u32x4* da = reinterpret_cast<u32x4*>(as + (t / 2) * kGemmStride + acol);
+        da[0] = ra[0];
+        da[1] = ra[1];
+        if constexpr (kBRows) {
+            u32x4* db = reinterpret_cast<u32x4*>(bs + (t / 2) * kGemmStride + bcol);
+            db[0] = rb[0];
+            db[1] = rb[1];
+        } else {
+            // Column j of the 16 loaded becomes element k of LDS row (column - n0).
+            const int col = (t % 8) * 16;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t word = rb[j / 8][(j % 8) / 2];
+                bs[(col + j) * kGemmStride + brow] = static_cast<uint16_t>((j & 1) ? word >> 16 : word);
+            }
+        }
+    };
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int r = lane % 16, q = (lane / 16) * 8;
+    load(0);
+    for (int k0 = 0; k0 < k; k0 += kGemmK) {
+        __syncthreads();  // the previous step's operand reads are done
+        store();
+        __syncthreads();
+        if (k0 + kGemmK < k)
+            load(k0 + kGemmK);
+        u32x4 fa[4], fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            fa[i] = *reinterpret_cast<const u32x4*>(as + (wm + i * 16 + r) * kGemmStride + q);
+            fb[i] = *reinterpret_cast<const u32x4*>(bs + (wn + i * 16 + r) * kGemmStride + q);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = mfma_16x16x32_bf16(fa[i], fb[j], acc[i][j]);
+    }
+    // Lane l holds rows 4 (l / 16) .. + 3 of column l % 16 of each 16 x 16 tile.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = n0 + wn + j * 16 + r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = m0 + wm + i * 16 + (lane / 16) * 4 + e;
+                if (row < m && col < n)
+                    c[static_cast<size_t>(row) * ldc + col] = bits16(Bf::round(acc[i][j][e]));
+            }
+        }
+}
+
 } // namespace
 
 bool MatrixPrefill::supports(const ti_worker_program_view& p)
@@ -232,8 +322,6 @@ MatrixPrefill::MatrixPrefill(const ti_worker_program_view& program) : p_(program
 
 MatrixPrefill::~MatrixPrefill()
 {
-    if (handle_)
-        (void)rocblas_destroy_handle(static_cast<rocblas_handle>(handle_));
     if (buffer_)
         (void)hipFree(buffer_);
 }
@@ -271,23 +359,17 @@ Views views(void* buffer, const ti_model_shape& s, size_t rows)
     return v;
 }
 
-// C (rows x n, row-major) = X (rows x k, row-major) W^T with W (n x k, row-major): in rocBLAS's
-// column-major terms C^T = op(W_cm) X^T, W_cm being the k x n matrix W's bytes form.
-rocblas_status gemm_xwt(rocblas_handle h, const uint16_t* x, int rows, int k, const uint16_t* w, int n, uint16_t* c, int ldc)
+// C (rows x n, row stride ldc) = X (rows x k) W^T, W (n x k) row-major; or = X W with W (k x n).
+int gemm(hipStream_t stream, bool w_rows, const uint16_t* x, int rows, int k, const uint16_t* w, int n, uint16_t* c, int ldc)
 {
-    const float one = 1.0f, zero = 0.0f;
-    return rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, n, rows, k, &one, w, rocblas_datatype_bf16_r, k,
-                           x, rocblas_datatype_bf16_r, k, &zero, c, rocblas_datatype_bf16_r, ldc, c, rocblas_datatype_bf16_r, ldc,
-                           rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-}
-
-// C (rows x n) = X (rows x k) W with W (k x n, row-major): Wdown as stored (transposed).
-rocblas_status gemm_xw(rocblas_handle h, const uint16_t* x, int rows, int k, const uint16_t* w, int n, uint16_t* c)
-{
-    const float one = 1.0f, zero = 0.0f;
-    return rocblas_gemm_ex(h, rocblas_operation_none, rocblas_operation_none, n, rows, k, &one, w, rocblas_datatype_bf16_r, n, x,
-                           rocblas_datatype_bf16_r, k, &zero, c, rocblas_datatype_bf16_r, n, c, rocblas_datatype_bf16_r, n,
-                           rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    if (rows < 1 || k % kGemmK != 0 || n % 16 != 0 || n < 16 || ldc < n)
+        return fail(TI_ERR_INVALID_ARGUMENT, "prefill GEMM shape (K a multiple of 32, N of 16)");
+    const dim3 grid((n + kGemmTile - 1) / kGemmTile, (rows + kGemmTile - 1) / kGemmTile);
+    if (w_rows)
+        hipLaunchKernelGGL(gemm_bf16<true>, grid, dim3(256), 0, stream, x, w, c, rows, n, k, ldc);
+    else
+        hipLaunchKernelGGL(gemm_bf16<false>, grid, dim3(256), 0, stream, x, w, c, rows, n, k, ldc);
+    return TI_OK;
 }
 } // namespace
 
@@ -301,21 +383,20 @@ int MatrixPrefill::layer(hipStream_t stream, void* kv, int layer, int position, 
                            static_cast<size_t>(layer) * p_.stack.layer_weight_stride;
     const ti_layer_layout& w = p_.layout;
     uint16_t* cache = static_cast<uint16_t*>(kv) + static_cast<size_t>(layer) * p_.stack.layer_kv_stride;
-    auto h = static_cast<rocblas_handle>(handle_);
     const float eps = p_.numeric.rms_norm_eps;
     const size_t hidden_count = static_cast<size_t>(rows) * d, ffn_count = static_cast<size_t>(rows) * f;
     const dim3 elementwise(static_cast<unsigned>(std::min<size_t>(4096, (ffn_count + kRowThreads - 1) / kRowThreads)));
-    rocblas_status st = rocblas_status_success;
-    auto gemm_ok = [&](rocblas_status status) {
-        st = status;
-        return status == rocblas_status_success;
+    int code = TI_OK;
+    auto gemm_ok = [&](int status) {
+        code = status;
+        return status == TI_OK;
     };
 
     hipLaunchKernelGGL(rms_rows, dim3(rows), dim3(kRowThreads), 0, stream, v.x, base + w.attn_norm, d, eps, v.u);
-    if (!gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wq, qw, v.qkv, qkvw)) ||
-        !gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wk, kvw, v.qkv + qw, qkvw)) ||
-        !gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wv, kvw, v.qkv + qw + kvw, qkvw)))
-        return fail(TI_ERR_RUNTIME, (std::string("prefill QKV GEMM: ") + rocblas_status_to_string(st)).c_str());
+    if (!gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wq, qw, v.qkv, qkvw)) ||
+        !gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wk, kvw, v.qkv + qw, qkvw)) ||
+        !gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wv, kvw, v.qkv + qw + kvw, qkvw)))
+        return code;
     hipLaunchKernelGGL(rope_rows, dim3(rows), dim3(kRowThreads), 0, stream, v.qkv, position, p_.rotary_frequencies, nq, nkv, dh,
                        v.q, cache + w.key, cache + w.value);
     const float scale = 1.0f / sqrtf(static_cast<float>(dh));
@@ -325,16 +406,16 @@ int MatrixPrefill::layer(hipStream_t stream, void* kv, int layer, int position, 
     else
         hipLaunchKernelGGL(attention_rows<128>, dim3(rows * nkv), dim3(kRowThreads), 0, stream, v.q, position, nq, nkv,
                            cache + w.key, cache + w.value, scale, v.attention);
-    if (!gemm_ok(gemm_xwt(h, v.attention, rows, qw, base + w.Wo, d, v.projected, d)))
-        return fail(TI_ERR_RUNTIME, (std::string("prefill output projection GEMM: ") + rocblas_status_to_string(st)).c_str());
+    if (!gemm_ok(gemm(stream, true, v.attention, rows, qw, base + w.Wo, d, v.projected, d)))
+        return code;
     hipLaunchKernelGGL(add_rows, elementwise, dim3(kRowThreads), 0, stream, v.projected, v.x, hidden_count, v.r);
     hipLaunchKernelGGL(rms_rows, dim3(rows), dim3(kRowThreads), 0, stream, v.r, base + w.ffn_norm, d, eps, v.u);
-    if (!gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wgate, f, v.gate, f)) ||
-        !gemm_ok(gemm_xwt(h, v.u, rows, d, base + w.Wup, f, v.up, f)))
-        return fail(TI_ERR_RUNTIME, (std::string("prefill gate/up GEMM: ") + rocblas_status_to_string(st)).c_str());
+    if (!gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wgate, f, v.gate, f)) ||
+        !gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wup, f, v.up, f)))
+        return code;
     hipLaunchKernelGGL(silu_rows, elementwise, dim3(kRowThreads), 0, stream, v.gate, v.up, ffn_count, v.gate);
-    if (!gemm_ok(gemm_xw(h, v.gate, rows, f, base + w.Wdown, d, v.projected)))
-        return fail(TI_ERR_RUNTIME, (std::string("prefill down GEMM: ") + rocblas_status_to_string(st)).c_str());
+    if (!gemm_ok(gemm(stream, false, v.gate, rows, f, base + w.Wdown, d, v.projected, d)))
+        return code;
     hipLaunchKernelGGL(add_rows, elementwise, dim3(kRowThreads), 0, stream, v.projected, v.r, hidden_count, v.x);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess)
@@ -358,14 +439,6 @@ int MatrixPrefill::enqueue(hipStream_t stream, void* kv, const ti_token_id* toke
             return hip_fail(e, "prefill buffers");
         }
     }
-    if (!handle_) {
-        rocblas_handle h = nullptr;
-        if (rocblas_create_handle(&h) != rocblas_status_success)
-            return fail(TI_ERR_RUNTIME, "rocBLAS handle");
-        handle_ = h;
-    }
-    if (rocblas_set_stream(static_cast<rocblas_handle>(handle_), stream) != rocblas_status_success)
-        return fail(TI_ERR_RUNTIME, "rocBLAS stream");
     const Views v = views(buffer_, p_.shape, kChunkRows);
     const uint16_t* embedding = static_cast<const uint16_t*>(p_.weights) + p_.stack.embedding_offset;
     for (int first = 0; first < count; first += kChunkRows) {

@@ -32,7 +32,6 @@ class MatrixPrefill {
 
   private:
     ti_worker_program_view p_;
-    void* handle_ = nullptr;  // rocblas_handle
     void* buffer_ = nullptr;  // every activation buffer, kChunkRows rows each
     size_t buffer_bytes_ = 0;
     int layer(hipStream_t stream, void* kv, int layer, int position, int rows);
