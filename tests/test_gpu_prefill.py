@@ -3,7 +3,7 @@ prefill on the same package and against the oracle's full causal block
 (oracle/decoder.py recompute_prefix, the reference's decoder_reference.py:273-312).
 
 Both device paths follow the same bf16 rounding points; they differ in the FP32 summation order
-of the dot products (rocBLAS GEMMs against the worker's GEMVs), so a K/V element can differ by a
+of the dot products (MFMA GEMM tiles against the worker's GEMVs), so a K/V element can differ by a
 bf16 rounding where a dot product lands near a rounding boundary, and such a difference can grow
 through later layers.  The bars below are stated per test."""
 

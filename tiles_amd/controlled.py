@@ -17,6 +17,12 @@ next to each other in time, and a bootstrap over the pairs gives the 95% interva
 difference.  Two arms of one package (an A/A run) measure the protocol's own resolution.  Rounds
 further than OUTLIER_FRACTION from their arm's median at one context are excluded and counted.
 
+Server placement biases a comparison: in an A/A run on MI355X the server started first was
+0.4-0.8% faster than the second, steadily (each process uploads its own weights and buffers).
+So halfway through each context's blocks every server is restarted in the reverse order; the
+paired mean over both halves cancels a symmetric placement effect, and half the difference
+between the halves' means is reported as that effect (``--no-swap`` keeps one spawn order).
+
     python -m tiles_amd.controlled --arm A=/tmp/llama4k --arm B=/tmp/llama4k --contexts 1 4096 \\
         --blocks 6 --rounds 5 --out report.json
 """
@@ -196,23 +202,35 @@ def main() -> int:
     parser.add_argument("--blocks", type=int, default=6)
     parser.add_argument("--rounds", type=int, default=5)
     parser.add_argument("--tokens", type=int, default=64)
+    parser.add_argument("--no-swap", action="store_true", help="keep the first spawn order for every block")
     parser.add_argument("--out", type=Path)
     a = parser.parse_args()
     if a.serve:
         return serve(a.serve)
     if len(a.arm) < 2:
         parser.error("at least two --arm")
-    arms = [Arm(spec) for spec in a.arm]
+    spawn_order = list(a.arm)
+    arms = [Arm(spec) for spec in spawn_order]
+    names = [arm.name for arm in arms]
     telemetry = Telemetry()
     report = {"protocol": {"blocks": a.blocks, "rounds": a.rounds, "tokens": a.tokens, "warmup_rounds_per_block": 1,
-                           "outlier_fraction": OUTLIER_FRACTION, "bootstrap": BOOTSTRAP, "order": "alternating"},
+                           "outlier_fraction": OUTLIER_FRACTION, "bootstrap": BOOTSTRAP, "order": "alternating",
+                           "spawn_order_swapped_halfway": not a.no_swap},
               "arms": {arm.name: arm.describe() for arm in arms}, "contexts": {}}
     try:
         for n in a.contexts:
-            raw = {arm.name: [] for arm in arms}
+            raw = {name: [] for name in names}
             blocks = []
+            spawned = {}
             for b in range(a.blocks):
-                order = arms if b % 2 == 0 else arms[::-1]
+                if not a.no_swap and a.blocks >= 2 and b == a.blocks // 2:
+                    for arm in arms:
+                        arm.close()
+                    spawn_order = spawn_order[::-1]
+                    arms = [Arm(spec) for spec in spawn_order]
+                by_name = {arm.name: arm for arm in arms}
+                spawned[b] = [arm.name for arm in arms]
+                order = [by_name[name] for name in (names if b % 2 == 0 else names[::-1])]
                 for arm in order:
                     start = time.time()
                     times = arm.measure(n, a.rounds, a.tokens)
@@ -220,28 +238,37 @@ def main() -> int:
                     raw[arm.name].append(times)
                     blocks.append({"block": b, "arm": arm.name, "start": start, "end": end, "us_per_token": times,
                                    "telemetry": telemetry.window(start, end)})
-                print(f"ctx {n} block {b}: " + "  ".join(f"{arm.name} {statistics.median(raw[arm.name][-1]):.1f}"
-                                                         for arm in arms), flush=True)
+                print(f"ctx {n} block {b} (spawned {', '.join(spawned[b])}): " +
+                      "  ".join(f"{name} {statistics.median(raw[name][-1]):.1f}" for name in names), flush=True)
             summary = {}
-            for arm in arms:
-                every = [t for block in raw[arm.name] for t in block]
+            for name in names:
+                every = [t for block in raw[name] for t in block]
                 median = statistics.median(every)
-                kept = [[t for t in block if abs(t - median) <= OUTLIER_FRACTION * median] for block in raw[arm.name]]
-                summary[arm.name] = {"median_us": median, "excluded_rounds": sum(len(x) for x in raw[arm.name]) - sum(len(k) for k in kept),
-                                     "block_medians_us": [statistics.median(k) if k else float("nan") for k in kept]}
-            reference = arms[0].name
-            for arm in arms[1:]:
-                summary[arm.name]["vs_" + reference] = paired(summary[reference]["block_medians_us"],
-                                                              summary[arm.name]["block_medians_us"], seed=n)
-            report["contexts"][str(n)] = {"summary": summary, "blocks": blocks}
-            for arm in arms:
-                s = summary[arm.name]
+                kept = [[t for t in block if abs(t - median) <= OUTLIER_FRACTION * median] for block in raw[name]]
+                summary[name] = {"median_us": median, "excluded_rounds": sum(len(x) for x in raw[name]) - sum(len(k) for k in kept),
+                                 "block_medians_us": [statistics.median(k) if k else float("nan") for k in kept]}
+            reference = names[0]
+            half = a.blocks // 2
+            for name in names[1:]:
+                ref_blocks, blocks_of = summary[reference]["block_medians_us"], summary[name]["block_medians_us"]
+                comparison = paired(ref_blocks, blocks_of, seed=n)
+                if not a.no_swap and half >= 1:
+                    first = float(np.mean(np.subtract(blocks_of[:half], ref_blocks[:half])))
+                    second = float(np.mean(np.subtract(blocks_of[half:], ref_blocks[half:])))
+                    comparison["first_half_mean_us"], comparison["second_half_mean_us"] = first, second
+                    comparison["spawn_order_effect_us"] = (first - second) / 2
+                summary[name]["vs_" + reference] = comparison
+            report["contexts"][str(n)] = {"summary": summary, "blocks": blocks, "spawn_order_by_block": spawned}
+            for name in names:
+                s = summary[name]
                 extra = ""
                 if "vs_" + reference in s:
                     p = s["vs_" + reference]
                     extra = (f"  vs {reference}: {p['mean_us']:+.2f} us [{p['ci95_us'][0]:+.2f}, {p['ci95_us'][1]:+.2f}] "
                              f"({p['mean_percent']:+.3f}%)")
-                print(f"ctx {n} {arm.name}: median {s['median_us']:.2f} us/token, {s['excluded_rounds']} rounds excluded{extra}",
+                    if "spawn_order_effect_us" in p:
+                        extra += f"; spawn-order effect {p['spawn_order_effect_us']:+.2f} us"
+                print(f"ctx {n} {name}: median {s['median_us']:.2f} us/token, {s['excluded_rounds']} rounds excluded{extra}",
                       flush=True)
     finally:
         telemetry.stop()
