@@ -12,7 +12,8 @@ RMSNorm and Llama-3 RoPE as in the full model) with a 4096-token vocabulary:
 
 A one-layer stack's K/V rows depend on the tokens alone, so the oracle fills its cache with
 ``append_kv`` (decode_one's own K/V operations) and runs the whole decoder only where logits are
-compared; the GPU prefills through its worker as in production.
+compared; the GPU prefills as in production: prompt positions but the last through the matrix
+prefill (tiles_amd/csrc/prefill.hip), the last one and the decode steps through the worker.
 
 Bars.  The prefix K/V rows differ from the oracle's in under 1% of elements, V by at most one
 bf16 spacing and K (through RoPE) by at most four (the projections' FP32 sums and the cos/sin

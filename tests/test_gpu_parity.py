@@ -190,6 +190,9 @@ def test_bf16_matrix_attention(target, tmp, head_dim, chunk_steps, fused_steps, 
     ospec = small_oracle_spec(spec)
     tokens = S.prompt(context, seed=context, vocab=spec.vocab_size)
     _, ctx = context_for(path)
+    # The worker prefills too, so its attention runs at every length up to the context's; the
+    # matrix prefill of these packages is checked in tests/test_gpu_prefill.py.
+    ctx.set_matrix_prefill(False)
     ctx.wait(ctx.enqueue_prefill(tokens[:-1]))
     got = ctx.collect(ctx.enqueue_decode(tokens[-1], logits=True))["logits"]
     cache = ref.StackCache.empty(ospec, torch.bfloat16)
