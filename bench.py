@@ -144,6 +144,10 @@ def main() -> int:
     parser.add_argument("--write-package-ctx4096", type=Path, default=None,
                         help="only write the ctx-4096 package (max_context 4160, --chunk-steps) to this directory and "
                              "its 4096-token prompt to DIR.ctx4096.json, then exit")
+    parser.add_argument("--lm-head-only", action="store_true",
+                        help="only the isolated LM-head step (BASELINE config 2) on the ctx-1 package: print its JSON "
+                             "object and exit (for a kernel trace of that launch alone)")
+    parser.add_argument("--lm-head-rounds", type=int, default=20, help="rounds of the isolated LM-head step")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the decode worker is single-GPU); --gpus {args.gpus} is not supported",
@@ -178,6 +182,30 @@ def main() -> int:
     log(f"ctx-1 package built in {time.time() - start:.1f}s")
     plan = R.load_plan(work / "llama", verify_weights=False)
     model = R.DecoderModel(plan)
+
+    # The LM-head step alone: h ~ N(0, 1) bf16 [2048] through the final
+    # RMSNorm (weight 1.0), the tied 128256 x 2048 bf16 embedding ~ N(0, 0.02) of the ctx-1 model
+    # and greedy argmax, as launches of the worker's logits tasks of their own
+    # (ti_context_lm_head_step): the median round's worker launch (HIP events around it), against
+    # its 525,344,768 bytes.  A seed kernel before it publishes h, a selection kernel after it
+    # reduces the tasks' candidates; both are outside the timed launch.
+    import torch
+
+    hidden = torch.randn(2048, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    head_ctx = model.create_context()
+    bits = hidden.view(torch.int16).numpy().view("uint16")
+    head = head_ctx.wait(head_ctx.enqueue_lm_head_step(bits, rounds=args.lm_head_rounds))
+    del head_ctx
+    head_us = head.compute_us
+    lm_head_step = {"us": head_us, "bytes": LM_HEAD_STEP_BYTES, "GBps": LM_HEAD_STEP_BYTES / (head_us * 1e-6) / 1e9,
+                    "fraction_of_stream_read": LM_HEAD_STEP_BYTES / (head_us * 1e-6) / 1e9 / stream_gbps,
+                    "token": head.generated[0], "rounds": args.lm_head_rounds,
+                    "measured": "isolated LM-head step (ti_context_lm_head_step): median over the rounds of the "
+                                "worker launch running the logits tasks alone (HIP events around it)"}
+    log(f"LM-head step: {head_us:.1f} us, {lm_head_step['GBps']:.0f} GB/s, token {head.generated[0]}")
+    if args.lm_head_only:
+        print(json.dumps({"lm_head_step": lm_head_step, "hbm_stream_read_GBps": stream_gbps}), flush=True)
+        return 0
     ctx = model.create_context()
 
     # ctx 1: 1-token prompt, 256 new tokens (4 launches of 64)
@@ -200,25 +228,6 @@ def main() -> int:
     achieved = total_bytes / (mean_us * 1e-6) / 1e9
     floor_ms = total_bytes / new_tokens / (stream_gbps * 1e9) * 1e3
     log(f"ctx1: {ms_per_token * 1e3:.1f} us/token, floor {floor_ms * 1e3:.1f} us")
-
-    # The LM-head step (BASELINE config 2's GEMV: final RMSNorm, 128256 x 2048 bf16 rows, argmax)
-    # inside one decode step: the logits wave of a timeline launch, from the first logits task's
-    # start (before it issues its first weight loads) to the last task's end, against its
-    # 525,344,768 bytes.  The span counts the loads issued while the final layer still ran.
-    from tiles_amd import timeline as T
-    ctx.set_timeline(True)
-    ctx.wait(ctx.enqueue_reset())
-    ctx.wait(ctx.enqueue_prefill(prompt))
-    ctx.wait(ctx.enqueue_generate(64))
-    plan_dict = json.loads((work / "llama" / "plan.json").read_text())
-    waves = T.budget(plan_dict, ctx.timeline().reshape(-1, 4), len(prompt) + 63, stream_gbps)["waves"]
-    ctx.set_timeline(False)
-    head_us = [w for w in waves if w["opcode"] == "logits"][-1]["span_us"]
-    lm_head_step = {"us": head_us, "bytes": LM_HEAD_STEP_BYTES, "GBps": LM_HEAD_STEP_BYTES / (head_us * 1e-6) / 1e9,
-                    "fraction_of_stream_read": LM_HEAD_STEP_BYTES / (head_us * 1e-6) / 1e9 / stream_gbps,
-                    "measured": "logits wave of the last step of a 64-token ctx-1 launch (timeline): first task "
-                                "start to last task end"}
-    log(f"LM-head step: {head_us:.1f} us, {lm_head_step['GBps']:.0f} GB/s")
 
     del ctx, model, plan
     gc.collect()

@@ -230,6 +230,20 @@ int ti_context_decode(ti_context* context, ti_token_id id, ti_diagnostic_request
 int ti_context_generate(ti_context* context, int32_t max_new_tokens, ti_token_id eos_id,
                         ti_diagnostic_request diag, ti_ticket** out);
 int ti_context_reset(ti_context* context, ti_ticket** out);
+/* The isolated LM-head step (no counterpart in the reference, which runs it
+ * only inside a decode step, ops.cuh:842-911): `hidden` (host, hidden_size elements of the
+ * package's weight type) through the final RMSNorm, the LM-head GEMV and greedy selection,
+ * `rounds` times.  Each round is the worker's own logits tasks in a launch of their own: a
+ * seed kernel publishes `hidden` as the last layer's output, the worker runs one step of a
+ * program holding only the package's logits tasks, and a selection kernel reduces their
+ * candidates.  The context must be empty (created or reset) and is left as a reset leaves it.
+ * ti_context_wait reports the selected token (count 1) and, as compute_us, the median round's
+ * worker launch (HIP events around it on the context's stream; the seed and selection kernels
+ * before and after it are outside);
+ * diag.logits collects the last round's logits; K/V and block outputs are refused.  A
+ * non-finite logit fails with "generation stopped: non-finite logits". */
+int ti_context_lm_head_step(ti_context* context, const void* hidden, int32_t rounds, ti_diagnostic_request diag,
+                            ti_ticket** out);
 /* 1 ready, 0 not ready, <0 error (marks the context invalid). */
 int ti_context_ready(ti_context* context, const ti_ticket* ticket);
 

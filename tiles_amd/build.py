@@ -20,7 +20,7 @@ LIBRARY = PACKAGE / "libtileinfer_amd.so"
 CLI = PACKAGE / "tile_runtime"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["worker_bf16.hip", "worker_f32.hip", "launch.hip", "static_exchange.hip", "prefill.hip", "plan.cpp",
+SOURCES = ["worker_bf16.hip", "worker_f32.hip", "launch.hip", "static_exchange.hip", "prefill.hip", "lm_head.hip", "plan.cpp",
            "runtime.cpp", "json.cpp", "sha256.cpp"]
 # Packed-FP32 instructions are kept out of every GPU code object (a known-bad form on this pool).
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", f"-I{ROOT / 'include'}", f"-I{CSRC}",

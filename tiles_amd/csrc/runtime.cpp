@@ -89,6 +89,10 @@ struct UploadedModel {
     LoadedPlan meta;  // everything but the weight bytes, which live on the device
     DeviceBuffer weights, instructions, streams, rope;
     ti_worker_program_view view{};
+    // The LM-head step's program: every worker's logits tasks, in stream order.
+    DeviceBuffer head_instructions, head_streams;
+    ti_worker_program_view head_view{};
+    size_t head_tasks = 0;
     size_t exchange_words = 0;
 
     size_t instruction_count = 0;
@@ -130,13 +134,35 @@ struct UploadedModel {
         view.stack = plan.stack;
         view.weight_dtype = plan.weight_dtype;
         exchange_words = ti_exchange_words(&plan.shape, plan.stack.layers, plan.selection_slots);
+
+        std::vector<ti_task_record> head_records;
+        std::vector<ti_worker_task_range> head_ranges(plan.streams.size());
+        for (size_t w = 0; w < plan.streams.size(); ++w) {
+            head_ranges[w].begin = static_cast<uint32_t>(head_records.size());
+            for (uint32_t i = 0; i < plan.streams[w].count; ++i) {
+                const ti_task_record& r = plan.instructions[plan.streams[w].begin + i];
+                if (r.opcode == TI_OP_LOGITS)
+                    head_records.push_back(r);
+            }
+            head_ranges[w].count = static_cast<uint32_t>(head_records.size()) - head_ranges[w].begin;
+        }
+        head_tasks = head_records.size();
+        head_instructions = DeviceBuffer(std::max<size_t>(1, head_records.size()) * sizeof(ti_task_record));
+        if (!head_records.empty())
+            check(hipMemcpy(head_instructions.ptr, head_records.data(), head_records.size() * sizeof(ti_task_record),
+                            hipMemcpyHostToDevice), "upload LM-head program");
+        head_streams = DeviceBuffer(head_ranges.size() * sizeof(ti_worker_task_range));
+        check(hipMemcpy(head_streams.ptr, head_ranges.data(), head_streams.bytes, hipMemcpyHostToDevice), "upload LM-head streams");
+        head_view = view;
+        head_view.instructions = head_instructions.as<ti_task_record>();
+        head_view.streams = head_streams.as<ti_worker_task_range>();
     }
     int elem() const { return element_bytes(meta.weight_dtype); }
     size_t kv_count() const { return meta.kv_bytes / elem(); }
 };
 
 struct Ticket {
-    enum class Kind { prefill, generate, reset } kind;
+    enum class Kind { prefill, generate, reset, lm_head } kind;
     hipEvent_t event = nullptr;
     const void* owner = nullptr;
     int end_position = 0;
@@ -148,10 +174,14 @@ struct Ticket {
     std::unique_ptr<PinnedBuffer> logits, kv, blocks, ffn, scratch;
     std::vector<uint32_t> launch_epochs;  // generation: the exchange epoch of each launch, in order
     bool settled = false;                 // generation: the context's epoch has followed its stop
+    std::vector<hipEvent_t> round_events;  // LM-head step: start and end of every round
+    std::unique_ptr<PinnedBuffer> hidden;  // LM-head step: the staged input vector
 
     explicit Ticket(Kind k) : kind(k) { check(hipEventCreateWithFlags(&event, hipEventDisableTiming), "ticket event"); }
     ~Ticket()
     {
+        for (hipEvent_t e : round_events)
+            (void)hipEventDestroy(e);
         if (event)
             (void)hipEventDestroy(event);
         if (compute_start)
@@ -166,6 +196,7 @@ struct Context {
     hipStream_t stream = nullptr;
     DeviceBuffer input, output, scratch, kv, attention_scores, partials, logits, candidates, exchange, tokens, generated, status;
     DeviceBuffer block_trace, ffn_trace;
+    DeviceBuffer head_hidden, head_token;  // LM-head step: input vector and selected token
     DeviceBuffer timeline;
     bool timeline_enabled = false;
     // Prompts longer than one worker launch prefill all but their last token with matrices
@@ -498,6 +529,60 @@ struct Context {
         return t;
     }
 
+    // The LM-head step alone, `rounds` times: `hidden` (host, hidden_size elements of the weight
+    // type) through the final RMSNorm, the LM head and greedy selection, by the worker's logits
+    // tasks in launches of their own, each timed by HIP events around the worker launch.  Runs on
+    // an empty context and leaves it as a reset does.
+    std::shared_ptr<Ticket> lm_head_step(const void* hidden, int rounds, ti_diagnostic_request diag)
+    {
+        require_ready();
+        if (model->head_tasks == 0)
+            throw std::runtime_error("package has no LM-head tasks");
+        if (queued_position != 0)
+            throw std::runtime_error("LM-head step requires an empty sequence context");
+        if (rounds < 1)
+            throw std::runtime_error("LM-head step requires a positive round count");
+        if (diag.kv || diag.block_outputs)
+            throw std::runtime_error("LM-head step collects logits only");
+        const size_t bytes = static_cast<size_t>(model->meta.shape.hidden_size) * model->elem();
+        auto t = std::make_shared<Ticket>(Ticket::Kind::lm_head);
+        t->end_position = 0;
+        t->requested = 1;
+        try {
+            if (!head_hidden.ptr) {
+                head_hidden = DeviceBuffer(bytes);
+                head_token = DeviceBuffer(sizeof(ti_token_id));
+            }
+            t->hidden = std::make_unique<PinnedBuffer>(bytes);
+            std::memcpy(t->hidden->ptr, hidden, bytes);
+            check(hipMemcpyAsync(head_hidden.ptr, t->hidden->ptr, bytes, hipMemcpyHostToDevice, stream), "copy hidden vector");
+            t->output = std::make_unique<PinnedBuffer>(sizeof(ti_token_id));
+            for (int r = 0; r < rounds; ++r) {
+                hipEvent_t start = nullptr, end = nullptr;
+                check(hipEventCreate(&start), "timing event");
+                t->round_events.push_back(start);
+                check(hipEventCreate(&end), "timing event");
+                t->round_events.push_back(end);
+                ti_worker_buffers b = worker_buffers(false);
+                b.timeline = nullptr;
+                b.epoch = epoch;
+                check_ti(enqueue_lm_head_step(stream, model->head_view, b, head_hidden.ptr, head_token.as<ti_token_id>(), start,
+                                              end));
+                advance_epoch();
+            }
+            check(hipMemcpyAsync(t->output->ptr, head_token.ptr, sizeof(ti_token_id), hipMemcpyDeviceToHost, stream), "copy token");
+            finish_ticket(t, diag);
+            // As a reset leaves the context: no exchange word of these launches stays behind.
+            check(hipMemsetAsync(exchange.ptr, 0, exchange.bytes, stream), "reset exchange");
+            epoch = 1;
+        } catch (...) {
+            valid = false;
+            (void)hipStreamSynchronize(stream);
+            throw;
+        }
+        return t;
+    }
+
     std::shared_ptr<Ticket> reset()
     {
         pending.reset();
@@ -545,6 +630,27 @@ struct Context {
         }
         ti_completion out{};
         out.position = t->end_position;
+        if (t->kind == Ticket::Kind::lm_head) {
+            check_control(*t);
+            // compute_us: the median round's worker launch (HIP events around it alone).
+            std::vector<float> rounds;
+            for (size_t i = 0; i + 1 < t->round_events.size(); i += 2) {
+                float ms = 0.0f;
+                check(hipEventElapsedTime(&ms, t->round_events[i], t->round_events[i + 1]), "timing");
+                rounds.push_back(ms);
+            }
+            std::sort(rounds.begin(), rounds.end());
+            const size_t n = rounds.size();
+            out.compute_us = 500.0 * (rounds[(n - 1) / 2] + rounds[n / 2]);
+            const ti_token_id token = t->output->as<ti_token_id>()[0];
+            if (token == TI_NON_FINITE)
+                throw std::runtime_error("generation stopped: non-finite logits");
+            out.count = 1;
+            out.stop_reason = TI_STOP_LIMIT;
+            if (ids)
+                ids->assign(1, token);
+            return out;
+        }
         if (!t->generation) {
             try {
                 check_control(*t);
@@ -696,6 +802,18 @@ extern "C" int ti_context_generate(ti_context* context, int32_t max_new_tokens, 
     return guarded(TI_ERR_RUNTIME, [&] {
         auto t = std::make_unique<ti_ticket>();
         t->ticket = context->context->generate(max_new_tokens, eos_id, diag);
+        *out = t.release();
+    });
+}
+
+extern "C" int ti_context_lm_head_step(ti_context* context, const void* hidden, int32_t rounds, ti_diagnostic_request diag,
+                                       ti_ticket** out)
+{
+    if (!context || !hidden || !out)
+        return TI_ERR_INVALID_ARGUMENT;
+    return guarded(TI_ERR_RUNTIME, [&] {
+        auto t = std::make_unique<ti_ticket>();
+        t->ticket = context->context->lm_head_step(hidden, rounds, diag);
         *out = t.release();
     });
 }

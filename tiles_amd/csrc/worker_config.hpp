@@ -53,6 +53,20 @@ __host__ __device__ inline uint32_t epochs_per_step(int layers) { return static_
 inline constexpr int kMaxTaggedLayers = 120;
 static_assert(TI_MAX_LAUNCH_STEPS * kPhases * (kMaxTaggedLayers + 1) < 65535, "tagged exchange epochs");
 
+// The 16-bit tag of an epoch in a bf16 exchange half: never 0 (a cleared word), and distinct
+// for epochs less than 65535 apart.
+__host__ __device__ inline uint32_t exchange_tag(uint32_t epoch) { return epoch % 65535u + 1u; }
+
+// Greedy order of candidates (ops.cuh:895-911): the larger value wins, the lower ID among equal
+// values, and a non-finite candidate wins over everything and stays.
+__host__ __device__ inline void keep_better(ti_candidate& best, ti_candidate other)
+{
+    if (best.id == TI_NON_FINITE)
+        return;
+    if (other.id == TI_NON_FINITE || other.value > best.value || (other.value == best.value && other.id < best.id))
+        best = other;
+}
+
 // Word offsets into the exchange area.  Each word: payload in bits 0-31 (one bf16 or fp32
 // element, or a candidate field), writer's epoch in bits 32-63.  In bf16, the vectors every
 // worker reads (hidden0/1, attn, r) hold two elements per word instead, each a 32-bit half with
@@ -190,6 +204,13 @@ int launch_worker_f32(hipStream_t stream, const ti_worker_program_view& p, const
 // launch from another stream to complete (two launches cannot share the device).
 int enqueue_worker(hipStream_t s, const ti_worker_program_view& program, const ti_worker_buffers& buffers, int32_t position,
                    ti_token_input token, ti_selection selection, bool order_streams);
+// The LM-head step alone (lm_head.hip): `hidden` (device, hidden_size elements of the weight
+// type) published as the last layer's output of a launch at buffers.epoch, one step of `head`
+// (a program of the package's logits tasks only), then greedy selection of the candidates into
+// `token` (device).  The launch uses exchange epochs [buffers.epoch, + ti_epochs_per_launch).
+// worker_start / worker_end (optional) are recorded around the worker launch alone.
+int enqueue_lm_head_step(hipStream_t stream, const ti_worker_program_view& head, const ti_worker_buffers& buffers,
+                         const void* hidden, ti_token_id* token, hipEvent_t worker_start, hipEvent_t worker_end);
 std::vector<const void*> worker_functions_bf16();
 std::vector<const void*> worker_functions_f32();
 

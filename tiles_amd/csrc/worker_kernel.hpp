@@ -234,7 +234,7 @@ __device__ inline bool stuck(uint64_t* exchange, const ExchangeLayout& xl, uint3
 // a reader waits for (every launch writes every element at its first step, and a failed launch
 // requires a reset, which clears the exchange): 64 x 8 x (layers + 1) epochs, below 65535 for
 // the kMaxTaggedLayers layers the launcher accepts.
-__device__ inline uint32_t exchange_tag(uint32_t epoch) { return epoch % 65535u + 1u; }
+// exchange_tag (worker_config.hpp) maps an epoch to that tag.
 
 // Whether exchange word w carries `want`: in its high half (one element per word), or in the
 // high 16 bits of both halves (two tagged bf16 elements per word).
@@ -1942,14 +1942,6 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
             publish_element<BF16>(L.exchange + L.xl.hidden((layer + 1) % 2), row, y, L.epoch_of(step, layer, kPhaseY));
         }
     }
-}
-
-__device__ inline void keep_better(ti_candidate& best, ti_candidate other)
-{
-    if (best.id == TI_NON_FINITE)
-        return;
-    if (other.id == TI_NON_FINITE || other.value > best.value || (other.value == best.value && other.id < best.id))
-        best = other;
 }
 
 // The last layer's output (the final norm's input, decoder_stack.py:126-132), raw into the work

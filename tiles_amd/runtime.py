@@ -103,7 +103,7 @@ EXPORTS = ("ti_error_string", "ti_last_error_message", "ti_abi", "ti_fingerprint
            "ti_context_decode", "ti_context_generate", "ti_context_reset", "ti_context_ready", "ti_context_wait",
            "ti_context_diagnostic_sizes", "ti_context_collect", "ti_context_intermediate_sizes",
            "ti_context_collect_intermediates", "ti_ticket_free", "ti_context_set_timeline",
-           "ti_context_timeline", "ti_context_set_matrix_prefill")
+           "ti_context_timeline", "ti_context_set_matrix_prefill", "ti_context_lm_head_step")
 
 _lib = None
 
@@ -150,6 +150,7 @@ def library() -> C.CDLL:
         lib.ti_context_decode.argtypes = [P, token_id, DiagnosticRequest, C.POINTER(P)]
         lib.ti_context_generate.argtypes = [P, C.c_int32, token_id, DiagnosticRequest, C.POINTER(P)]
         lib.ti_context_reset.argtypes = [P, C.POINTER(P)]
+        lib.ti_context_lm_head_step.argtypes = [P, P, C.c_int32, DiagnosticRequest, C.POINTER(P)]
         lib.ti_context_ready.argtypes = [P, P]
         lib.ti_context_wait.argtypes = [P, P, C.POINTER(Completion), C.POINTER(token_id), C.c_size_t]
         lib.ti_context_diagnostic_sizes.argtypes = [P, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
@@ -326,6 +327,21 @@ class SequenceContext:
         _check(library().ti_context_wait(self._handle, ticket._handle, C.byref(done), ids, ticket.requested))
         return Result(list(ids[: done.count]) if ticket.requested else [], done.position,
                       STOP_REASONS.get(done.stop_reason, "none"), done.compute_us)
+
+    def enqueue_lm_head_step(self, hidden, rounds: int = 1, logits: bool = False) -> Ticket:
+        """The isolated LM-head step, `rounds` times, on an empty context: `hidden` (hidden_size
+        values, bf16 bits as uint16 for a bf16 package, float32 otherwise) through the final
+        RMSNorm, the LM head and greedy selection by the worker's logits tasks.  wait() gives
+        the token and, as compute_us, the median round's worker launch."""
+        import numpy as np
+        view = self.model.program_view()
+        vector = np.ascontiguousarray(hidden, dtype=np.uint16 if view.weight_dtype == 1 else np.float32)
+        if vector.size != view.shape.hidden_size:
+            raise ValueError("hidden vector of the wrong size")
+        handle = C.c_void_p()
+        _check(library().ti_context_lm_head_step(self._handle, vector.ctypes.data_as(C.c_void_p), int(rounds),
+                                                 self._request(logits, False, False), C.byref(handle)))
+        return Ticket(self, handle, "lm_head", 1)
 
     def set_matrix_prefill(self, enabled: bool) -> None:
         """Prefills of more than 64 tokens on bf16 stacks run all but the last token as matrices
