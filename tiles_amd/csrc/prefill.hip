@@ -9,8 +9,8 @@
 //   u = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * attn_norm)      rms_rows
 //   q, k, v = bf16(W u)                                          gemm_bf16 (MFMA, FP32 sums)
 //   q, k rotated as the worker rotates them; K, V rows -> cache  rope_rows
-//   s = bf16(bf16(q . k) / sqrt(dh)); P = bf16(exp(s - M) / S)   attention_rows (causal, exact
-//   attention = bf16(sum P v)                                    softmax statistics per row)
+//   s = bf16(bf16(q . k) * (1 / sqrt(dh)));                       attention_tiles (causal: M the
+//   P = bf16(exp(s - M) / S); attention = bf16(sum P v)          row's maximum, S its FP32 exp-sum)
 //   r = bf16(bf16(Wo attention) + x)                             GEMM, add_rows
 //   z = RMSNorm(r) with ffn_norm                                 rms_rows
 //   p = bf16(bf16(silu(bf16(Wgate z))) * bf16(Wup z))            GEMMs, silu_rows
@@ -109,94 +109,170 @@ __global__ void __launch_bounds__(kRowThreads) rope_rows(const uint16_t* qkv, in
         value_cache[static_cast<size_t>(pos) * nkv * dh + index] = src[(nq + nkv) * dh + index];
 }
 
-// Causal attention of row r (position `position + r`) for the query heads of K/V head h: one
-// wave per query head of the group.  Pass 1 finds each head's maximum score M and
-// S = sum exp(s - M) over positions 0..pos, a tile of 64 positions (one per lane) at a time,
-// rescaling S when M grows; pass 2 recomputes the scores, rounds P = exp(s - M) / S to bf16 and
-// adds P V in FP32 through LDS, and the result is rounded once.
+// Causal attention on the matrix cores, for 64 rows (positions position + r0 ..) and every
+// query head of K/V head blockIdx.y: wave w takes rows r0 + 16 w .. + 15.  Scores are
+// computed transposed, S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A: 16 key rows of the cache, B:
+// the 16 query rows of one head), so that lane l holds query l % 16 against keys 4 (l / 16) + i of
+// each 16-key subtile.  Each score is bf16(bf16(dot) * scale) (the decode worker's score_of), keys past the
+// query's position are masked.  Pass 1 keeps each lane's running maximum and exp-sum per head,
+// rescaled when the maximum grows, and merges the four lanes of a query at the end (exact
+// maximum M, FP32 S).  Pass 2 recomputes the scores, rounds P = exp(s - M) / S to bf16 in
+// registers and takes P V on the matrix cores with P as the A operand straight from the score
+// layout: a 32-key step's k-elements 8 g .. 8 g + 7 of lane group g are keys 4 g .. 4 g + 3 and
+// 16 + 4 g .. + 3 of the step (the sum over keys does not depend on their order), and V^T, staged
+// in LDS per 64-key tile, supplies the same keys as two 8-byte reads.  The output is rounded
+// once.  Keys past the block's last position are clamped to it when loaded and masked.
+constexpr int kAttnThreads = 256;
+constexpr int kAttnRows = 64;  // query positions per block: 16 per wave
+
 template <int DH>
-__global__ void __launch_bounds__(kRowThreads) attention_rows(const uint16_t* q_rot, int position, int nq, int nkv,
-                                                              const uint16_t* key_cache, const uint16_t* value_cache,
-                                                              float scale, uint16_t* out)
+__global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* q_rot, int position, int rows, int nq, int nkv,
+                                                                const uint16_t* key_cache, const uint16_t* value_cache,
+                                                                float scale, uint16_t* out)
 {
-    constexpr int kPairs = DH / 2;
-    constexpr int kVectors = DH / 8;  // 16-byte vectors of a K or V row
-    __shared__ float probability[kMaxGroup][kTile];
-    __shared__ uint16_t values[kTile][DH];
-    const int r = blockIdx.x / nkv, h = blockIdx.x - r * nkv;
-    const int group = nq / nkv;
-    const int pos = position + r;
-    const int length = pos + 1;
+    constexpr int KS = DH / 32;       // 32-dim steps of a score
+    constexpr int NT = DH / 16;       // 16-dim output tiles
+    constexpr int kVtStride = kTile + 8;  // bf16 per V^T row: 144 bytes, 16-byte aligned
+    __shared__ __attribute__((aligned(16))) uint16_t vt[DH * kVtStride];
+    const int h = blockIdx.y, group = nq / nkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x / 64;
-    const int head = h * group + (wave < group ? wave : 0);
-    // The lane's copy of its head's query as packed bf16 pairs.
-    uint32_t q[kPairs];
-    const uint32_t* qsrc = reinterpret_cast<const uint32_t*>(q_rot + (static_cast<size_t>(r) * nq + head) * DH);
+    const int col = lane & 15, g4 = lane >> 4;
+    const int r0 = blockIdx.x * kAttnRows;
+    const int last_row = min(r0 + kAttnRows, rows) - 1;
+    const int last_key = position + last_row;  // the block's last key: every load stays at or below it
+    const int tiles = last_key / kTile + 1;
+    const int qrow = r0 + 16 * wave + col;     // this lane's query row (B operand, output column)
+    const int qpos = position + qrow;
+
+    // B operands of the scores: query row qrow of each head, dims 32 k + 8 g4 .. + 7.
+    u32x4 qb[kMaxGroup][KS];
 #pragma unroll
-    for (int j = 0; j < kPairs; ++j)
-        q[j] = qsrc[j];
-    auto score = [&](int t) {
-        const u32x4* krow = reinterpret_cast<const u32x4*>(key_cache + (static_cast<size_t>(t) * nkv + h) * DH);
-        float a = 0.0f, b = 0.0f;
+    for (int g = 0; g < kMaxGroup; ++g)
 #pragma unroll
-        for (int v = 0; v < kVectors; ++v) {
-            const u32x4 k = krow[v];
-            a = dot2_bf16(k[0], q[4 * v], a);
-            b = dot2_bf16(k[1], q[4 * v + 1], b);
-            a = dot2_bf16(k[2], q[4 * v + 2], a);
-            b = dot2_bf16(k[3], q[4 * v + 3], b);
+        for (int k = 0; k < KS; ++k) {
+            const bool live = g < group && qrow < rows;
+            const size_t at = (static_cast<size_t>(live ? qrow : 0) * nq + h * group + (live ? g : 0)) * DH + 32 * k + 8 * g4;
+            qb[g][k] = live ? *reinterpret_cast<const u32x4*>(q_rot + at) : u32x4{0u, 0u, 0u, 0u};
         }
-        return Bf::round(Bf::round(a + b) * scale);
+    // Scores of subtile j of tile kt for every head: s[g][i] at key 64 kt + 16 j + 4 g4 + i.
+    auto scores = [&](int kt, int j, float (&s)[kMaxGroup][4]) {
+        const int key = min(kt * kTile + 16 * j + col, last_key);  // A row: key `key`
+        u32x4 ka[KS];
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+            ka[k] = *reinterpret_cast<const u32x4*>(key_cache + (static_cast<size_t>(key) * nkv + h) * DH + 32 * k + 8 * g4);
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                acc = mfma_16x16x32_bf16(ka[k], qb[g][k], acc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = kt * kTile + 16 * j + 4 * g4 + i;
+                s[g][i] = t <= qpos && qrow < rows ? Bf::round(Bf::round(acc[i]) * scale) : -INFINITY;
+            }
+        }
     };
-    float m = -INFINITY, total = 0.0f;
-    if (wave < group)
-        for (int base = 0; base < length; base += kTile) {
-            const int t = base + lane;
-            const float s = t < length ? score(t) : -INFINITY;
-            float tile_max = s;
-            for (int offset = 32; offset > 0; offset >>= 1)
-                tile_max = fmaxf(tile_max, __shfl_xor(tile_max, offset));
-            const float grown = fmaxf(m, tile_max);
-            float e = t < length ? expf(s - grown) : 0.0f;
-            for (int offset = 32; offset > 0; offset >>= 1)
-                e += __shfl_xor(e, offset);
-            total = total * expf(m - grown) + e;
-            m = grown;
-        }
-    constexpr int kOutputs = (kMaxGroup * DH + kRowThreads - 1) / kRowThreads;
-    float acc[kOutputs] = {};
-    for (int base = 0; base < length; base += kTile) {
-        if (wave < group) {
-            const int t = base + lane;
-            probability[wave][lane] = t < length ? Bf::round(expf(score(t) - m) / total) : 0.0f;
-        }
-        for (int index = threadIdx.x; index < kTile * kVectors; index += kRowThreads) {
-            const int t = index / kVectors, v = index - t * kVectors;
-            const u32x4 row = base + t < length
-                                  ? reinterpret_cast<const u32x4*>(value_cache + (static_cast<size_t>(base + t) * nkv + h) * DH)[v]
-                                  : u32x4{0u, 0u, 0u, 0u};
-            reinterpret_cast<u32x4*>(values[t])[v] = row;
-        }
-        __syncthreads();
+
+    // Pass 1: this lane's running maximum and exp-sum per head, over its keys.
+    float m[kMaxGroup], total[kMaxGroup];
 #pragma unroll
-        for (int k = 0; k < kOutputs; ++k) {
-            const int o = threadIdx.x + k * kRowThreads;
-            if (o < group * DH) {
-                const int g = o / DH, j = o - g * DH;
-                float sum = acc[k];
-                for (int t = 0; t < kTile; ++t)
-                    sum = fmaf(probability[g][t], bf(values[t][j]), sum);
-                acc[k] = sum;
+    for (int g = 0; g < kMaxGroup; ++g) {
+        m[g] = -INFINITY;
+        total[g] = 0.0f;
+    }
+    for (int kt = 0; kt < tiles; ++kt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float s[kMaxGroup][4];
+            scores(kt, j, s);
+#pragma unroll
+            for (int g = 0; g < kMaxGroup; ++g) {
+                const float grown = fmaxf(m[g], fmaxf(fmaxf(s[g][0], s[g][1]), fmaxf(s[g][2], s[g][3])));
+                if (grown == -INFINITY)
+                    continue;  // every key so far masked
+                float sum = total[g] * expf(m[g] - grown);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    sum += expf(s[g][i] - grown);
+                total[g] = sum;
+                m[g] = grown;
+            }
+        }
+    // The four lanes of a query (lane groups g4 = 0..3) merge: M exact, S rescaled to it.
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+        for (int offset = 16; offset < 64; offset <<= 1) {
+            const float om = __shfl_xor(m[g], offset), ot = __shfl_xor(total[g], offset);
+            const float grown = fmaxf(m[g], om);
+            if (grown != -INFINITY) {
+                total[g] = total[g] * expf(m[g] - grown) + ot * expf(om - grown);
+                m[g] = grown;
+            }
+        }
+
+    // Pass 2: P = bf16(exp(s - M) / S) as A operands, P V against V^T from LDS.
+    f32x4 o[kMaxGroup][NT];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+            o[g][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kt = 0; kt < tiles; ++kt) {
+        __syncthreads();  // the previous tile's V^T reads are done
+        for (int index = threadIdx.x; index < kTile * (DH / 8); index += kAttnThreads) {
+            const int t = index / (DH / 8), v = index - t * (DH / 8);
+            const int key = min(kt * kTile + t, last_key);
+            const u32x4 row = *reinterpret_cast<const u32x4*>(value_cache + (static_cast<size_t>(key) * nkv + h) * DH + 8 * v);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                vt[(8 * v + 2 * q) * kVtStride + t] = static_cast<uint16_t>(row[q]);
+                vt[(8 * v + 2 * q + 1) * kVtStride + t] = static_cast<uint16_t>(row[q] >> 16);
             }
         }
         __syncthreads();
-    }
 #pragma unroll
-    for (int k = 0; k < kOutputs; ++k) {
-        const int o = threadIdx.x + k * kRowThreads;
-        if (o < group * DH)
-            out[static_cast<size_t>(r) * nq * DH + h * group * DH + o] = bits16(Bf::round(acc[k]));
+        for (int step = 0; step < 2; ++step) {  // keys 32 step .. + 31 of the tile
+            float s0[kMaxGroup][4], s1[kMaxGroup][4];
+            scores(kt, 2 * step, s0);
+            scores(kt, 2 * step + 1, s1);
+            u32x4 vb[NT];
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                const uint16_t* row = vt + (16 * n + col) * kVtStride + 32 * step + 4 * g4;
+                const uint2 lo = *reinterpret_cast<const uint2*>(row), hi = *reinterpret_cast<const uint2*>(row + 16);
+                vb[n] = u32x4{lo.x, lo.y, hi.x, hi.y};
+            }
+#pragma unroll
+            for (int g = 0; g < kMaxGroup; ++g) {
+                if (g >= group)
+                    continue;
+                float p[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    p[i] = s0[g][i] == -INFINITY ? 0.0f : Bf::round(expf(s0[g][i] - m[g]) / total[g]);
+                    p[4 + i] = s1[g][i] == -INFINITY ? 0.0f : Bf::round(expf(s1[g][i] - m[g]) / total[g]);
+                }
+                const u32x4 pa = {pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                    o[g][n] = mfma_16x16x32_bf16(pa, vb[n], o[g][n]);
+            }
+        }
     }
+    // o[g][n]: lane l holds query rows r0 + 16 wave + 4 g4 + i, dim 16 n + col.
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = r0 + 16 * wave + 4 * g4 + i;
+            if (g < group && r < rows)
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                    out[(static_cast<size_t>(r) * nq + h * group + g) * DH + 16 * n + col] = bits16(Bf::round(o[g][n][i]));
+        }
 }
 
 // out = bf16(a + b) elementwise (a and b bf16).
@@ -400,11 +476,12 @@ int MatrixPrefill::layer(hipStream_t stream, void* kv, int layer, int position, 
     hipLaunchKernelGGL(rope_rows, dim3(rows), dim3(kRowThreads), 0, stream, v.qkv, position, p_.rotary_frequencies, nq, nkv, dh,
                        v.q, cache + w.key, cache + w.value);
     const float scale = 1.0f / sqrtf(static_cast<float>(dh));
+    const dim3 attention_grid((rows + kAttnRows - 1) / kAttnRows, nkv);
     if (dh == 64)
-        hipLaunchKernelGGL(attention_rows<64>, dim3(rows * nkv), dim3(kRowThreads), 0, stream, v.q, position, nq, nkv,
+        hipLaunchKernelGGL(attention_tiles<64>, attention_grid, dim3(kAttnThreads), 0, stream, v.q, position, rows, nq, nkv,
                            cache + w.key, cache + w.value, scale, v.attention);
     else
-        hipLaunchKernelGGL(attention_rows<128>, dim3(rows * nkv), dim3(kRowThreads), 0, stream, v.q, position, nq, nkv,
+        hipLaunchKernelGGL(attention_tiles<128>, attention_grid, dim3(kAttnThreads), 0, stream, v.q, position, rows, nq, nkv,
                            cache + w.key, cache + w.value, scale, v.attention);
     if (!gemm_ok(gemm(stream, true, v.attention, rows, qw, base + w.Wo, d, v.projected, d)))
         return code;
