@@ -204,6 +204,17 @@ class SequenceContext {
         detail::check(ti_context_reset(context_.get(), &t));
         return Ticket(t, 0, {});
     }
+    // Extensions without a counterpart in the reference's runtime.hpp (ti_context_lm_head_step,
+    // ti_context_set_matrix_prefill): the isolated LM-head step on an empty context, `hidden`
+    // holding hidden_size elements of the package's weight type (bf16 bits or float); wait()
+    // gives the token and, as compute_us, the median round's worker launch.
+    Ticket enqueue_lm_head_step(const void* hidden, int rounds = 1, DiagnosticRequest diagnostics = {})
+    {
+        ti_ticket* t = nullptr;
+        detail::check(ti_context_lm_head_step(context_.get(), hidden, rounds, raw(diagnostics), &t));
+        return Ticket(t, 1, diagnostics);
+    }
+    void set_matrix_prefill(bool enabled) { detail::check(ti_context_set_matrix_prefill(context_.get(), enabled ? 1 : 0)); }
     // Marks the context invalid if the queued work failed.
     [[nodiscard]] bool ready(const Ticket& ticket)
     {

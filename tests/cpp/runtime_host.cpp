@@ -1,6 +1,7 @@
 // A host written against include/tileinfer_amd.hpp the way one is written against the
 // reference's runtime.hpp (sequence_context_smoke.cpp:60-166 drives the same calls): one model,
-// two contexts sharing it, prefill, decode with diagnostics, generate, reset, move-only tickets.
+// two contexts sharing it, prefill, decode with diagnostics, generate, reset, move-only tickets;
+// then the extensions: the isolated LM-head step on the reset context (hidden = bf16 ones).
 // Prints one JSON line.  TEST INFRASTRUCTURE ONLY (tests/test_cpp_runtime.py).
 #include "tileinfer_amd.hpp"
 
@@ -44,13 +45,17 @@ int main(int argc, char** argv)
         while (!a.ready(r)) {
         }
         const tileinfer::Completion after_reset = a.wait(r);
+        const std::vector<unsigned short> ones(256, 0x3f80);
+        tileinfer::Ticket h = a.enqueue_lm_head_step(ones.data(), 2);
+        const tileinfer::Completion head = a.wait(h);
         std::printf("{\"generated\":%s,\"position\":%d,\"stop\":\"%s\",\"b_position\":%d,\"b_logits\":%zu,"
-                    "\"b_argmax\":%d,\"b_kv\":%zu,\"reset_position\":%d}\n",
+                    "\"b_argmax\":%d,\"b_kv\":%zu,\"reset_position\":%d,\"head_token\":%d}\n",
                     ints(ca.generated).c_str(), ca.position,
                     ca.stop_reason == tileinfer::StopReason::limit ? "limit"
                     : ca.stop_reason == tileinfer::StopReason::eos ? "eos"
                                                                     : "none",
-                    cb.position, diag.logits.size(), argmax, diag.kv.size(), after_reset.position);
+                    cb.position, diag.logits.size(), argmax, diag.kv.size(), after_reset.position,
+                    head.generated.empty() ? -1 : head.generated[0]);
         return 0;
     } catch (const tileinfer::Error& e) {
         std::fprintf(stderr, "runtime_host: %s (code %d)\n", e.what(), e.code());

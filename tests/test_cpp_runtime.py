@@ -61,6 +61,9 @@ def test_cpp_host_matches_the_python_binding(tmp_path):
     assert got["b_logits"] == 512 and got["b_argmax"] == int(np.argmax(logits))
     assert got["b_kv"] == 0  # not requested: empty, as the reference's collect
     assert got["reset_position"] == 0
+    head = model.create_context()
+    want_head = head.wait(head.enqueue_lm_head_step(np.full(256, 0x3F80, dtype=np.uint16), rounds=2)).generated
+    assert got["head_token"] == want_head[0]
     # and the tokens are the oracle's
     packed = K.read_weights(tmp_path / "pkg", spec, "bfloat16")
     ospec = ref.Spec(hidden_size=256, intermediate_size=512, num_attention_heads=4, num_key_value_heads=1,
