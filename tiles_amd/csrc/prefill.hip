@@ -111,17 +111,19 @@ __global__ void __launch_bounds__(kRowThreads) rope_rows(const uint16_t* qkv, in
 
 // Causal attention on the matrix cores, for 64 rows (positions position + r0 ..) and every
 // query head of K/V head blockIdx.y: wave w takes rows r0 + 16 w .. + 15.  Scores are
-// computed transposed, S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A: 16 key rows of the cache, B:
-// the 16 query rows of one head), so that lane l holds query l % 16 against keys 4 (l / 16) + i of
-// each 16-key subtile.  Each score is bf16(bf16(dot) * scale) (the decode worker's score_of), keys past the
-// query's position are masked.  Pass 1 keeps each lane's running maximum and exp-sum per head,
-// rescaled when the maximum grows, and merges the four lanes of a query at the end (exact
+// computed transposed, S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A: 16 key rows, B: the 16
+// query rows of one head), so that lane l holds query l % 16 against keys 4 (l / 16) + i of each
+// 16-key subtile.  Each score is bf16(bf16(dot) * scale) (the decode worker's score_of), keys past
+// the query's position are masked.  Pass 1 keeps each lane's running maximum and exp-sum per
+// head, rescaled when the maximum grows, and merges the four lanes of a query at the end (exact
 // maximum M, FP32 S).  Pass 2 recomputes the scores, rounds P = exp(s - M) / S to bf16 in
 // registers and takes P V on the matrix cores with P as the A operand straight from the score
 // layout: a 32-key step's k-elements 8 g .. 8 g + 7 of lane group g are keys 4 g .. 4 g + 3 and
-// 16 + 4 g .. + 3 of the step (the sum over keys does not depend on their order), and V^T, staged
-// in LDS per 64-key tile, supplies the same keys as two 8-byte reads.  The output is rounded
-// once.  Keys past the block's last position are clamped to it when loaded and masked.
+// 16 + 4 g .. + 3 of the step (the sum over keys does not depend on their order), and V^T
+// supplies the same keys as two 8-byte reads.  The block stages each 64-key tile's K rows (and,
+// in pass 2, V^T) in LDS once for its four waves, while the next tile's rows load into registers.
+// The output is rounded once.  Keys past the block's last position are clamped to it when loaded
+// and masked.
 constexpr int kAttnThreads = 256;
 constexpr int kAttnRows = 64;  // query positions per block: 16 per wave
 
@@ -130,10 +132,15 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
                                                                 const uint16_t* key_cache, const uint16_t* value_cache,
                                                                 float scale, uint16_t* out)
 {
-    constexpr int KS = DH / 32;       // 32-dim steps of a score
-    constexpr int NT = DH / 16;       // 16-dim output tiles
-    constexpr int kVtStride = kTile + 8;  // bf16 per V^T row: 144 bytes, 16-byte aligned
+    constexpr int KS = DH / 32;                              // 32-dim steps of a score
+    constexpr int NT = DH / 16;                              // 16-dim output tiles
+    constexpr int kVtStride = kTile + 8;                     // bf16 per V^T row: 144 bytes
+    constexpr int kKStride = DH + 8;                         // bf16 per staged K row
+    constexpr int kVectors = DH / 8;                         // 16-byte vectors of a K or V row
+    constexpr int kLoads = kTile * kVectors / kAttnThreads;  // vectors per thread per tile
+    static_assert(kTile * kVectors % kAttnThreads == 0, "whole vectors per thread");
     __shared__ __attribute__((aligned(16))) uint16_t vt[DH * kVtStride];
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kTile * kKStride];
     const int h = blockIdx.y, group = nq / nkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x / 64;
     const int col = lane & 15, g4 = lane >> 4;
@@ -154,13 +161,39 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
             const size_t at = (static_cast<size_t>(live ? qrow : 0) * nq + h * group + (live ? g : 0)) * DH + 32 * k + 8 * g4;
             qb[g][k] = live ? *reinterpret_cast<const u32x4*>(q_rot + at) : u32x4{0u, 0u, 0u, 0u};
         }
-    // Scores of subtile j of tile kt for every head: s[g][i] at key 64 kt + 16 j + 4 g4 + i.
+    // This thread's vectors of tile kt's rows (K or V cache), keys clamped to the last key.
+    auto load_rows = [&](const uint16_t* cache, int kt, u32x4 (&r)[kLoads]) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int index = threadIdx.x + i * kAttnThreads, t = index / kVectors, v = index - t * kVectors;
+            const int key = min(kt * kTile + t, last_key);
+            r[i] = *reinterpret_cast<const u32x4*>(cache + (static_cast<size_t>(key) * nkv + h) * DH + 8 * v);
+        }
+    };
+    auto stage_k = [&](const u32x4 (&r)[kLoads]) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int index = threadIdx.x + i * kAttnThreads, t = index / kVectors, v = index - t * kVectors;
+            *reinterpret_cast<u32x4*>(ks + t * kKStride + 8 * v) = r[i];
+        }
+    };
+    auto stage_vt = [&](const u32x4 (&r)[kLoads]) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int index = threadIdx.x + i * kAttnThreads, t = index / kVectors, v = index - t * kVectors;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                vt[(8 * v + 2 * q) * kVtStride + t] = static_cast<uint16_t>(r[i][q]);
+                vt[(8 * v + 2 * q + 1) * kVtStride + t] = static_cast<uint16_t>(r[i][q] >> 16);
+            }
+        }
+    };
+    // Scores of subtile j of the staged tile kt for every head: s[g][i] at key 64 kt + 16 j + 4 g4 + i.
     auto scores = [&](int kt, int j, float (&s)[kMaxGroup][4]) {
-        const int key = min(kt * kTile + 16 * j + col, last_key);  // A row: key `key`
         u32x4 ka[KS];
 #pragma unroll
         for (int k = 0; k < KS; ++k)
-            ka[k] = *reinterpret_cast<const u32x4*>(key_cache + (static_cast<size_t>(key) * nkv + h) * DH + 32 * k + 8 * g4);
+            ka[k] = *reinterpret_cast<const u32x4*>(ks + (16 * j + col) * kKStride + 32 * k + 8 * g4);
 #pragma unroll
         for (int g = 0; g < kMaxGroup; ++g) {
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -182,7 +215,13 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
         m[g] = -INFINITY;
         total[g] = 0.0f;
     }
-    for (int kt = 0; kt < tiles; ++kt)
+    u32x4 kr[kLoads], vr[kLoads];
+    load_rows(key_cache, 0, kr);
+    for (int kt = 0; kt < tiles; ++kt) {
+        __syncthreads();  // the previous tile's K reads are done
+        stage_k(kr);
+        load_rows(key_cache, kt + 1, kr);  // the next tile (clamped past the last) in flight
+        __syncthreads();
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float s[kMaxGroup][4];
@@ -200,6 +239,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
                 m[g] = grown;
             }
         }
+    }
     // The four lanes of a query (lane groups g4 = 0..3) merge: M exact, S rescaled to it.
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g)
@@ -220,18 +260,14 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
 #pragma unroll
         for (int n = 0; n < NT; ++n)
             o[g][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    load_rows(key_cache, 0, kr);
+    load_rows(value_cache, 0, vr);
     for (int kt = 0; kt < tiles; ++kt) {
-        __syncthreads();  // the previous tile's V^T reads are done
-        for (int index = threadIdx.x; index < kTile * (DH / 8); index += kAttnThreads) {
-            const int t = index / (DH / 8), v = index - t * (DH / 8);
-            const int key = min(kt * kTile + t, last_key);
-            const u32x4 row = *reinterpret_cast<const u32x4*>(value_cache + (static_cast<size_t>(key) * nkv + h) * DH + 8 * v);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                vt[(8 * v + 2 * q) * kVtStride + t] = static_cast<uint16_t>(row[q]);
-                vt[(8 * v + 2 * q + 1) * kVtStride + t] = static_cast<uint16_t>(row[q] >> 16);
-            }
-        }
+        __syncthreads();  // the previous tile's K and V^T reads are done
+        stage_k(kr);
+        stage_vt(vr);
+        load_rows(key_cache, kt + 1, kr);
+        load_rows(value_cache, kt + 1, vr);
         __syncthreads();
 #pragma unroll
         for (int step = 0; step < 2; ++step) {  // keys 32 step .. + 31 of the tile
