@@ -133,18 +133,19 @@ def test_matrix_prefill_matches_the_worker_and_the_oracle(tmp_path):
 
 
 def test_matrix_prefill_over_a_chunk_boundary(tmp_path):
-    """2100 tokens: positions 0..2047 are one matrix pass, 2048..2098 the next, attending to the
-    rows the first pass cached, 2099 the worker.  Bars of check_against_oracle over all 2099
-    rows, and rows 2040..2059 of layer 0 within 1 ulp of the oracle's."""
-    spec, path, packed, ospec = build(tmp_path, 256, 512, 4, 1, 2, 512, 2200, seed=42)
-    prompt = np.random.default_rng(7).integers(0, 512, 2100).tolist()
+    """4200 tokens: positions 0..4095 are one matrix pass (MatrixPrefill::kChunkRows), 4096..4198
+    the next, attending to the rows the first pass cached, 4199 the worker.  Bars of
+    check_against_oracle over all 4199 rows, and rows 4090..4109 of layer 0 within 1 ulp of the
+    oracle's."""
+    spec, path, packed, ospec = build(tmp_path, 256, 512, 4, 1, 2, 512, 4300, seed=42)
+    prompt = np.random.default_rng(7).integers(0, 512, 4200).tolist()
     got = prefill_both(path, prompt, 4)
     plan = K.read_plan(path)
     assert not check_against_oracle(got, plan, prompt, packed, ospec, 2, 64)
     oracle, _ = oracle_kv_and_logits(prompt, packed, ospec, 1, 64)
-    matrix = kv_rows(got["matrix"][0], plan, 1, 2100, 64)
+    matrix = kv_rows(got["matrix"][0], plan, 1, 4200, 64)
     for i in range(2):
-        assert bf16_ulps(matrix[0][i][2040:2060], oracle[0][i][2040:2060]).max() <= 1
+        assert bf16_ulps(matrix[0][i][4090:4110], oracle[0][i][4090:4110]).max() <= 1
 
 
 def test_matrix_prefill_at_llama_width(tmp_path):

@@ -14,7 +14,7 @@ namespace tiles {
 class MatrixPrefill {
   public:
     // Positions per pass through the layers: the activation buffers hold this many rows.
-    static constexpr int kChunkRows = 2048;
+    static constexpr int kChunkRows = 4096;
 
     explicit MatrixPrefill(const ti_worker_program_view& program);
     ~MatrixPrefill();
