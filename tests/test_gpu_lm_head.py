@@ -100,3 +100,43 @@ def test_lm_head_step_leaves_the_context_empty(head):
         used.enqueue_lm_head_step(bits_of(h))
     used.wait(used.enqueue_reset())
     assert used.wait(used.enqueue_lm_head_step(bits_of(h))).generated == first
+
+
+def test_lm_head_step_fp32_and_small_bf16(tmp_path):
+    """The step on small stacks of both element types (hidden 256, vocabulary 512, one layer):
+    fp32 logits within 1e-5 of the oracle's FP32 final norm and GEMV, bf16 logits bit-equal to the
+    exactly evaluated contract in at least 99% of entries, and both tokens the oracle's wherever
+    its top-2 gap exceeds that difference."""
+    block = P.BlockSpec(hidden_size=256, intermediate_size=512, num_attention_heads=4, num_key_value_heads=1,
+                        head_dim=64, max_context=8)
+    spec = P.StackSpec(block, 1, 512, True)
+    ospec = ref.Spec(hidden_size=256, intermediate_size=512, num_attention_heads=4, num_key_value_heads=1,
+                     head_dim=64, max_context=8, layers=1, vocab_size=512)
+    weights = K.random_weights(spec, seed=23, std=0.08, dtype=torch.float32)
+    generator = torch.Generator().manual_seed(24)
+    for dtype, tdt in (("float32", torch.float32), ("bfloat16", torch.bfloat16)):
+        path = tmp_path / dtype
+        K.build_stack_package(spec, weights, probe.probe_library(), path, dtype)
+        packed = K.read_weights(path, spec, dtype)
+        ctx = R.DecoderModel(R.load_plan(path)).create_context()
+        for _ in range(3):
+            h = torch.randn(256, generator=generator).to(tdt)
+            vector = h.numpy() if dtype == "float32" else bits_of(h)
+            ticket = ctx.enqueue_lm_head_step(vector, rounds=1, logits=True)
+            logits = ctx.collect(ticket)["logits"]
+            token = ctx.wait(ticket).generated[0]
+            with torch.inference_mode():
+                want = (packed["embedding"] @ ref.final_norm(h, packed["final_norm"], ospec.rms_norm_eps)).float().numpy()
+            if dtype == "float32":
+                diff = float(np.abs(logits - want).max())
+                assert diff <= 1e-5, diff
+            else:
+                contract = C64.Contract({"final_norm": packed["final_norm"]}, ospec)
+                exact = C64.bf16(C64.as64(packed["embedding"]) @ contract.rms_norm(C64.as64(h), contract.w["final_norm"]))
+                assert float((logits == exact).mean()) >= 0.99
+                diff = float(np.abs(logits - want).max())
+            top = np.sort(want)[-2:]
+            print(f"{dtype}: token {token}, oracle {int(np.argmax(want))}, max |got - oracle| {diff:.3g}, "
+                  f"top-2 gap {top[1] - top[0]:.3g}", flush=True)
+            if top[1] - top[0] > diff:
+                assert token == int(np.argmax(want))
