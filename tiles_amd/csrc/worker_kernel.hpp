@@ -1199,9 +1199,11 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 if ((tile0 + gi * kWaves) * kTile < span)
                     tile_scores(tile0 + gi * kWaves, kb[gi]);
         }
+        // V^T columns past the chunk's last 32-position step are never read: P V stops there.
+        const int live0 = min(kBlockTiles, 2 * ((min(span, PB) + 31) / 32));
 #pragma unroll
         for (int j = 0; j < TW; ++j)
-            if (wave + j * kWaves < kBlockTiles)
+            if (wave + j * kWaves < live0)
                 write_vt(0, j, vfirst[j]);
     } else {
         // Scores of rows [begin, end).  Every lane holds its slice of all MG query heads (heads
@@ -1444,11 +1446,12 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         // The next block's V tiles load while this block's P V runs.
         u32x4 vnext[TW][KS];
         for (int first = 0; first < span; first += PB) {
+            const int steps = (min(span - first, PB) + 31) / 32;  // 32-position steps of this block
             if (first > 0) {
                 block_sync(sh);  // the previous block's V^T has been read
 #pragma unroll
                 for (int j = 0; j < TW; ++j)
-                    if (wave + j * kWaves < kBlockTiles)
+                    if (wave + j * kWaves < min(kBlockTiles, 2 * steps))
                         write_vt(first / kTile, j, vnext[j]);
                 block_sync(sh);
             }
@@ -1460,6 +1463,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
                 for (int q = 0; q < PB / 32; ++q) {
+                    if (q >= steps)
+                        break;
                     const int t0 = first + 32 * q + 8 * tk;
                     const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + vt_row(16 * n + tr) + 32 * q + 8 * tk);
                     const u32x4 p = *reinterpret_cast<const u32x4*>(pbits + (tr < group ? tr : 0) * span_pad + t0);
@@ -1469,6 +1474,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             } else if (n < dh / 16) {
 #pragma unroll
                 for (int q = 0; q < PB / 32; ++q) {
+                    if (q >= steps)
+                        break;
                     const int t0 = first + 32 * q + 8 * tk;
                     const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + vt_row(16 * n + tr) + 32 * q + 8 * tk);
                     float p[8];
