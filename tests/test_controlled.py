@@ -1,5 +1,6 @@
 """Statistics and telemetry parsing of the controlled timing protocol (tiles_amd/controlled.py),
-on the CPU: the paired bootstrap recovers a known shift, and amd-smi JSON flattens to numeric
+on the CPU: the paired bootstrap recovers a known shift, the restart in reverse spawn order
+separates a placement effect from a real difference, and amd-smi JSON flattens to numeric
 leaves keyed by path."""
 
 import numpy as np
@@ -29,3 +30,16 @@ def test_amd_smi_records_flatten_to_numeric_leaves():
     flat = C.flatten(record)
     assert flat == {"gpu": 0.0, "power.socket_power": 312.0, "clock.gfx_0.clk": 2100.0, "clock.gfx_0.max_clk": 2400.0,
                     "temperature.hotspot": 55.0}
+
+
+def test_spawn_order_effect_is_separated_from_the_difference():
+    """Arm B is 1.0 us slower than A; the first-started server runs 0.6 us faster, A started first
+    in blocks 0-2 and B in blocks 3-5.  The paired mean over both halves is the real 1.0 us, and
+    half the halves' difference is the 0.6 us placement effect."""
+    base = [640.0, 640.4, 639.8, 640.2, 640.1, 639.9]
+    a = [t - (0.6 if k < 3 else 0.0) for k, t in enumerate(base)]
+    b = [t + 1.0 - (0.0 if k < 3 else 0.6) for k, t in enumerate(base)]
+    assert abs(C.paired(a, b, seed=4)["mean_us"] - 1.0) < 1e-9
+    effect = C.spawn_order_effect(a, b, 3)
+    assert abs(effect["first_half_mean_us"] - 1.6) < 1e-9 and abs(effect["second_half_mean_us"] - 0.4) < 1e-9
+    assert abs(effect["spawn_order_effect_us"] - 0.6) < 1e-9

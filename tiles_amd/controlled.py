@@ -194,6 +194,15 @@ def paired(reference: list[float], other: list[float], seed: int) -> dict:
             "ci95_percent": [100 * float(low) / base, 100 * float(high) / base], "pairs": len(d)}
 
 
+def spawn_order_effect(reference: list[float], other: list[float], half: int) -> dict:
+    """The paired means of the blocks before and after the servers were restarted in the reverse
+    order (block `half` on), and half their difference: the placement effect that the mean over
+    both halves cancels when it is the same size either way round."""
+    first = float(np.mean(np.subtract(other[:half], reference[:half])))
+    second = float(np.mean(np.subtract(other[half:], reference[half:])))
+    return {"first_half_mean_us": first, "second_half_mean_us": second, "spawn_order_effect_us": (first - second) / 2}
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--serve", help=argparse.SUPPRESS)
@@ -253,10 +262,7 @@ def main() -> int:
                 ref_blocks, blocks_of = summary[reference]["block_medians_us"], summary[name]["block_medians_us"]
                 comparison = paired(ref_blocks, blocks_of, seed=n)
                 if not a.no_swap and half >= 1:
-                    first = float(np.mean(np.subtract(blocks_of[:half], ref_blocks[:half])))
-                    second = float(np.mean(np.subtract(blocks_of[half:], ref_blocks[half:])))
-                    comparison["first_half_mean_us"], comparison["second_half_mean_us"] = first, second
-                    comparison["spawn_order_effect_us"] = (first - second) / 2
+                    comparison.update(spawn_order_effect(ref_blocks, blocks_of, half))
                 summary[name]["vs_" + reference] = comparison
             report["contexts"][str(n)] = {"summary": summary, "blocks": blocks, "spawn_order_by_block": spawned}
             for name in names:
