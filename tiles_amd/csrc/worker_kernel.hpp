@@ -139,7 +139,7 @@ constexpr int hidden_slots()
     return (VPL * 64 * Num<BF16>::kPerVec + kThreads - 1) / kThreads;
 }
 
-// bf16 elements of the attention's V^T block: head_dim rows of (block positions + 8).  It
+// bf16 elements of the attention's staged V block: one row of (head_dim + 8) per position.  It
 // shares LDS with the input vector.  A block holds the most positions (a multiple of 32, at most
 // 160) whose rows fit.
 constexpr int kVtElements = kLdsHidden * 3;
@@ -147,11 +147,11 @@ constexpr int kMaxThreadsPadded = kThreads;  // floats of a split chunk's own pa
 constexpr int vt_block_positions(int dh)
 {
     int positions = 160;
-    while (positions > 32 && dh * (positions + 8) > kVtElements)
+    while (positions > 32 && positions * (dh + 8) > kVtElements)
         positions -= 32;
     return positions;
 }
-static_assert(kMaxHeadDim * (vt_block_positions(kMaxHeadDim) + 8) <= kVtElements, "V^T blocks");
+static_assert(vt_block_positions(kMaxHeadDim) * (kMaxHeadDim + 8) <= kVtElements, "V blocks");
 
 struct Shared {
     union {
@@ -162,7 +162,7 @@ struct Shared {
             // lane, lanes 32 bytes apart) put 16 lanes on each LDS bank.
             uint16_t vbits[kLdsHidden];
         };
-        alignas(16) uint16_t vt[kVtElements];  // attention: V^T of a block of positions (no input vector)
+        alignas(16) uint16_t vt[kVtElements];  // attention: V rows of a block of positions (no input vector)
     };
     alignas(16) float region[kLdsRegionFloats];  // scores/probabilities, reductions, FFN gate/up/product
     float xsave[kLdsHidden];      // the layer input this worker last read, before the norm
@@ -959,11 +959,11 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     constexpr bool kMfma = BF16 && dh % 32 == 0;
     constexpr int KS = dh / 32;                      // 32-dim slices of a head (matrix path)
     constexpr int kTile = 16;                        // positions per matrix tile
-    constexpr int PB = vt_block_positions(dh);       // positions per V^T block in LDS
-    constexpr int kVtStride = PB + 8;                // bf16 elements per V^T row
+    constexpr int PB = vt_block_positions(dh);       // positions per staged V block in LDS
     constexpr int kBlockTiles = PB / kTile;
     constexpr int TW = (kBlockTiles + kWaves - 1) / kWaves;  // tiles per wave in a block
-    static_assert(!kMfma || dh * kVtStride + (dh / 8) * 16 <= kVtElements, "V^T block exceeds its LDS area");
+    constexpr int kVRow = dh + 8;  // bf16 per staged V row: 4 rows of 16-byte-apart chunks hit distinct banks
+    static_assert(!kMfma || PB * kVRow <= kVtElements, "V block exceeds its LDS area");
     static_assert(!kMfma || dh / 16 <= kWaves, "a wave per 16 output dims");
     constexpr int kRowsPerWave = 64 / LRK;
     constexpr int kBlockRows = kWaves * kRowsPerWave;
@@ -1130,30 +1130,38 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             v[q] = pack_bf16(src[2 * q], src[2 * q + 1]);
         return v;
     };
-    // Matrix path: V^T of the PB positions from tile first_tile of the chunk, one column per
-    // position; the wave writes its tile wave + 8 j of the block (vb: that tile's rows).
+    // Matrix path: V rows of the PB positions from tile first_tile of the chunk; the wave writes
+    // its tile wave + 8 j of the block (vb: that tile's rows).
     uint16_t* vt = sh.vt;
-    // Row `dim` of V^T starts at vt_row(dim): every 8 rows are skewed 16 elements further, so that
-    // the 16-bit stores of one instruction (dims 8 apart across its lane groups) fall in distinct
-    // LDS banks; rows stay 16-byte aligned for the operand reads.
-    auto vt_row = [](int dim) { return dim * kVtStride + (dim >> 3) * 16; };
-    auto write_vt = [&](int first_tile, int j, const u32x4* vb) {
+    // V is staged as it is stored, a row per position (`kVRow` apart), one 16-byte store per lane
+    // and 32 dims; P V's B operand (dim 16 n + tr at 8 positions) then comes from two transposing
+    // reads, ds_read_b64_tr_b16: within a 16-lane group, lane j names row 4 h + j / 4, dims
+    // 16 n + 4 (j % 4) .. + 3, and lane i receives element i % 4 of lanes 4 e + i / 4, e = 0..3,
+    // i.e. dim 16 n + i of the group's four rows.
+    auto write_v = [&](int first_tile, int j, const u32x4* vb) {
         const int tile = wave + j * kWaves;
-        const int column = tile * kTile + tr;
+        const int row = tile * kTile + tr;
         const bool current = begin + (first_tile + tile) * kTile + tr == position;
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
             const u32x4 now = pack8(sh.vcur + 32 * k + 8 * tk);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t pair = current ? now[q] : vb[k][q];
-                const int dim = 32 * k + 8 * tk + 2 * q;
-                vt[vt_row(dim) + column] = static_cast<uint16_t>(pair);
-                vt[vt_row(dim + 1) + column] = static_cast<uint16_t>(pair >> 16);
-            }
+            *reinterpret_cast<u32x4*>(vt + row * kVRow + 32 * k + 8 * tk) = current ? now : vb[k];
         }
     };
-
+    auto v_operand = [&](int q, int n) {
+        u32x4 out;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int row = 32 * q + 8 * tk + 4 * h + (tr >> 2);
+            typedef short v4s __attribute__((ext_vector_type(4)));
+            const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4s*)(vt + row * kVRow + 16 * n + 4 * (tr & 3)));
+            const uint2 pair = __builtin_bit_cast(uint2, r);
+            out[2 * h] = pair.x;
+            out[2 * h + 1] = pair.y;
+        }
+        return out;
+    };
     if constexpr (kMfma) {
         // A: query head tr (zero past the group); the current K row stands in for the
         // position's own tile row.
@@ -1199,12 +1207,12 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 if ((tile0 + gi * kWaves) * kTile < span)
                     tile_scores(tile0 + gi * kWaves, kb[gi]);
         }
-        // V^T columns past the chunk's last 32-position step are never read: P V stops there.
+        // V rows past the chunk's last 32-position step are never read: P V stops there.
         const int live0 = min(kBlockTiles, 2 * ((min(span, PB) + 31) / 32));
 #pragma unroll
         for (int j = 0; j < TW; ++j)
             if (wave + j * kWaves < live0)
-                write_vt(0, j, vfirst[j]);
+                write_v(0, j, vfirst[j]);
     } else {
         // Scores of rows [begin, end).  Every lane holds its slice of all MG query heads (heads
         // past the group compute values that are never stored) and of the current K row.
@@ -1273,7 +1281,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     float* merged_sum = sh.small + 3 * kMaxGroup;
     const bool fused = chunks == 1;
     // Matrix path: the rounded probabilities also go to LDS as the bf16 operands of P V, each
-    // head's positions contiguous and zero up to whole V^T blocks, so that one 16-byte read is a
+    // head's positions contiguous and zero up to whole V blocks, so that one 16-byte read is a
     // lane's 8 positions.  Chunks too long for the work region pack them from the FP32 values.
     const int span_pad = (span + PB - 1) / PB * PB;
     const int p_offset = (group * span + 7) / 8 * 8;  // floats: after the scores, 16-byte aligned
@@ -1283,7 +1291,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     uint16_t* pbits = reinterpret_cast<uint16_t*>(scores + p_offset);  // [group][span_pad]
     auto put_p = [&](int g, int i, float v) { pbits[g * span_pad + i] = static_cast<uint16_t>(__float_as_uint(v) >> 16); };
     if (wave < group && packed_p && span_pad <= 3 * 64) {
-        // At most one V^T block: the wave's scores stay in registers (3 per lane), read once.
+        // At most one V block: the wave's scores stay in registers (3 per lane), read once.
         const float* row = scores + wave * span;
         float v[3], e[3];
 #pragma unroll
@@ -1440,7 +1448,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     if constexpr (kMfma) {
         // Wave n < dh / 16 accumulates output dims 16 n .. 16 n + 15 of every head over the
         // chunk's positions, PB at a time: A = probabilities of head tr at 8 consecutive
-        // positions (zero past the group or the span), B = the same positions of V^T row 16 n + tr.
+        // positions (zero past the group or the span), B = dim 16 n + tr of the same positions.
         f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
         const int n = wave;
         // The next block's V tiles load while this block's P V runs.
@@ -1448,11 +1456,11 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         for (int first = 0; first < span; first += PB) {
             const int steps = (min(span - first, PB) + 31) / 32;  // 32-position steps of this block
             if (first > 0) {
-                block_sync(sh);  // the previous block's V^T has been read
+                block_sync(sh);  // the previous block's V rows have been read
 #pragma unroll
                 for (int j = 0; j < TW; ++j)
                     if (wave + j * kWaves < min(kBlockTiles, 2 * steps))
-                        write_vt(first / kTile, j, vnext[j]);
+                        write_v(first / kTile, j, vnext[j]);
                 block_sync(sh);
             }
             if (first + PB < span)  // block-uniform
@@ -1466,7 +1474,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                     if (q >= steps)
                         break;
                     const int t0 = first + 32 * q + 8 * tk;
-                    const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + vt_row(16 * n + tr) + 32 * q + 8 * tk);
+                    const u32x4 vb = v_operand(q, n);
                     const u32x4 p = *reinterpret_cast<const u32x4*>(pbits + (tr < group ? tr : 0) * span_pad + t0);
                     const u32x4 pa = tr < group ? p : zero;
                     o = mfma_16x16x32_bf16(pa, vb, o);
@@ -1477,7 +1485,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                     if (q >= steps)
                         break;
                     const int t0 = first + 32 * q + 8 * tk;
-                    const u32x4 vb = *reinterpret_cast<const u32x4*>(vt + vt_row(16 * n + tr) + 32 * q + 8 * tk);
+                    const u32x4 vb = v_operand(q, n);
                     float p[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
