@@ -333,7 +333,8 @@ __global__ void __launch_bounds__(kRowThreads) silu_rows(const uint16_t* gate, c
 // (!kBRows: B is [K][N], Wdown as stored), all bf16 and row-major, A [M][K]; C rounded to bf16
 // from FP32 sums (ldc: C's row stride).  Tiles of 128 x 128 per block of 4 waves, each wave
 // 64 x 64 as 4 x 4 v_mfma_f32_16x16x32_bf16 tiles, K in steps of 32 through LDS (rows padded to
-// 40 elements: 16-byte operand reads of 16 rows 80 bytes apart fall on distinct bank groups), the
+// 40 elements: 16-byte operand reads of 16 rows 80 bytes apart fall on distinct bank groups; a
+// [K][N] B tile stays as loaded and its operands come from gfx950's transposing LDS reads), the
 // next step's tile loaded into registers while this one's MFMAs run.  K % 32 == 0 and N % 16 == 0
 // (the launcher checks); rows and columns past M and N are clamped on load and not stored.
 constexpr int kGemmTile = 128, kGemmK = 32, kGemmStride = kGemmK + 8;
@@ -342,7 +343,11 @@ template <bool kBRows>
 __global__ void __launch_bounds__(256) gemm_bf16(const uint16_t* a, const uint16_t* b, uint16_t* c, int m, int n, int k, int ldc)
 {
     __shared__ __attribute__((aligned(16))) uint16_t as[kGemmTile * kGemmStride];
-    __shared__ __attribute__((aligned(16))) uint16_t bs[kGemmTile * kGemmStride];  // [n][k] either way
+    // kBRows: B as [n][k] rows; !kBRows: B as loaded, [k][n] rows kBkStride apart, its operands
+    // read by transposing LDS reads.
+    __shared__ __attribute__((aligned(16))) uint16_t bs[kGemmTile * kGemmStride];
+    constexpr int kBkStride = kGemmTile + 16;  // 288-byte rows: four rows of a transposing read on distinct banks
+    static_assert(kGemmK * kBkStride <= kGemmTile * kGemmStride, "B tile exceeds its LDS area");
     const int t = threadIdx.x, lane = t & 63, wave = t / 64;
     const int m0 = blockIdx.y * kGemmTile, n0 = blockIdx.x * kGemmTile;
     const int wm = (wave / 2) * 64, wn = (wave % 2) * 64;
@@ -370,13 +375,9 @@ __global__ void __launch_bounds__(256) gemm_bf16(const uint16_t* a, const uint16
             db[0] = rb[0];
             db[1] = rb[1];
         } else {
-            // Column j of the 16 loaded becomes element k of LDS row (column - n0).
-            const int col = (t % 8) * 16;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const uint32_t word = rb[j / 8][(j % 8) / 2];
-                bs[(col + j) * kGemmStride + brow] = static_cast<uint16_t>((j & 1) ? word >> 16 : word);
-            }
+            u32x4* db = reinterpret_cast<u32x4*>(bs + brow * kBkStride + (t % 8) * 16);
+            db[0] = rb[0];
+            db[1] = rb[1];
         }
     };
     f32x4 acc[4][4];
@@ -397,7 +398,22 @@ __global__ void __launch_bounds__(256) gemm_bf16(const uint16_t* a, const uint16
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             fa[i] = *reinterpret_cast<const u32x4*>(as + (wm + i * 16 + r) * kGemmStride + q);
-            fb[i] = *reinterpret_cast<const u32x4*>(bs + (wn + i * 16 + r) * kGemmStride + q);
+            if constexpr (kBRows) {
+                fb[i] = *reinterpret_cast<const u32x4*>(bs + (wn + i * 16 + r) * kGemmStride + q);
+            } else {
+                // ds_read_b64_tr_b16: within a 16-lane group, lane j names row q + 4 h + j / 4,
+                // columns wn + 16 i + 4 (j % 4) .. + 3, and lane r receives column wn + 16 i + r
+                // of the group's four rows.
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    typedef short v4s __attribute__((ext_vector_type(4)));
+                    const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s*)(bs + (q + 4 * h + (r >> 2)) * kBkStride + wn + i * 16 + 4 * (r & 3)));
+                    const uint2 pair = __builtin_bit_cast(uint2, v);
+                    fb[i][2 * h] = pair.x;
+                    fb[i][2 * h + 1] = pair.y;
+                }
+            }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
