@@ -119,9 +119,10 @@ __global__ void __launch_bounds__(kRowThreads) rope_rows(const uint16_t* qkv, in
 // maximum M, FP32 S).  Pass 2 recomputes the scores, rounds P = exp(s - M) / S to bf16 in
 // registers and takes P V on the matrix cores with P as the A operand straight from the score
 // layout: a 32-key step's k-elements 8 g .. 8 g + 7 of lane group g are keys 4 g .. 4 g + 3 and
-// 16 + 4 g .. + 3 of the step (the sum over keys does not depend on their order), and V^T
-// supplies the same keys as two 8-byte reads.  The block stages each 64-key tile's K rows (and,
-// in pass 2, V^T) in LDS once for its four waves, while the next tile's rows load into registers.
+// 16 + 4 g .. + 3 of the step (the sum over keys does not depend on their order), and two
+// transposing LDS reads of the V rows supply the same keys.  The block stages each 64-key tile's
+// K rows (and, in pass 2, V rows) in LDS once for its four waves, as stored, while the next
+// tile's rows load into registers.
 // The output is rounded once.  Keys past the block's last position are clamped to it when loaded
 // and masked.
 constexpr int kAttnThreads = 256;
@@ -134,12 +135,12 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
 {
     constexpr int KS = DH / 32;                              // 32-dim steps of a score
     constexpr int NT = DH / 16;                              // 16-dim output tiles
-    constexpr int kVtStride = kTile + 8;                     // bf16 per V^T row: 144 bytes
+    constexpr int kVStride = DH + 8;                         // bf16 per staged V row
     constexpr int kKStride = DH + 8;                         // bf16 per staged K row
     constexpr int kVectors = DH / 8;                         // 16-byte vectors of a K or V row
     constexpr int kLoads = kTile * kVectors / kAttnThreads;  // vectors per thread per tile
     static_assert(kTile * kVectors % kAttnThreads == 0, "whole vectors per thread");
-    __shared__ __attribute__((aligned(16))) uint16_t vt[DH * kVtStride];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[kTile * kVStride];
     __shared__ __attribute__((aligned(16))) uint16_t ks[kTile * kKStride];
     const int h = blockIdx.y, group = nq / nkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x / 64;
@@ -177,16 +178,30 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
             *reinterpret_cast<u32x4*>(ks + t * kKStride + 8 * v) = r[i];
         }
     };
-    auto stage_vt = [&](const u32x4 (&r)[kLoads]) {
+    auto stage_v = [&](const u32x4 (&r)[kLoads]) {
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
             const int index = threadIdx.x + i * kAttnThreads, t = index / kVectors, v = index - t * kVectors;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                vt[(8 * v + 2 * q) * kVtStride + t] = static_cast<uint16_t>(r[i][q]);
-                vt[(8 * v + 2 * q + 1) * kVtStride + t] = static_cast<uint16_t>(r[i][q] >> 16);
-            }
+            *reinterpret_cast<u32x4*>(vs + t * kVStride + 8 * v) = r[i];
         }
+    };
+    // B operand of P V for dims 16 n .. + 15 over keys 4 g4 .. + 3 and 16 + 4 g4 .. + 3 of the
+    // 32-key step: two transposing reads (ds_read_b64_tr_b16) of the V rows as stored.  Within a
+    // 16-lane group lane j names key row 4 e + .. (e = j / 4) and dims 16 n + 4 (j % 4) .. + 3;
+    // lane `col` receives dim 16 n + col of the four rows.
+    auto v_operand = [&](int step, int n) {
+        u32x4 out;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            typedef short v4s __attribute__((ext_vector_type(4)));
+            const int row = 32 * step + 16 * h + 4 * g4 + (col >> 2);
+            const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4s*)(vs + row * kVStride + 16 * n + 4 * (col & 3)));
+            const uint2 pair = __builtin_bit_cast(uint2, v);
+            out[2 * h] = pair.x;
+            out[2 * h + 1] = pair.y;
+        }
+        return out;
     };
     // Scores of subtile j of the staged tile kt for every head: s[g][i] at key 64 kt + 16 j + 4 g4 + i.
     auto scores = [&](int kt, int j, float (&s)[kMaxGroup][4]) {
@@ -253,7 +268,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
             }
         }
 
-    // Pass 2: P = bf16(exp(s - M) / S) as A operands, P V against V^T from LDS.
+    // Pass 2: P = bf16(exp(s - M) / S) as A operands, P V against the staged V rows.
     f32x4 o[kMaxGroup][NT];
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g)
@@ -263,9 +278,9 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
     load_rows(key_cache, 0, kr);
     load_rows(value_cache, 0, vr);
     for (int kt = 0; kt < tiles; ++kt) {
-        __syncthreads();  // the previous tile's K and V^T reads are done
+        __syncthreads();  // the previous tile's K and V reads are done
         stage_k(kr);
-        stage_vt(vr);
+        stage_v(vr);
         load_rows(key_cache, kt + 1, kr);
         load_rows(value_cache, kt + 1, vr);
         __syncthreads();
@@ -276,11 +291,8 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
             scores(kt, 2 * step + 1, s1);
             u32x4 vb[NT];
 #pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                const uint16_t* row = vt + (16 * n + col) * kVtStride + 32 * step + 4 * g4;
-                const uint2 lo = *reinterpret_cast<const uint2*>(row), hi = *reinterpret_cast<const uint2*>(row + 16);
-                vb[n] = u32x4{lo.x, lo.y, hi.x, hi.y};
-            }
+            for (int n = 0; n < NT; ++n)
+                vb[n] = v_operand(step, n);
 #pragma unroll
             for (int g = 0; g < kMaxGroup; ++g) {
                 if (g >= group)
