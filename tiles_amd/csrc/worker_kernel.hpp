@@ -141,12 +141,12 @@ constexpr int hidden_slots()
 
 // bf16 elements of the attention's staged V block: one row of (head_dim + 8) per position.  It
 // shares LDS with the input vector.  A block holds the most positions (a multiple of 32, at most
-// 160) whose rows fit.
-constexpr int kVtElements = kLdsHidden * 3;
+// 192) whose rows fit: 192 for 64-dim heads.
+constexpr int kVtElements = 192 * (64 + 8) > kLdsHidden * 3 ? 192 * (64 + 8) : kLdsHidden * 3;
 constexpr int kMaxThreadsPadded = kThreads;  // floats of a split chunk's own partial in the work region
 constexpr int vt_block_positions(int dh)
 {
-    int positions = 160;
+    int positions = 192;
     while (positions > 32 && positions * (dh + 8) > kVtElements)
         positions -= 32;
     return positions;
