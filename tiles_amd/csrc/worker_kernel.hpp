@@ -1196,7 +1196,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         // Tiles past the preloaded ones (chunks longer than TW * kWaves tiles): kGroup per wave
         // in flight at once, one wait per group instead of one per tile (tiles past the chunk
         // read zeros without memory traffic).
-        constexpr int kGroup = 4;
+        constexpr int kGroup = KS <= 2 ? 7 : 4;  // wider heads do not fit seven tiles in registers
         for (int tile0 = wave + TW * kWaves; tile0 * kTile < span; tile0 += kGroup * kWaves) {
             u32x4 kb[kGroup][KS];
 #pragma unroll
