@@ -1320,12 +1320,15 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             stat_sum[wave] = sum;
         }
     } else if (wave < group) {
+        // Longer chunks: unrolled, so that several LDS reads are in flight.
         float* row = scores + wave * span;
         float m = -INFINITY;
+#pragma unroll 4
         for (int i = lane; i < span; i += 64)
             m = fmaxf(m, row[i]);
         m = lane_value(group_max(m, 64), 63);
         float sum = 0.0f;
+#pragma unroll 4
         for (int i = lane; i < span; i += 64) {
             const float e = expf(row[i] - m);
             if (fused)
@@ -1334,6 +1337,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         }
         sum = lane_value(group_sum<64>(sum), 63);
         if (fused) {
+#pragma unroll 4
             for (int i = lane; i < span; i += 64) {
                 const float v = N::round(row[i] / sum);
                 row[i] = v;
@@ -1430,6 +1434,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         if (wave < group) {
             const float m = merged_max[wave], total = merged_sum[wave];
             float* row = scores + wave * span;
+#pragma unroll 4
             for (int i = lane; i < (packed_p ? span_pad : span); i += 64) {
                 const float p = i < span ? N::round(expf(row[i] - m) / total) : 0.0f;
                 if (i < span)
