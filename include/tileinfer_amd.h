@@ -110,11 +110,22 @@ typedef struct {
     float* attention_partials;
     ti_candidate* selection;
     float* ffn_trace;
-    uint64_t* timeline; /* optional: 4 words per instruction (launch.cuh:25-28): device clock at start, first
-                           exchange read, inputs complete, end */
+    uint64_t* timeline; /* optional: timeline_fields words per encoded instruction (below) */
     uint64_t* exchange;
     uint32_t epoch;
+    int32_t timeline_fields; /* 0 or TI_TIMELINE_REFERENCE_FIELDS: the reference's record; TI_TIMELINE_FIELDS:
+                                this build's record; any other value is rejected */
 } ti_worker_buffers;
+
+/* Timeline records written by thread 0 of the worker that runs an instruction (barrier records
+ * are left as they are).  With timeline_fields 0 or TI_TIMELINE_REFERENCE_FIELDS, the record is
+ * the reference's (launch.cuh:25-28, kTimelineFields; its host allocates 3 words per instruction,
+ * diagnostic_context.cu:264): {shader cycle counter (s_memtime) at the start, the same at the end,
+ * the 100 MHz device clock (s_memrealtime) at the start in ns}.  With TI_TIMELINE_FIELDS it is this
+ * build's: the 100 MHz device clock at the start, when the instruction's first exchange read
+ * returned, when its inputs were complete, and at its end. */
+#define TI_TIMELINE_REFERENCE_FIELDS 3
+#define TI_TIMELINE_FIELDS 4
 
 typedef struct { ti_token_id immediate; const ti_token_id* ids; int32_t steps; } ti_token_input; /* launch.cuh:49-54 */
 
@@ -263,11 +274,11 @@ int ti_context_collect(ti_context* context, const ti_ticket* ticket, float* logi
 int ti_context_intermediate_sizes(const ti_context* context, size_t* scratch, size_t* ffn);
 int ti_context_collect_intermediates(ti_context* context, const ti_ticket* ticket, float* scratch, float* ffn);
 /* Timeline mode (diagnostic_context.cu:257-285, main.cpp --timeline-stack): while enabled, every
- * launch stamps each instruction of its last step with the 100 MHz device clock at start, when
- * its first exchange read returned, when its inputs were complete, and at its end (0 where an
- * instruction read no exchange).  ti_context_timeline copies 4 words per instruction (plan
- * instruction order) after waiting for the context's queued work; `count` receives the number
- * of instructions. */
+ * launch stamps each instruction of its last step with this build's record (TI_TIMELINE_FIELDS:
+ * the 100 MHz device clock at start, when its first exchange read returned, when its inputs were
+ * complete, and at its end; 0 where an instruction read no exchange).  ti_context_timeline copies
+ * TI_TIMELINE_FIELDS words per instruction (plan instruction order) after waiting for the
+ * context's queued work; `count` receives the number of instructions. */
 int ti_context_set_timeline(ti_context* context, int32_t enabled);
 /* No counterpart in the reference, which prefills one position per worker step and lists a
  * matrix prefill as an open question (docs/development.md:331).  With it on (the default), a

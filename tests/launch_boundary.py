@@ -52,6 +52,8 @@ class LaunchHost:
         self.timeout = torch.zeros(1, dtype=torch.int32, device=dev)
         self.epoch = 1
         self.position = 0
+        self.timeline = None  # optional device tensor of 64-bit words, timeline_fields per instruction
+        self.timeline_fields = 0
         self.stream = torch.cuda.current_stream().cuda_stream
 
     def buffers(self) -> R.WorkerBuffers:
@@ -61,6 +63,9 @@ class LaunchHost:
         b.selection = _ptr(self.candidates)
         b.exchange = _ptr(self.exchange)
         b.epoch = self.epoch
+        if self.timeline is not None:
+            b.timeline = _ptr(self.timeline)
+        b.timeline_fields = self.timeline_fields
         return b
 
     def _launch(self, steps: int, token: R.TokenInput, selection: R.Selection) -> None:

@@ -88,3 +88,35 @@ def test_two_contexts_share_one_model(package):
     assert a.wait(ta).generated == want_a[0]
     np.testing.assert_array_equal(a.collect(ta)["kv"], want_a[1])
     np.testing.assert_array_equal(b.collect(tb)["kv"], want_b[1])
+
+
+@pytest.mark.parametrize("fields", [0, R.TIMELINE_REFERENCE_FIELDS, R.TIMELINE_FIELDS])
+def test_timeline_records_stay_inside_a_buffer_of_their_size(package, fields):
+    """A host that allocates the reference's kTimelineFields (3) words per instruction
+    (diagnostic_context.cu:264) and leaves timeline_fields zero, or asks for 3 or for this build's
+    4, gets every task's record inside that buffer: guard words past its end are intact, barrier
+    records untouched, and each task record ordered in time (reference record: end cycle after
+    the start cycle, a start time in ns; this build's: start <= inputs complete <= end)."""
+    plan = K.read_plan(package)
+    info = R.load_plan(package).inspect()
+    count, tasks = info["instruction_count"], info["task_count"]
+    width = fields or R.TIMELINE_REFERENCE_FIELDS
+    guard_words, guard = 256, 0x5A5A5A5A5A5A5A5A
+    host = LaunchHost(R.DecoderModel(R.load_plan(package)), plan)
+    host.timeline = torch.full((width * count + guard_words,), guard, dtype=torch.int64, device="cuda")
+    host.timeline_fields = fields
+    host.feed(S.prompt(40, seed=9, vocab=512))
+    torch.cuda.synchronize()
+    words = host.timeline.cpu().numpy().view(np.uint64)
+    assert (words[width * count:] == guard).all()
+    records = words[: width * count].reshape(count, width)
+    written = ~(records == guard).all(axis=1)
+    assert int(written.sum()) == tasks
+    r = records[written].astype(np.int64)
+    if width == R.TIMELINE_REFERENCE_FIELDS:
+        assert (r[:, 1] > r[:, 0]).all() and (r[:, 2] > 0).all()
+        # all workers share the ns clock: the step's records span well under a second
+        assert r[:, 2].max() - r[:, 2].min() < 1_000_000_000
+    else:
+        ready = r[:, 2] > 0
+        assert (r[:, 3] >= r[:, 0]).all() and (r[ready, 2] >= r[ready, 0]).all() and (r[ready, 3] >= r[ready, 2]).all()

@@ -205,3 +205,16 @@ def test_matrix_prefill_drift_matches_the_oracles(tmp_path):
     print(f"mean RMS: matrix {rows[:, 1].mean():.5f}, oracle {rows[:, 3].mean():.5f}", flush=True)
     assert rows[:, 1].mean() <= 1.25 * rows[:, 3].mean()
     assert (rows[:, 0] <= 2.5 * np.maximum(rows[:, 2], 0.02)).all()
+
+
+def test_stack_outside_the_gemm_shapes_prefills_through_the_worker(tmp_path):
+    """A stack whose FFN width (1000) is no multiple of the prefill GEMM's K step (32): a prompt
+    longer than one launch must not reach the matrix prefill (whose GEMM would reject the shape
+    after layer 0's kernels were queued) but prefill through the worker, so the default context
+    and one with the matrix prefill switched off give bit-identical K/V, logits and tokens."""
+    spec, path, packed, ospec = build(tmp_path, 256, 1000, 4, 1, 2, 512, 320, seed=44)
+    prompt = np.random.default_rng(8).integers(0, 512, 100).tolist()
+    got = prefill_both(path, prompt, 8)
+    assert np.array_equal(got["matrix"][0].view(np.uint32), got["worker"][0].view(np.uint32))
+    assert np.array_equal(got["matrix"][1], got["worker"][1])
+    assert got["matrix"][2] == got["worker"][2]

@@ -123,6 +123,8 @@ MUTATIONS = [
     ("policy", lambda p: p["model"].update(numeric_policy="x"), "inconsistent numeric policy"),
     ("hidden", lambda p: p["model"].update(hidden_size=48), "unsupported decoder dimensions"),
     ("chunks", lambda p: p["model"].update(attention_chunks=2), "invalid attention chunking"),
+    ("kv_range", lambda p: p["model"].update(max_context=1 << 26),
+     "K/V cache of one layer exceeds the worker's 2 GiB buffer addressing"),
     ("layers", lambda p: p["model"].update(layers=121), "more layers than the bf16 worker's exchange tags allow"),
     ("descriptor", lambda p: p["model"]["tensors"][2].update(shape=[1, 1]), "invalid tensor descriptors"),
     ("fingerprint", lambda p: p["target"].update(kernel_fingerprint="sm86"), "does not match compiled worker"),
@@ -248,3 +250,29 @@ def test_static_entry_point_rejects_an_oversized_exchange_before_any_device_call
     code = R.library().ti_enqueue_worker_static(None, C.byref(view), C.byref(buffers), 0, R.TokenInput(-1, None, 1),
                                                 R.Selection(), None)
     assert code == 1 and "exceeds the static array" in R.library().ti_last_error_message().decode()
+
+
+def test_timeline_record_sizes_follow_the_header():
+    """The header's timeline record sizes (the reference's kTimelineFields = 3, launch.cuh:25-28,
+    and this build's 4) are the ones the Python binding uses, and a launch asking for any other
+    size is rejected before any device call."""
+    header = (ROOT / "include" / "tileinfer_amd.h").read_text()
+    assert re.search(r"#define TI_TIMELINE_REFERENCE_FIELDS 3\b", header)
+    assert re.search(r"#define TI_TIMELINE_FIELDS 4\b", header)
+    assert (R.TIMELINE_REFERENCE_FIELDS, R.TIMELINE_FIELDS) == (3, 4)
+    view = R.ProgramView()
+    s = view.shape
+    s.hidden_size, s.intermediate_size, s.query_heads, s.kv_heads, s.head_dim = 2048, 8192, 32, 8, 64
+    s.max_context, s.attention_chunks, s.attention_chunk_steps, s.attention_fused_steps, s.ffn_chunks = 321, 1, 1056, 384, 256
+    view.stack.layers, view.stack.vocab_size, view.stack.full_stack = 16, 128256, 1
+    view.stack.layer_weight_stride = 60_000_000
+    view.workers, view.selection_slots, view.weight_dtype = 256, 256, 1
+    view.instructions = view.streams = view.weights = 16
+    view.rotary_frequencies = 16
+    buffers = R.WorkerBuffers()
+    for field in ("input", "output", "scratch", "kv", "logits", "attention_partials", "selection", "exchange"):
+        setattr(buffers, field, 16)
+    buffers.epoch, buffers.timeline_fields = 1, 5
+    code = R.library().ti_enqueue_worker(None, C.byref(view), C.byref(buffers), 0, R.TokenInput(-1, None, 1),
+                                         R.Selection())
+    assert code == 1 and b"invalid timeline record size" in R.library().ti_last_error_message()

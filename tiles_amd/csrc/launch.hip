@@ -105,6 +105,11 @@ std::string check_shape(const ti_model_shape& s, int dtype)
         return "attention chunk count exceeds the compiled worker's merge capacity";
     if (static_cast<long>(s.max_context) * (s.attention_chunks > 0 ? s.attention_chunks : 1) >= (1L << 31))
         return "context too long for the worker's 32-bit chunk arithmetic";
+    // Attention addresses one layer's K (or V) table through a buffer resource with 32-bit
+    // offsets, and points rows it masks at offset 2^31, past the table, where the load returns 0.
+    if (static_cast<uint64_t>(s.max_context) * static_cast<uint64_t>(s.kv_heads) * static_cast<uint64_t>(s.head_dim) * elem >=
+        (1ull << 31))
+        return "K/V cache of one layer exceeds the worker's 2 GiB buffer addressing";
     if (s.intermediate_size % 2 != 0)
         return "odd intermediate size";
     return {};
@@ -119,6 +124,8 @@ std::string check_launch_shape(const ti_worker_program_view& p, const ti_worker_
         return "incomplete program view";
     if (!b.input || !b.output || !b.scratch || !b.kv || !b.logits || !b.attention_partials || !b.selection || !b.exchange)
         return "incomplete worker buffers";
+    if (b.timeline_fields != 0 && b.timeline_fields != TI_TIMELINE_REFERENCE_FIELDS && b.timeline_fields != TI_TIMELINE_FIELDS)
+        return "invalid timeline record size";
     if (p.workers <= 0 || p.workers > 4096)
         return "invalid worker count";
     if (position < 0 || position + steps > p.shape.max_context)

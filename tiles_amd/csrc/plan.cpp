@@ -489,7 +489,11 @@ void validate_program(const Json& document, LoadedPlan& out)
             const Json& lane = entry.at("workers")[static_cast<size_t>(worker)];
             require(lane.is_array(), "invalid worker task list");
             // The chunks of one K/V head exchange their softmax statistics and wait for each
-            // other, so a worker may run at most one chunk of a head in an attention wave.
+            // other, so a worker may run at most one chunk of a head in an attention wave, and
+            // with several chunks per head a worker runs its chunks in ascending K/V head order:
+            // a chunk then waits only for chunks of its own head, which every other worker
+            // reaches after chunks of lower heads alone, so the lowest unfinished head always
+            // completes and no two workers wait on each other in a cycle.
             std::vector<uint32_t> heads;
             for (const auto& item : lane.items()) {
                 const int id = index_in(item, count);
@@ -499,6 +503,8 @@ void validate_program(const Json& document, LoadedPlan& out)
                 if (t.record.opcode == TI_OP_ATTENTION_SCORES) {
                     require(std::find(heads.begin(), heads.end(), t.record.kv_head) == heads.end(),
                             "two attention chunks of one K/V head share a worker");
+                    require(out.shape.attention_chunks == 1 || heads.empty() || heads.back() < t.record.kv_head,
+                            "attention chunks of a worker out of K/V head order");
                     heads.push_back(t.record.kv_head);
                 }
                 seen[static_cast<size_t>(id)] = 1;

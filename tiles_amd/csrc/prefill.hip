@@ -452,10 +452,17 @@ __global__ void __launch_bounds__(256) gemm_bf16(const uint16_t* a, const uint16
 
 bool MatrixPrefill::supports(const ti_worker_program_view& p)
 {
-    const int dh = p.shape.head_dim;
-    return p.weight_dtype == TI_DTYPE_BFLOAT16 && p.stack.full_stack && (dh == 64 || dh == 128) &&
-           p.shape.kv_heads > 0 && p.shape.query_heads % p.shape.kv_heads == 0 &&
-           p.shape.query_heads / p.shape.kv_heads <= kMaxGroup;
+    const ti_model_shape& s = p.shape;
+    const int dh = s.head_dim;
+    if (p.weight_dtype != TI_DTYPE_BFLOAT16 || !p.stack.full_stack || (dh != 64 && dh != 128) || s.kv_heads <= 0 ||
+        s.query_heads % s.kv_heads != 0 || s.query_heads / s.kv_heads > kMaxGroup)
+        return false;
+    // Every GEMM of MatrixPrefill::layer, as (K, N): Q/K/V (d, heads x dh), Wo (query width, d),
+    // gate/up (d, f), down (f, d).  gemm() takes K a multiple of kGemmK and N a multiple of 16; the
+    // head widths are multiples of 64 already.  A stack outside these prefills through the worker.
+    auto gemm_shape = [](int k, int n) { return k >= kGemmK && k % kGemmK == 0 && n >= 16 && n % 16 == 0; };
+    const int d = s.hidden_size, f = s.intermediate_size, qw = s.query_heads * dh, kvw = s.kv_heads * dh;
+    return gemm_shape(d, qw) && gemm_shape(d, kvw) && gemm_shape(qw, d) && gemm_shape(d, f) && gemm_shape(f, d);
 }
 
 MatrixPrefill::MatrixPrefill(const ti_worker_program_view& program) : p_(program) {}

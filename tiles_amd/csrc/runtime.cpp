@@ -334,6 +334,7 @@ struct Context {
         b.selection = candidates.as<ti_candidate>();
         b.exchange = exchange.as<uint64_t>();
         b.timeline = timeline_enabled ? timeline.as<uint64_t>() : nullptr;
+        b.timeline_fields = TI_TIMELINE_FIELDS;
         return b;
     }
 
@@ -925,7 +926,7 @@ extern "C" int ti_context_set_timeline(ti_context* context, int32_t enabled)
     return guarded(TI_ERR_HIP, [&] {
         auto& c = *context->context;
         if (enabled && !c.timeline.ptr) {
-            c.timeline = tiles::DeviceBuffer(c.model->instruction_count * 4 * sizeof(uint64_t));
+            c.timeline = tiles::DeviceBuffer(c.model->instruction_count * TI_TIMELINE_FIELDS * sizeof(uint64_t));
             if (hipMemset(c.timeline.ptr, 0, c.timeline.bytes) != hipSuccess)
                 throw std::runtime_error("clear timeline");
         }
@@ -944,7 +945,7 @@ extern "C" int ti_context_timeline(ti_context* context, uint64_t* words, size_t 
             return;
         if (hipStreamSynchronize(c.stream) != hipSuccess)
             throw std::runtime_error("wait for timeline");
-        const size_t n = std::min(capacity, 4 * c.model->instruction_count);
+        const size_t n = std::min(capacity, TI_TIMELINE_FIELDS * c.model->instruction_count);
         if (hipMemcpy(words, c.timeline.ptr, n * sizeof(uint64_t), hipMemcpyDeviceToHost) != hipSuccess)
             throw std::runtime_error("copy timeline");
     });

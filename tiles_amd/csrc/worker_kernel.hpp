@@ -80,6 +80,7 @@ struct Launch {
     float* ffn_trace;
     ti_candidate* selection_out;
     uint64_t* timeline;
+    int timeline_fields;  // TI_TIMELINE_FIELDS, or TI_TIMELINE_REFERENCE_FIELDS (the reference's record)
     uint64_t* exchange;
     ExchangeLayout xl;
     uint32_t epoch;
@@ -181,6 +182,8 @@ struct Shared {
     int token;
     uint64_t mark_read;   // timeline: when the instruction's first exchange read returned
     uint64_t mark_ready;  // timeline: when its last exchange wait ended
+    uint64_t mark_start;         // timeline: 100 MHz device clock at the instruction's start
+    uint64_t mark_start_cycles;  // timeline (the reference's record): shader cycle counter at its start
 };
 
 // ---------------------------------------------------------------- block synchronization
@@ -2148,11 +2151,14 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
             const ti_task_record task = cached ? sh.stream[index - stream.begin] : load_record(L.instructions + index);
             if (task.opcode == TI_OP_BARRIER)
                 continue;  // waves synchronize through the exchange words
-            // Optional timeline: 100 MHz device clock (s_memrealtime) at the start of every
-            // instruction of the launch's last step, when its first exchange read returned,
-            // when its inputs were complete, and at its end (diagnostic_context.cu:257-285).
+            // Optional timeline of every instruction, the last step's left in the buffer
+            // (diagnostic_context.cu:257-285): this build's record, the 100 MHz device clock
+            // (s_memrealtime) at the start, when the first exchange read returned, when the inputs
+            // were complete and at the end; or the reference's (launch.cuh:25-28), the shader
+            // cycle counter (s_memtime) at the start and end and the device clock at the start in ns.
             if (L.timeline && tid() == 0) {
-                global(L.timeline)[4 * static_cast<size_t>(index)] = __builtin_amdgcn_s_memrealtime();
+                sh.mark_start_cycles = __builtin_amdgcn_s_memtime();
+                sh.mark_start = __builtin_amdgcn_s_memrealtime();
                 sh.mark_read = 0;
                 sh.mark_ready = 0;
             }
@@ -2175,9 +2181,20 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
             }
             block_sync(sh);
             if (L.timeline && tid() == 0) {
-                global(L.timeline)[4 * static_cast<size_t>(index) + 1] = sh.mark_read;
-                global(L.timeline)[4 * static_cast<size_t>(index) + 2] = sh.mark_ready;
-                global(L.timeline)[4 * static_cast<size_t>(index) + 3] = __builtin_amdgcn_s_memrealtime();
+                if (L.timeline_fields == TI_TIMELINE_FIELDS) {
+                    TILES_GLOBAL uint64_t* record = global(L.timeline) + TI_TIMELINE_FIELDS * static_cast<size_t>(index);
+                    record[0] = sh.mark_start;
+                    record[1] = sh.mark_read;
+                    record[2] = sh.mark_ready;
+                    record[3] = __builtin_amdgcn_s_memrealtime();
+                } else {
+                    const uint64_t end_cycles = __builtin_amdgcn_s_memtime();
+                    TILES_GLOBAL uint64_t* record =
+                        global(L.timeline) + TI_TIMELINE_REFERENCE_FIELDS * static_cast<size_t>(index);
+                    record[0] = sh.mark_start_cycles;
+                    record[1] = end_cycles;
+                    record[2] = sh.mark_start * 10u;  // 100 MHz ticks in ns
+                }
             }
         }
         if (sh.aborted) {
@@ -2216,6 +2233,7 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     L.ffn_trace = b.ffn_trace;
     L.selection_out = b.selection;
     L.timeline = b.timeline;
+    L.timeline_fields = b.timeline_fields == TI_TIMELINE_FIELDS ? TI_TIMELINE_FIELDS : TI_TIMELINE_REFERENCE_FIELDS;
     L.exchange = b.exchange;
     L.xl = exchange_layout(p.shape, p.stack.layers, p.selection_slots);
     L.epoch = b.epoch;

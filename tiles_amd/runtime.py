@@ -59,11 +59,17 @@ class ProgramView(C.Structure):
                 ("weight_dtype", C.c_int32)]
 
 
+# Words per instruction of a worker timeline record (include/tileinfer_amd.h): the reference's
+# {start cycles, end cycles, start ns} and this build's {start, first read, inputs complete, end}.
+TIMELINE_REFERENCE_FIELDS = 3
+TIMELINE_FIELDS = 4
+
+
 class WorkerBuffers(C.Structure):
     """ti_worker_buffers (WorkerBuffers, launch.cuh:31-45, plus the exchange area and its epoch)."""
     _fields_ = [(n, C.c_void_p) for n in ("input", "output", "scratch", "kv", "logits", "block_trace",
                                           "attention_scores", "attention_partials", "selection", "ffn_trace",
-                                          "timeline", "exchange")] + [("epoch", C.c_uint32)]
+                                          "timeline", "exchange")] + [("epoch", C.c_uint32), ("timeline_fields", C.c_int32)]
 
 
 class TokenInput(C.Structure):

@@ -253,9 +253,15 @@ def _layer_graph(spec: BlockSpec, workers: int, chunking: dict, dtype: str) -> l
         values += [add("attention_values", {"kv_head": kv_head, "chunk": c},
                        [{"workspace": "partials", "chunk": c, "heads": queries}], group_scores, chunk_work)
                    for c in range(chunks)]
+    # MI355X re-partition (this planner's rule, not plan_core's): when attention runs on at most
+    # half the workers, the output projection's rows are split over the others only, and
+    # schedule() keeps them off the attention workers.  Those finish attention last, and rows of
+    # theirs would be the projection wave's last to start.
+    attention_tasks = nkv * chunks
+    projection_workers = workers - attention_tasks if 2 * attention_tasks <= workers else workers
     attention = [add("output_projection", {"rows": [b, e]},
                      [rows("r", b, e)] + ([rows("attention", 0, d)] if b == 0 else []), values, (e - b) * d)
-                 for b, e in split(d, workers)]
+                 for b, e in split(d, projection_workers)]
     product = [add("ffn", {"rows": [b, e], "chunk": c},
                    [rows("product", b, e), {"workspace": "ffn_partials", "chunk": c}], attention, 3 * (e - b) * d)
                for c, (b, e) in enumerate(split(f, workers))]
@@ -305,7 +311,9 @@ def program(spec: BlockSpec, dtype: str, workers: int, chunking: dict, layers: i
 
 def schedule(tasks: list[dict], workers: int) -> list[dict]:
     """Earliest wave per task; within a wave, tasks in (-work, id) order go to the least
-    loaded worker, lowest index on ties (plan_core.py:524-549)."""
+    loaded worker, lowest index on ties (plan_core.py:524-549).  An output projection wave
+    that has no more tasks than the workers the preceding attention wave left idle goes to
+    those workers alone (_layer_graph sizes it so)."""
     buckets: list[list[int]] = []
     for task in tasks:
         wave = 0 if not task["predecessors"] else 1 + max(tasks[p]["wave"] for p in task["predecessors"])
@@ -317,7 +325,13 @@ def schedule(tasks: list[dict], workers: int) -> list[dict]:
     for wave, ids in enumerate(buckets):
         lanes: list[list[int]] = [[] for _ in range(workers)]
         loads = [0] * workers
-        heap = [(0, w) for w in range(workers)]
+        busy: set[int] = set()
+        if wave > 0 and tasks[ids[0]]["opcode"].startswith("output_projection"):
+            busy = {w for w, lane in enumerate(result[-1]["workers"]) if lane
+                    and tasks[lane[0]]["opcode"].startswith("attention")}
+            if len(ids) > workers - len(busy):
+                busy = set()
+        heap = [(0, w) for w in range(workers) if w not in busy]
         for task_id in sorted(ids, key=lambda i: (-tasks[i]["estimated_work"], i)):
             load, worker = heapq.heappop(heap)
             tasks[task_id]["worker"] = worker
