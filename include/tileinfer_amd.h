@@ -133,6 +133,7 @@ typedef struct { ti_token_id immediate; const ti_token_id* ids; int32_t steps; }
 enum { TI_STATUS_COUNT = 0, TI_STATUS_EOS = 1, TI_STATUS_ERROR = 2, TI_STATUS_WORDS = 3 };
 enum { TI_DEVICE_NO_ERROR = 0, TI_DEVICE_NON_FINITE = 1, TI_DEVICE_TOKEN_RANGE = 2, TI_DEVICE_SYNC_TIMEOUT = 3 };
 #define TI_MAX_LAUNCH_STEPS 64
+#define TI_DEFAULT_SPIN_LIMIT (1u << 20) /* polls of one worker wait before it declares the exchange stuck */
 
 typedef struct { ti_token_id* generated; int32_t* status; int32_t first; ti_token_id eos_id; } ti_selection; /* launch.cuh:79-85 */
 
@@ -148,6 +149,14 @@ typedef struct {
     int32_t bf16_registers, bf16_shared_bytes, bf16_active_blocks;
 } ti_target;
 
+/* No counterpart in the reference, whose grid barrier has no time limit.  Polls one wait of the
+ * worker makes before it declares the exchange stuck (default TI_DEFAULT_SPIN_LIMIT), process-wide,
+ * for launches enqueued after the call.  A stuck wait sets the exchange's control word; every wait
+ * of every worker then gives up, every worker returns, a generating launch stores
+ * TI_DEVICE_SYNC_TIMEOUT in its status, and the runtime fails the request with "worker
+ * synchronization timed out" and requires a reset.  Tests of that path set 0: the first wait that
+ * has to poll again gives up. */
+void ti_set_worker_spin_limit(uint32_t polls);
 const char* ti_error_string(int code);
 const char* ti_last_error_message(void);
 const char* ti_abi(void);          /* "tileinfer-decoder-v10" (plan.hpp:16) */

@@ -120,3 +120,38 @@ def test_timeline_records_stay_inside_a_buffer_of_their_size(package, fields):
     else:
         ready = r[:, 2] > 0
         assert (r[:, 3] >= r[:, 0]).all() and (r[ready, 2] >= r[ready, 0]).all() and (r[ready, 3] >= r[ready, 2]).all()
+
+
+def test_stuck_waits_end_the_launch_and_reset_recovers(package):
+    """The timeout path that replaces the reference's grid barrier (worker_kernel.cu:107,192, which
+    has none): with the spin limit at 0 (ti_set_worker_spin_limit), the first wait of a launch
+    that has to poll again declares the exchange stuck, every wait of every worker then gives up
+    and every block returns (the call ends), a generating launch stores TI_DEVICE_SYNC_TIMEOUT in
+    its status, and the runtime fails the request with "worker synchronization timed out", then
+    requires a reset; after the reset the context decodes exactly as a fresh one."""
+    plan = K.read_plan(package)
+    model = R.DecoderModel(R.load_plan(package))
+    lib = R.library()
+    prompt = S.prompt(30, seed=12, vocab=512)
+    fresh = model.create_context()
+    fresh.wait(fresh.enqueue_prefill(prompt))
+    want = fresh.wait(fresh.enqueue_generate(70)).generated
+
+    host = LaunchHost(model, plan)
+    host.feed(prompt)
+    ctx = model.create_context()
+    ctx.wait(ctx.enqueue_prefill(prompt))
+    lib.ti_set_worker_spin_limit(0)
+    try:
+        host.generate(70)
+        assert int(host.status[2].item()) == 3  # TI_DEVICE_SYNC_TIMEOUT
+        assert int(host.exchange[0].item()) != 0  # the control word a stuck wait sets
+        with pytest.raises(RuntimeError, match="worker synchronization timed out"):
+            ctx.wait(ctx.enqueue_generate(70))
+    finally:
+        lib.ti_set_worker_spin_limit(R.DEFAULT_SPIN_LIMIT)
+    with pytest.raises(RuntimeError, match="reset required"):
+        ctx.wait(ctx.enqueue_decode(5))
+    ctx.wait(ctx.enqueue_reset())
+    ctx.wait(ctx.enqueue_prefill(prompt))
+    assert ctx.wait(ctx.enqueue_generate(70)).generated == want

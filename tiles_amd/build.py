@@ -17,6 +17,10 @@ ROOT = PACKAGE.parent
 CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libtileinfer_amd.so"
+# The stress build: the same library with the worker compiled with TILES_DELAY_INJECTION (random
+# sleeps before every exchange publish and poll), for tests/test_gpu_delay_injection.py.
+DELAY_LIBRARY = PACKAGE / "libtileinfer_amd_delay.so"
+WORKER_SOURCES = ("worker_bf16.hip", "worker_f32.hip")
 CLI = PACKAGE / "tile_runtime"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -34,25 +38,33 @@ def _run(command: list[str]) -> None:
         raise RuntimeError(f"build step failed: {' '.join(command)}")
 
 
-def _object(source: str) -> Path:
-    out = BUILD / (source.replace(".", "_") + ".o")
+def _object(source: str, delay: bool = False) -> Path:
+    out = BUILD / (source.replace(".", "_") + ("_delay" if delay else "") + ".o")
     language = ["-x", "hip"] if source.endswith(".cpp") else []
-    _run([HIPCC, *FLAGS, *language, "-c", str(CSRC / source), "-o", str(out)])
+    defines = ["-DTILES_DELAY_INJECTION=1"] if delay else []
+    _run([HIPCC, *FLAGS, *defines, *language, "-c", str(CSRC / source), "-o", str(out)])
     return out
+
+
+def _link(library: Path, objects: list[Path]) -> None:
+    temporary = library.with_suffix(".so.tmp")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(temporary), *map(str, objects)])
+    os.replace(temporary, library)
 
 
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as pool:
-        objects = list(pool.map(_object, SOURCES))
-    temporary = LIBRARY.with_suffix(".so.tmp")
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(temporary), *map(str, objects)])
-    os.replace(temporary, LIBRARY)
+    jobs = [(source, False) for source in SOURCES] + [(source, True) for source in WORKER_SOURCES]
+    with ThreadPoolExecutor(max_workers=8) as pool:
+        built = list(pool.map(lambda job: _object(*job), jobs))
+    objects, delayed = built[: len(SOURCES)], dict(zip(WORKER_SOURCES, built[len(SOURCES):]))
+    _link(LIBRARY, objects)
+    _link(DELAY_LIBRARY, [delayed.get(source, obj) for source, obj in zip(SOURCES, objects)])
     cli_object = _object("main.cpp")
     _run([HIPCC, "--offload-arch=gfx950", "-o", str(CLI), str(cli_object), f"-L{PACKAGE}", "-ltileinfer_amd",
           f"-Wl,-rpath,$ORIGIN"])
     if verbose:
-        print(f"built {LIBRARY} and {CLI}")
+        print(f"built {LIBRARY}, {DELAY_LIBRARY} and {CLI}")
     return LIBRARY
 
 

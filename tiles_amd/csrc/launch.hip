@@ -3,6 +3,7 @@
 // snapshot zeroing and widening, snapshot.cu:8-62; the streaming-read roofline probe,
 // bandwidth_probe.cu:509-549).
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -142,6 +143,15 @@ std::string check_launch_shape(const ti_worker_program_view& p, const ti_worker_
     return {};
 }
 } // namespace tiles
+
+namespace tiles {
+namespace {
+std::atomic<uint32_t> g_spin_limit{kSpinLimit};
+}
+uint32_t worker_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
+} // namespace tiles
+
+extern "C" void ti_set_worker_spin_limit(uint32_t polls) { tiles::g_spin_limit.store(polls, std::memory_order_relaxed); }
 
 extern "C" const char* ti_error_string(int code)
 {

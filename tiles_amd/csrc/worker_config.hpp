@@ -31,7 +31,7 @@ inline constexpr int kAttentionSharedBytes = 8448;
 // 3 parts x 4 heads x 1120 padded positions of bf16 = 10,944 floats.
 inline constexpr int kRegionFloats = 11008;
 inline constexpr uint64_t kBufferRange = 1ull << 31;   // bytes a weight buffer resource addresses
-inline constexpr uint32_t kSpinLimit = 1u << 20;    // polls before a wait is declared stuck
+inline constexpr uint32_t kSpinLimit = TI_DEFAULT_SPIN_LIMIT;  // polls before a wait is declared stuck
 inline constexpr const char* kAbi = "tileinfer-decoder-v10";
 inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-v4-b512";
 
@@ -213,6 +213,10 @@ int enqueue_lm_head_step(hipStream_t stream, const ti_worker_program_view& head,
                          const void* hidden, ti_token_id* token, hipEvent_t worker_start, hipEvent_t worker_end);
 std::vector<const void*> worker_functions_bf16();
 std::vector<const void*> worker_functions_f32();
+
+// Polls of one worker wait before it declares the exchange stuck, for launches enqueued from now
+// on (ti_set_worker_spin_limit; kSpinLimit unless set).
+uint32_t worker_spin_limit();
 
 // Thread-local message of the last failed call (ti_last_error_message).
 const char* last_message();

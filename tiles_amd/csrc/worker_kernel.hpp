@@ -58,6 +58,30 @@ __device__ inline unsigned tid()
 // so that branches on it stay scalar branches.
 __device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6); }
 
+// Stress build (compiled with TILES_DELAY_INJECTION, tiles_amd/libtileinfer_amd_delay.so): at the
+// start of every task and before every exchange publish, cache-row store and poll, the calling wave
+// sleeps a pseudo-random 0 to about 2.5 us (s_sleep 4 is about 108 ns), drawn from a hash of a fixed
+// seed, the worker, the wave, the call site and the device clock.  The decode must stay
+// bit-identical to the undelayed build: nothing in the exchange protocol may rest on timing.  (The
+// reference runs its cases under racecheck/synccheck and with random delays before tasks,
+// counter_probe.cu:14-15.)  In the product build the call compiles to nothing.
+__device__ inline void inject_delay(uint32_t site)
+{
+#if defined(TILES_DELAY_INJECTION)
+    uint32_t x = 0x2545F491u ^ (blockIdx.x * 0x9E3779B1u) ^ (static_cast<uint32_t>(wave_id()) * 0x85EBCA6Bu) ^
+                 (site * 0xC2B2AE35u) ^ static_cast<uint32_t>(__builtin_amdgcn_s_memrealtime());
+    x ^= x >> 16;
+    x *= 0x7FEB352Du;
+    x ^= x >> 15;
+    x *= 0x846CA68Bu;
+    x ^= x >> 16;
+    for (uint32_t i = __builtin_amdgcn_readfirstlane(x) % 24u; i > 0; --i)
+        __builtin_amdgcn_s_sleep(4);
+#else
+    (void)site;
+#endif
+}
+
 // ---------------------------------------------------------------- launch record
 
 template <bool BF16>
@@ -81,6 +105,7 @@ struct Launch {
     ti_candidate* selection_out;
     uint64_t* timeline;
     int timeline_fields;  // TI_TIMELINE_FIELDS, or TI_TIMELINE_REFERENCE_FIELDS (the reference's record)
+    uint32_t spin_limit;  // polls of one wait before it declares the exchange stuck
     uint64_t* exchange;
     ExchangeLayout xl;
     uint32_t epoch;
@@ -179,6 +204,7 @@ struct Shared {
     uint32_t rsave_tag;  // epoch_of(step, layer, kPhaseR) of rsave's contents
     int flag;
     int aborted;
+    uint32_t spin_limit;  // polls of one wait before it declares the exchange stuck
     int token;
     uint64_t mark_read;   // timeline: when the instruction's first exchange read returned
     uint64_t mark_ready;  // timeline: when its last exchange wait ended
@@ -213,13 +239,14 @@ __device__ inline bool block_sync_and(Shared& sh, bool pred)
 
 // ---------------------------------------------------------------- exchange polling
 
-// Every 64th spin of a wait checks the shared abort word and the spin limit; a stuck wait
-// sets it so that every worker leaves its loops and the kernel drains.
+// A wait declares the exchange stuck past the launch's spin limit (ti_set_worker_spin_limit), and
+// every 64th spin checks the shared abort word; a stuck wait sets it, so that every worker leaves
+// its loops and the kernel drains.
 __device__ inline bool stuck(uint64_t* exchange, const ExchangeLayout& xl, uint32_t spins, Shared& sh)
 {
     if (sh.aborted)
         return true;
-    if ((spins & 63u) == 0 && (coherent_load64(exchange + xl.control) != 0 || spins > kSpinLimit)) {
+    if (spins > sh.spin_limit || ((spins & 63u) == 0 && coherent_load64(exchange + xl.control) != 0)) {
         sh.aborted = 1;
         coherent_store64(exchange + xl.control, 1);
         return true;
@@ -306,6 +333,7 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
                                           const ExchangeLayout& xl, Shared& sh, Sink sink, Overlap overlap = {})
 {
     constexpr int kBatch = ((kHalves ? kLdsHidden / 2 : kLdsHidden) + kThreads - 1) / kThreads;
+    inject_delay(__LINE__);
     const int words = kHalves ? count / 2 : count;
     (void)stride;
     const uint32_t want = kHalves ? exchange_tag(epoch) : epoch;
@@ -391,6 +419,7 @@ __device__ __forceinline__ void poll_words_one_wave(const uint64_t* src, int cou
     // Rounds of at most 16 words per lane (one round for a 2048-element bf16 vector): more would
     // spill the registers that hold the wave's weight loads.
     constexpr int kBatch = (kWords + 63) / 64 < 16 ? (kWords + 63) / 64 : 16;
+    inject_delay(__LINE__);
     const int lane = static_cast<int>(tid() & 63);
     const int words = kHalves ? count / 2 : count;
     const int stride_words = kHalves ? (stride > 1 ? stride / 2 : 1) : stride;
@@ -447,6 +476,7 @@ __device__ __forceinline__ void poll_words_one_wave(const uint64_t* src, int cou
 __device__ inline uint32_t poll_one(const uint64_t* src, uint32_t epoch, uint64_t* exchange, const ExchangeLayout& xl,
                                     Shared& sh)
 {
+    inject_delay(__LINE__);
     uint64_t w = coherent_load64(src);
     uint32_t spins = 0;
     while (static_cast<uint32_t>(w >> 32) != epoch && !sh.aborted) {
@@ -463,6 +493,7 @@ __device__ inline uint32_t poll_element(const uint64_t* region, int index, uint3
                                         const ExchangeLayout& xl, Shared& sh)
 {
     if constexpr (BF16) {
+        inject_delay(__LINE__);
         const uint32_t* src = reinterpret_cast<const uint32_t*>(region) + index;
         const uint32_t want = exchange_tag(epoch);
         uint32_t w = coherent_load32(src);
@@ -488,6 +519,7 @@ __device__ __forceinline__ void wait_witnesses(int n, Witness witness, uint32_t 
                                               const ExchangeLayout& xl, Shared& sh)
 {
     constexpr int kBatch = 8;
+    inject_delay(__LINE__);
     if (tid() < 64) {
         const int lane = tid();
         uint32_t spins = 0;
@@ -519,6 +551,7 @@ __device__ __forceinline__ void wait_witnesses(int n, Witness witness, uint32_t 
 template <bool BF16>
 __device__ inline void publish(uint64_t* dst, int index, float rounded, uint32_t epoch)
 {
+    inject_delay(__LINE__);
     coherent_store64(dst + index, (static_cast<uint64_t>(epoch) << 32) | Num<BF16>::payload(rounded));
 }
 
@@ -526,6 +559,7 @@ __device__ inline void publish(uint64_t* dst, int index, float rounded, uint32_t
 template <bool BF16>
 __device__ inline void publish_element(uint64_t* region, int index, float rounded, uint32_t epoch)
 {
+    inject_delay(__LINE__);
     if constexpr (BF16)
         coherent_store32(reinterpret_cast<uint32_t*>(region) + index, (exchange_tag(epoch) << 16) | Num<BF16>::payload(rounded));
     else
@@ -913,6 +947,7 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     void* cache = L.cache(layer, L.layout.value);
     if (wave_id() != 0)
         return;
+    inject_delay(__LINE__);
     for (int row = first_v + (static_cast<int>(tid()) & 63); row < end; row += 64) {
         const size_t index = static_cast<size_t>(position) * kvw + (row - d - kvw);
         if constexpr (BF16)
@@ -1075,6 +1110,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     // explicit wait says so to the compiler, which would otherwise make later waits for those loads
     // wait for these stores too.
     auto store_rotated = [&](int index, float value) {
+        inject_delay(__LINE__);
         if (index < group * dh) {
             if (L.block_trace)  // scratch intermediates only on traced launches
                 N::store(L.scratch, L.layout.q_rot + first_head * dh + index, value);
@@ -1369,6 +1405,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         // the head then reads all chunks' words, this chunk's own from LDS.  Every read of a round
         // issues before any is looked at; a round with a word missing is read again.
         const uint32_t stat_epoch = L.epoch_of(step, layer, kPhaseAttnStats);
+        inject_delay(__LINE__);
         if (tid() < 2 * group) {
             const int g = static_cast<int>(tid()) >> 1;
             const float value = (tid() & 1) ? stat_sum[g] : stat_max[g];
@@ -1380,6 +1417,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         const int stats_offset = packed_p ? (p_offset + (group * span_pad + 1) / 2 + 3) / 4 * 4 : p_offset;
         float* all_stats = scores + stats_offset;
         constexpr int kStatBatch = 2;
+        inject_delay(__LINE__);
         for (int base = 0; base < stat_words; base += kStatBatch * kThreads) {  // block-uniform
             uint64_t w[kStatBatch];
             auto word_index = [&](int u) { return min(base + u * kThreads + static_cast<int>(tid()), stat_words - 1); };
@@ -1598,6 +1636,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const uint32_t part_epoch = L.epoch_of(step, layer, kPhaseAttnPart);
     if (chunk == 0)
         wait_stores();  // the K row chunk 0 stored is in the cache before any output of the head is published
+    inject_delay(__LINE__);
     if (owner)
         coherent_store64(blocks + static_cast<size_t>(chunk) * part_words + mine,
                          (static_cast<uint64_t>(part_epoch) << 32) | __float_as_uint(out));
@@ -1610,6 +1649,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     if (owner)
         own[mine] = out;
     constexpr int kMergeBatch = 2;
+    inject_delay(__LINE__);
     for (int base = 0; base < words; base += kMergeBatch * kThreads) {  // block-uniform
         uint64_t w[kMergeBatch];
         auto slot = [&](int u) { return min(base + u * kThreads + static_cast<int>(tid()), words - 1); };
@@ -1882,6 +1922,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
                               __float_as_uint(acc[k * PV + 4 * h + 2]), __float_as_uint(acc[k * PV + 4 * h + 3])};
                 }
         block_sync(sh);
+        inject_delay(__LINE__);
         for (int o = tid(); o < KS * slice; o += kThreads) {
             const int kk = o / slice, c = o - kk * slice;
             float total = 0.0f;
@@ -1914,6 +1955,7 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
     const int slots = kThreads >> shift;
     const int slot = static_cast<int>(tid()) >> shift, lane = static_cast<int>(tid()) & (tpr - 1);
     const uint64_t* base = L.exchange + L.xl.ffn;
+    inject_delay(__LINE__);
     for (int first = 0; first < rows; first += slots) {
         const int row = begin + first + slot;
         const bool row_ok = first + slot < rows;
@@ -2032,6 +2074,7 @@ __device__ __forceinline__ void op_logits(const Launch<BF16>& L, const ti_task_r
         global(&L.selection_out[t.chunk].id)[0] = result.id;
         const uint32_t epoch = L.epoch_of(step, L.stack.layers, kPhaseCandidate);
         uint64_t* slot = L.exchange + L.xl.candidates + 2 * static_cast<size_t>(t.chunk);
+        inject_delay(__LINE__);
         coherent_store64(slot, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(result.value));
         coherent_store64(slot + 1, (static_cast<uint64_t>(epoch) << 32) | static_cast<uint32_t>(result.id));
     }
@@ -2047,6 +2090,7 @@ __device__ __forceinline__ ti_token_id greedy(const Launch<BF16>& L, int step, S
     const uint32_t epoch = step > 0 ? L.epoch_of(step - 1, L.stack.layers, kPhaseCandidate) : 0u;
     ti_candidate best{-INFINITY, 0x7fffffff};
     const uint64_t* candidates = L.exchange + L.xl.candidates;
+    inject_delay(__LINE__);
     for (int base = 0; base < slots; base += kThreads) {  // block-uniform
         const int slot = base + static_cast<int>(tid());
         const bool real = slot < slots;
@@ -2114,6 +2158,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
     if (tid() == 0) {
         record = launch;
         sh.aborted = 0;
+        sh.spin_limit = launch.spin_limit;
         sh.rope_position = -1;
         sh.flag = 0;
         sh.xsave_tag = 0;
@@ -2161,6 +2206,7 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
                 sh.mark_read = 0;
                 sh.mark_ready = 0;
             }
+            inject_delay(__LINE__);
             switch (task.opcode) {
             case TI_OP_QKV: op_qkv<BF16, VPL, LRK>(L, task, step, token, sh); break;
             case TI_OP_ATTENTION_SCORES: op_attention<BF16, LRK>(L, task, step, sh); break;
@@ -2233,6 +2279,7 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     L.selection_out = b.selection;
     L.timeline = b.timeline;
     L.timeline_fields = b.timeline_fields == TI_TIMELINE_FIELDS ? TI_TIMELINE_FIELDS : TI_TIMELINE_REFERENCE_FIELDS;
+    L.spin_limit = worker_spin_limit();
     L.exchange = b.exchange;
     L.xl = exchange_layout(p.shape, p.stack.layers, p.selection_slots);
     L.epoch = b.epoch;
@@ -2253,7 +2300,7 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     // device-wide resource to the process's queue, and while one process holds it every other
     // process's cooperative launch fails (hipErrorIllegalState): a host running the tile_runtime
     // CLI beside its own context could not decode.  Nothing in the worker needs that resource;
-    // its waits are the exchange polls, bounded by kSpinLimit, so blocks held off the device by
+    // its waits are the exchange polls, bounded by the spin limit, so blocks held off the device by
     // another process's kernels end the launch with TI_DEVICE_SYNC_TIMEOUT instead of a hang.
     const void* function = reinterpret_cast<const void*>(&decoder_worker<BF16, VPL, LRK>);
     static std::atomic<int> resident[kResidencyDevices] = {};

@@ -109,18 +109,31 @@ EXPORTS = ("ti_error_string", "ti_last_error_message", "ti_abi", "ti_fingerprint
            "ti_context_decode", "ti_context_generate", "ti_context_reset", "ti_context_ready", "ti_context_wait",
            "ti_context_diagnostic_sizes", "ti_context_collect", "ti_context_intermediate_sizes",
            "ti_context_collect_intermediates", "ti_ticket_free", "ti_context_set_timeline",
-           "ti_context_timeline", "ti_context_set_matrix_prefill", "ti_context_lm_head_step")
+           "ti_context_timeline", "ti_context_set_matrix_prefill", "ti_context_lm_head_step",
+           "ti_set_worker_spin_limit")
+DEFAULT_SPIN_LIMIT = 1 << 20  # TI_DEFAULT_SPIN_LIMIT
 
 _lib = None
+
+
+def library_path() -> Path:
+    """The in-tree library this process uses: libtileinfer_amd.so, or another build of it in the
+    package directory named by TILES_AMD_LIBRARY (the delay-injection stress build,
+    libtileinfer_amd_delay.so)."""
+    name = os.environ.get("TILES_AMD_LIBRARY", LIBRARY.name)
+    if "/" in name or not name.startswith("libtileinfer_amd") or not name.endswith(".so"):
+        raise RuntimeError(f"TILES_AMD_LIBRARY must name a build of the library in {LIBRARY.parent}")
+    return LIBRARY.parent / name
 
 
 def library() -> C.CDLL:
     """The loaded C-ABI library; raises if it was not built (no CPU fallback exists)."""
     global _lib
     if _lib is None:
-        if not LIBRARY.exists():
-            raise RuntimeError(f"{LIBRARY} is missing: run python -m tiles_amd.build (hipcc, gfx950)")
-        lib = C.CDLL(str(LIBRARY), mode=os.RTLD_NOW | C.RTLD_GLOBAL)
+        path = library_path()
+        if not path.exists():
+            raise RuntimeError(f"{path} is missing: run python -m tiles_amd.build (hipcc, gfx950)")
+        lib = C.CDLL(str(path), mode=os.RTLD_NOW | C.RTLD_GLOBAL)
         P = C.c_void_p
         lib.ti_error_string.restype = C.c_char_p
         lib.ti_last_error_message.restype = C.c_char_p
@@ -167,6 +180,8 @@ def library() -> C.CDLL:
         lib.ti_ticket_free.restype = None
         lib.ti_context_set_timeline.argtypes = [P, C.c_int32]
         lib.ti_context_set_matrix_prefill.argtypes = [P, C.c_int32]
+        lib.ti_set_worker_spin_limit.argtypes = [C.c_uint32]
+        lib.ti_set_worker_spin_limit.restype = None
         lib.ti_context_timeline.argtypes = [P, C.POINTER(C.c_uint64), C.c_size_t, C.POINTER(C.c_size_t)]
         _lib = lib
     return _lib

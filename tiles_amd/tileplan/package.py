@@ -153,6 +153,30 @@ def build_stack_package(spec: P.StackSpec, weights: dict, target: dict, out: Pat
     return report
 
 
+def build_block_package(block: P.BlockSpec, weights: dict, target: dict, out: Path, dtype: str = "bfloat16",
+                        chunk_steps: int | None = None, fused_steps: int | None = None) -> dict:
+    """Plan + pack a single-layer block package (decoder_block.py:50-70): weights.bin holds the
+    layer's weights (keys without a layer prefix, as decoder_m1's weights.npz) at their region
+    offsets, Wdown transposed."""
+    out = Path(out)
+    size = P.weight_size(dtype)
+    entries, total = P.regions(block, P.WEIGHTS, 64, size)
+    raw = bytearray(total)
+    for e in entries:
+        name = P.TENSOR_NAMES[e["tensor"]]
+        value = weights[name].T if name == "Wdown" else weights[name]
+        data = _pack(value, dtype)
+        raw[e["offset"]:e["offset"] + len(data)] = data
+    with new_package_dir(out) as directory:
+        (directory / "weights.bin").write_bytes(bytes(raw))
+        plan = P.block_plan(block, P.plan_target(target), dtype, hashlib.sha256(raw).hexdigest(), chunk_steps, fused_steps)
+        data = P.json_bytes(plan)
+        (directory / "plan.json").write_bytes(data)
+        report = summary(plan, hashlib.sha256(data).hexdigest())
+        (directory / "planning_report.json").write_bytes(P.json_bytes(report))
+    return report
+
+
 def read_plan(package: Path) -> dict:
     return json.loads((Path(package) / "plan.json").read_text())
 

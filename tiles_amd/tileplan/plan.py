@@ -445,5 +445,5 @@ def block_plan(block: BlockSpec, target: dict, dtype: str, weights_sha256: str,
     size = weight_size(dtype)
     storage = storage_section(block, dtype, chunking["attention_chunks"], workers, 1,
                               block.hidden_size * size, block.hidden_size * size)
-    return assemble(MODEL_KIND_BLOCK, target, model_section(block.as_dict(), block, dtype, chunking, workers),
+    return assemble(MODEL_KIND_BLOCK, target, model_section({**block.as_dict(), "layers": 1}, block, dtype, chunking, workers),
                     storage, scheduled_program(block, dtype, workers, chunking), weights_sha256)
