@@ -52,10 +52,14 @@ def sha256(path: Path) -> str:
     return hashlib.sha256(Path(path).read_bytes()).hexdigest()
 
 
-def prompt_for(context: int) -> list[int]:
+def prompt_for(context: int, vocab: int = 128256) -> list[int]:
+    """The benchmark's prompts: Llama's BOS alone at context 1, else `context` seeded uniform
+    tokens; for a model whose vocabulary lacks BOS, token 1 alone."""
     from . import synthetic as S
 
-    return [S.BOS] if context == 1 else S.prompt(context, seed=context)
+    if context == 1:
+        return [S.BOS if S.BOS < vocab else 1]
+    return S.prompt(context, seed=context, vocab=vocab)
 
 
 # ---------------------------------------------------------------- the resident server
@@ -71,10 +75,11 @@ def serve(package: str) -> int:
     print(json.dumps({"ready": True, "library": str(library), "library_sha256": sha256(library),
                       "plan_sha256": sha256(Path(package) / "plan.json")}), flush=True)
     prompts: dict[int, list[int]] = {}
+    vocab = json.loads((Path(package) / "plan.json").read_text())["model"].get("vocab_size", 128256)
     for line in sys.stdin:
         request = json.loads(line)
         n = int(request["context"])
-        prompt = prompts.setdefault(n, prompt_for(n))
+        prompt = prompts.setdefault(n, prompt_for(n, vocab))
         times = []
         for k in range(int(request.get("warmup", 1)) + int(request["rounds"])):
             ctx.wait(ctx.enqueue_reset())
