@@ -149,6 +149,13 @@ typedef struct {
     int32_t bf16_registers, bf16_shared_bytes, bf16_active_blocks;
 } ti_target;
 
+/* No counterpart in the reference.  Rewrites each layer's Wdown region of an uploaded model's
+ * device weights (`program->weights`, a device copy of weights.bin) in place, from the package's
+ * transposed [intermediate][hidden] to row-major [hidden][intermediate]: this worker's down
+ * projection streams Wdown rows (and the matrix prefill reads them so).  A host calls it exactly
+ * once after the upload, before any launch (a second call transposes back), and waits for it
+ * (the call synchronizes `stream`).  It allocates and frees one layer's Wdown of device memory. */
+int ti_relayout_weights(void* stream, const ti_worker_program_view* program);
 /* No counterpart in the reference, whose grid barrier has no time limit.  Polls one wait of the
  * worker makes before it declares the exchange stuck (default TI_DEFAULT_SPIN_LIMIT), process-wide,
  * for launches enqueued after the call.  A stuck wait sets the exchange's control word; every wait

@@ -244,7 +244,7 @@ def test_static_entry_point_rejects_an_oversized_exchange_before_any_device_call
     """ti_enqueue_worker_static checks the model's exchange area against its device array before
     it touches a device (this container has none)."""
     view = R.ProgramView()
-    view.shape.hidden_size, view.shape.ffn_chunks, view.shape.kv_heads = 4096, 4096, 8
+    view.shape.hidden_size, view.shape.intermediate_size, view.shape.kv_heads = 4096, 1 << 22, 8
     view.stack.layers, view.selection_slots, view.weight_dtype = 16, 256, 1
     buffers = R.WorkerBuffers()
     code = R.library().ti_enqueue_worker_static(None, C.byref(view), C.byref(buffers), 0, R.TokenInput(-1, None, 1),

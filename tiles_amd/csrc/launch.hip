@@ -113,6 +113,12 @@ std::string check_shape(const ti_model_shape& s, int dtype)
         return "K/V cache of one layer exceeds the worker's 2 GiB buffer addressing";
     if (s.intermediate_size % 2 != 0)
         return "odd intermediate size";
+    // The down projection reads Wdown rows (intermediate elements) as 16-byte vectors, at most
+    // kMaxDownVectorsPerThread per thread, and stages the product vector in the work region.
+    if (static_cast<long>(s.intermediate_size) * elem % 16 != 0)
+        return "intermediate size unsupported by the compiled worker's 16-byte Wdown row vectors";
+    if (static_cast<long>(s.intermediate_size) * elem / 16 > 4L * kThreads)
+        return "intermediate size exceeds the compiled worker's down projection";
     return {};
 }
 
@@ -152,6 +158,70 @@ uint32_t worker_spin_limit() { return g_spin_limit.load(std::memory_order_relaxe
 } // namespace tiles
 
 extern "C" void ti_set_worker_spin_limit(uint32_t polls) { tiles::g_spin_limit.store(polls, std::memory_order_relaxed); }
+
+namespace tiles {
+namespace {
+// dst[c][r] = src[r][c] for a rows x cols matrix, through 32 x 32 LDS tiles (256 threads).
+template <typename E>
+__global__ void transpose_matrix(const E* src, E* dst, int rows, int cols)
+{
+    __shared__ E tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int y = ty; y < 32; y += 8)
+        if (r0 + y < rows && c0 + tx < cols)
+            tile[y][tx] = src[static_cast<size_t>(r0 + y) * cols + c0 + tx];
+    __syncthreads();
+    for (int y = ty; y < 32; y += 8)
+        if (c0 + y < cols && r0 + tx < rows)
+            dst[static_cast<size_t>(c0 + y) * rows + r0 + tx] = tile[tx][y];
+}
+} // namespace
+
+int relayout_weights(hipStream_t stream, const ti_worker_program_view& p)
+{
+    if (!p.weights || p.stack.layers <= 0 || p.shape.hidden_size <= 0 || p.shape.intermediate_size <= 0)
+        return fail(TI_ERR_INVALID_ARGUMENT, "incomplete program view");
+    const bool bf16 = p.weight_dtype == TI_DTYPE_BFLOAT16;
+    const size_t elem = bf16 ? 2 : 4;
+    const int f = p.shape.intermediate_size, d = p.shape.hidden_size;
+    const size_t bytes = static_cast<size_t>(f) * d * elem;
+    void* temporary = nullptr;
+    hipError_t e = hipMalloc(&temporary, bytes);
+    if (e != hipSuccess)
+        return hip_fail(e, "Wdown relayout buffer");
+    const dim3 grid((d + 31) / 32, (f + 31) / 32);
+    for (int layer = 0; layer < p.stack.layers && e == hipSuccess; ++layer) {
+        char* region = static_cast<char*>(const_cast<void*>(p.weights)) +
+                       (static_cast<size_t>(p.stack.layer_weights_offset) + static_cast<size_t>(layer) * p.stack.layer_weight_stride +
+                        p.layout.Wdown) * elem;
+        e = hipMemcpyAsync(temporary, region, bytes, hipMemcpyDeviceToDevice, stream);
+        if (e != hipSuccess)
+            break;
+        if (bf16)
+            hipLaunchKernelGGL(transpose_matrix<uint16_t>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(temporary),
+                               reinterpret_cast<uint16_t*>(region), f, d);
+        else
+            hipLaunchKernelGGL(transpose_matrix<uint32_t>, grid, dim3(256), 0, stream, static_cast<const uint32_t*>(temporary),
+                               reinterpret_cast<uint32_t*>(region), f, d);
+        e = hipGetLastError();
+    }
+    const hipError_t done = hipStreamSynchronize(stream);
+    (void)hipFree(temporary);
+    if (e != hipSuccess)
+        return hip_fail(e, "Wdown relayout");
+    if (done != hipSuccess)
+        return hip_fail(done, "Wdown relayout");
+    return TI_OK;
+}
+} // namespace tiles
+
+extern "C" int ti_relayout_weights(void* stream, const ti_worker_program_view* program)
+{
+    if (!program)
+        return tiles::fail(TI_ERR_INVALID_ARGUMENT, "null program");
+    return tiles::relayout_weights(static_cast<hipStream_t>(stream), *program);
+}
 
 extern "C" const char* ti_error_string(int code)
 {

@@ -562,7 +562,8 @@ int MatrixPrefill::layer(hipStream_t stream, void* kv, int layer, int position, 
         !gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wup, f, v.up, f)))
         return code;
     hipLaunchKernelGGL(silu_rows, elementwise, dim3(kRowThreads), 0, stream, v.gate, v.up, ffn_count, v.gate);
-    if (!gemm_ok(gemm(stream, false, v.gate, rows, f, base + w.Wdown, d, v.projected, d)))
+    // Wdown row-major [hidden][intermediate] on the device (ti_relayout_weights).
+    if (!gemm_ok(gemm(stream, true, v.gate, rows, f, base + w.Wdown, d, v.projected, d)))
         return code;
     hipLaunchKernelGGL(add_rows, elementwise, dim3(kRowThreads), 0, stream, v.projected, v.r, hidden_count, v.x);
     const hipError_t e = hipGetLastError();

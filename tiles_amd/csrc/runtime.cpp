@@ -133,6 +133,9 @@ struct UploadedModel {
         view.numeric = plan.numeric;
         view.stack = plan.stack;
         view.weight_dtype = plan.weight_dtype;
+        // The worker's down projection and the matrix prefill read Wdown row-major.
+        if (relayout_weights(nullptr, view) != TI_OK)
+            throw std::runtime_error(last_message());
         exchange_words = ti_exchange_words(&plan.shape, plan.stack.layers, plan.selection_slots);
 
         std::vector<ti_task_record> head_records;

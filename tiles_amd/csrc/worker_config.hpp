@@ -39,7 +39,7 @@ inline constexpr const char* kFingerprint = "decoder-gfx950-wave64-exchange-v4-b
 inline constexpr int kPhaseQKV = 0;
 inline constexpr int kPhaseAttn = 1;
 inline constexpr int kPhaseR = 2;
-inline constexpr int kPhaseFfn = 3;
+inline constexpr int kPhaseFfn = 3;        // the FFN's products p (the down projection's input)
 inline constexpr int kPhaseY = 4;
 inline constexpr int kPhaseAttnPart = 5;   // attention chunk partials of a split context
 inline constexpr int kPhaseAttnStats = 6;  // attention chunk softmax statistics of a split context
@@ -69,15 +69,16 @@ __host__ __device__ inline void keep_better(ti_candidate& best, ti_candidate oth
 
 // Word offsets into the exchange area.  Each word: payload in bits 0-31 (one bf16 or fp32
 // element, or a candidate field), writer's epoch in bits 32-63.  In bf16, the vectors every
-// worker reads (hidden0/1, attn, r) hold two elements per word instead, each a 32-bit half with
-// a 16-bit epoch tag (worker_kernel.hpp, exchange_tag), and use the first half of their region.
+// worker reads (hidden0/1, attn, r, product) hold two elements per word instead, each a 32-bit
+// half with a 16-bit epoch tag (worker_kernel.hpp, exchange_tag), and use the first half of their
+// region.
 struct ExchangeLayout {
     size_t control;      // [0]: nonzero once a worker declared a wait stuck
     size_t hidden0, hidden1;  // layer outputs, alternating like the hidden buffers
     size_t qkv;          // per K/V head: its group's unrotated Q, then K, then V of the current position
     size_t attn;         // merged attention output
     size_t r;            // attention block output
-    size_t ffn;          // FP32 down partials, [ffn_chunks][hidden]
+    size_t product;      // the FFN's products p = SiLU(gate) * up, [intermediate] (tagged halves in bf16)
     size_t candidates;   // greedy candidates, 2 words per slot
     size_t parts;        // split attention, per K/V head and chunk: the group's FP32 partial P V, then (max, sum) per head
     size_t total;
@@ -105,8 +106,8 @@ __host__ __device__ inline ExchangeLayout exchange_layout(const ti_model_shape& 
     x.qkv = x.hidden1 + d;
     x.attn = x.qkv + d + 2 * kvw;
     x.r = x.attn + d;
-    x.ffn = x.r + d;
-    x.candidates = x.ffn + static_cast<size_t>(s.ffn_chunks) * d;
+    x.product = x.r + d;
+    x.candidates = x.product + static_cast<size_t>(s.intermediate_size);
     x.parts = x.candidates + 2 * static_cast<size_t>(slots > 0 ? slots : 1);
     x.total = x.parts + static_cast<size_t>(s.kv_heads) * s.attention_chunks * attention_part_words(s);
     (void)layers;
@@ -217,6 +218,11 @@ std::vector<const void*> worker_functions_f32();
 // Polls of one worker wait before it declares the exchange stuck, for launches enqueued from now
 // on (ti_set_worker_spin_limit; kSpinLimit unless set).
 uint32_t worker_spin_limit();
+
+// Rewrites each layer's Wdown region of the device weights in place from the package's
+// transposed [intermediate][hidden] to row-major [hidden][intermediate], the layout the worker's
+// down projection and the matrix prefill read (ti_relayout_weights).
+int relayout_weights(hipStream_t stream, const ti_worker_program_view& program);
 
 // Thread-local message of the last failed call (ti_last_error_message).
 const char* last_message();

@@ -106,6 +106,7 @@ struct Launch {
     uint64_t* timeline;
     int timeline_fields;  // TI_TIMELINE_FIELDS, or TI_TIMELINE_REFERENCE_FIELDS (the reference's record)
     uint32_t spin_limit;  // polls of one wait before it declares the exchange stuck
+    int down_vectors;     // 16-byte vectors of a Wdown row per thread in the down projection (1-4)
     uint64_t* exchange;
     ExchangeLayout xl;
     uint32_t epoch;
@@ -311,7 +312,7 @@ __device__ inline void wait_witness_words(const uint64_t* src, int count, int st
     }
 }
 
-// Reads `count` (at most kLdsHidden) exchange elements from `src` until each carries `epoch`
+// Reads `count` (at most kMaxCount) exchange elements from `src` until each carries `epoch`
 // and hands each payload to `sink(index, payload)`: one element per word, or with kHalves two
 // tagged bf16 elements per word (exchange_tag; `count` even).  Block-wide: every thread must
 // call it.
@@ -328,11 +329,11 @@ struct NoOverlap {
     __device__ void operator()() const {}
 };
 
-template <bool kHalves, typename Sink, typename Overlap = NoOverlap>
+template <bool kHalves, int kMaxCount = kLdsHidden, typename Sink, typename Overlap = NoOverlap>
 __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
                                           const ExchangeLayout& xl, Shared& sh, Sink sink, Overlap overlap = {})
 {
-    constexpr int kBatch = ((kHalves ? kLdsHidden / 2 : kLdsHidden) + kThreads - 1) / kThreads;
+    constexpr int kBatch = ((kHalves ? kMaxCount / 2 : kMaxCount) + kThreads - 1) / kThreads;
     inject_delay(__LINE__);
     const int words = kHalves ? count / 2 : count;
     (void)stride;
@@ -1737,27 +1738,25 @@ __device__ __forceinline__ void op_output_projection(const Launch<BF16>& L, cons
                        });
 }
 
-// One FFN product chunk (ops.cuh:739-813): z = RMSNorm(r); p = round(round(silu(round(gate)))
-// * round(up)) for rows [begin, end); then the chunk's FP32 down partial over every output,
-// published for the reduce wave.  Wdown is stored transposed, [intermediate, hidden].
+// One FFN product chunk (ops.cuh:739-757): z = RMSNorm(r); p = round(round(silu(round(gate))) *
+// round(up)) for rows [begin, end), published into the exchange's product vector (phase
+// kPhaseFfn) for the down projection (op_down).
 //
-// Rows stream whole: a lane group takes row i's gate and up slices and the same slice of
-// Wdown^T row i in one pass, so p_i multiplies the down row as soon as the group has it, and
-// every pass loads the same amount (3 x VPL 16-byte vectors per lane).  A lane owns the output
-// columns that match its input slice; waves then sum their partials through LDS.  D passes are
-// in flight per wave.  Waves 1-7 issue all of theirs before the task waits for r; wave 0 issues
-// one, polls r alone and issues the rest.  A wave's loads return in issue order, so polling from
-// waves with D passes queued saw r only when those passes had drained, 5-7 us after the chunk
-// began (the burst is 48 MB across the chip); wave 0 sees it about 2 us sooner (696 against 717
-// us per token at ctx 1, 812 against 834 at ctx 4096).
+// A lane group takes row i's gate and up slices in one pass (2 x VPL 16-byte vectors per lane); D
+// passes are in flight per wave.  Waves 1-7 issue all of theirs before the task waits for r; wave
+// 0 issues one, polls r alone and issues the rest.  A wave's loads return in issue order, so
+// polling from waves with D passes queued saw r only when those passes had drained, 5-7 us after
+// the chunk began (the burst is 48 MB across the chip); wave 0 sees it about 2 us sooner.  The
+// products wait in LDS and are published after the pass loop: a store inside it would make each
+// pass's wait a wait for every load in flight (loads and stores share vmcnt).
 template <bool BF16, int VPL>
 __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
-    constexpr int NV = 3 * VPL;                      // vectors per lane and row: gate, up, down
-    constexpr int D = VPL >= 8 ? 1 : (VPL >= 4 ? 2 : 4);
-    constexpr int kOut = VPL * PV;                   // outputs a lane owns
+    constexpr int NV = 2 * VPL;                      // vectors per lane and row: gate, up
+    constexpr int D = VPL >= 8 ? 1 : (VPL >= 4 ? 3 : 4);
+    constexpr int kOut = VPL * PV;                   // hidden elements per lane of a row
     const int d = hidden_size<BF16, VPL>(L);
     const int layer = static_cast<int>(t.layer);
     const int r0 = static_cast<int>(t.begin), r1 = static_cast<int>(t.end);
@@ -1788,9 +1787,8 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     const uint32_t row_bytes = static_cast<uint32_t>(d) * N::kBytes;
     const char* gate = L.layer_weight(layer, L.layout.Wgate) + g.col * 16;
     const char* up = L.layer_weight(layer, L.layout.Wup) + g.col * 16;
-    const char* down = L.layer_weight(layer, L.layout.Wdown) + g.col * 16;
     // Lanes past the chunk all read the first 16 bytes of its first row (one cached request
-    // per instruction); their product is zero.
+    // per instruction); their product is not kept.
     auto issue = [&](int pass, u32x4* w) {
         const int row = row_of(pass);
         const bool inside = row < r1;
@@ -1800,7 +1798,6 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
             const size_t o = at + (inside ? static_cast<size_t>(k) * g.lr * 16 : 0);
             w[k] = load_weights(gate + o);
             w[VPL + k] = load_weights(up + o);
-            w[2 * VPL + k] = load_weights(down + o);
         }
     };
     u32x4 w[D][NV];
@@ -1840,14 +1837,10 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     else
         rms_apply<BF16, kSlots>(sh.rsave, d, RegisterScale<kSlots>{scale}, L.numeric.rms_norm_eps, sh);
     const InputSlice<VPL> in(gemv_input<BF16>(sh), g.col, g.lr);
-    float acc[kOut];
-#pragma unroll
-    for (int n = 0; n < kOut; ++n)
-        acc[n] = 0.0f;
     const int lane = tid() & 63;
-    // One product row: gate and up dots, p = round(round(silu(round(gate))) * round(up)) (zero
-    // past the chunk), then the lane's slice of the down row times p.
-    auto product_row = [&](const u32x4* wg, const u32x4* wu, const u32x4* wd, int row) {
+    float* staged = sh.small;  // [row - r0]: the chunk's products (rms_apply's barrier freed it)
+    // One product row: gate and up dots, p = round(round(silu(round(gate))) * round(up)).
+    auto product_row = [&](const u32x4* wg, const u32x4* wu, int row) {
         float gate_dot = VPL > 1 ? group_sum<64>(in.template dot<BF16>(wg)) : group_sum(in.template dot<BF16>(wg), g.lr);
         float up_dot = VPL > 1 ? group_sum<64>(in.template dot<BF16>(wu)) : group_sum(in.template dot<BF16>(wu), g.lr);
         // The group's sums sit in its last lane (in every lane when the group has <= 16).
@@ -1860,140 +1853,141 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
         }
         const float gr = N::round(gate_dot);
         const float silu = N::round(gr / (1.0f + expf(-gr)));
-        const float p = row < r1 ? N::round(silu * N::round(up_dot)) : 0.0f;
-        // The product trace waits in LDS: a global store here would make the compiler wait for
-        // every weight load in flight at each later wait (loads and stores share vmcnt).
-        if (traced && row < r1 && g.col == g.lr - 1)
-            sh.small[row - r0] = p;
-#pragma unroll
-        for (int k = 0; k < VPL; ++k)
-#pragma unroll
-            for (int j = 0; j < PV; ++j)
-                acc[k * PV + j] += N::elem(wd[k], j) * p;
+        if (row < r1 && g.col == g.lr - 1)
+            staged[row - r0] = N::round(silu * N::round(up_dot));
     };
-    // Whole groups of D passes, without branches (a pass past the chunk weighs 0), and an
-    // explicit wait for each pass's loads, the later passes staying in flight: with a branch in
-    // the loop the compiler's count, merged at the loop header, waited for every load in flight.
-    // The last group issues nothing, so no load past the chunk delays the publication.
+    // Whole groups of D passes, without branches, and an explicit wait for each pass's loads, the
+    // later passes staying in flight: with a branch in the loop the compiler's count, merged at the
+    // loop header, waited for every load in flight.  The last group issues nothing.
     int base = 0;
     for (; g.first_row(r0, base + D) < r1; base += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
             const int pass = base + s;
             wait_vmem<(D - 1) * NV>();
-            product_row(&w[s][0], &w[s][VPL], &w[s][2 * VPL], row_of(pass));
+            product_row(&w[s][0], &w[s][VPL], row_of(pass));
             issue(pass + D, w[s]);
         }
     }
     unroll<D>([&](auto step) {
         constexpr int s = decltype(step)::value;
         wait_vmem<(D - 1 - s) * NV>();
-        product_row(&w[s][0], &w[s][VPL], &w[s][2 * VPL], row_of(base + s));
+        product_row(&w[s][0], &w[s][VPL], row_of(base + s));
     });
-    if (traced)  // the lanes that staged them, after the last weight load
-        for (int pass = 0; g.first_row(r0, pass) < r1; ++pass) {
-            const int row = row_of(pass);
-            if (row < r1 && g.col == g.lr - 1)
-                N::store(L.scratch, L.layout.product + row, sh.small[row - r0]);
-        }
-    // Lanes of one wave that hold the same columns (several rows per pass) add up first.
-    if (g.lr < 64)
-        residue_sum(acc, g.lr);
-    // Then the waves, KS slices of VPL at a time through LDS ([slice][wave][lr * PV] floats,
-    // as many slices as fit the work region), each round published with consecutive threads on
-    // consecutive words.
+    block_sync(sh);
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseFfn);
-    uint64_t* partials = L.exchange + L.xl.ffn + static_cast<size_t>(t.chunk) * d;
-    float* reduction = sh.region;
-    const int slice = g.lr * PV;
-    constexpr int KS = VPL >= 2 && kWaves * 64 * PV * 2 <= kLdsRegionFloats ? 2 : 1;
-    static_assert(kWaves * 64 * PV * KS <= kLdsRegionFloats, "FFN reduction rounds exceed the work region");
-#pragma unroll
-    for (int k0 = 0; k0 < VPL; k0 += KS) {
-        block_sync(sh);
-        if (g.sub == 0)
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk)
-#pragma unroll
-                for (int h = 0; h < PV / 4; ++h) {
-                    const int k = k0 + kk;
-                    reinterpret_cast<u32x4*>(reduction + (kk * kWaves + g.wave) * slice + g.col * PV)[h] =
-                        u32x4{__float_as_uint(acc[k * PV + 4 * h]), __float_as_uint(acc[k * PV + 4 * h + 1]),
-                              __float_as_uint(acc[k * PV + 4 * h + 2]), __float_as_uint(acc[k * PV + 4 * h + 3])};
-                }
-        block_sync(sh);
-        inject_delay(__LINE__);
-        for (int o = tid(); o < KS * slice; o += kThreads) {
-            const int kk = o / slice, c = o - kk * slice;
-            float total = 0.0f;
-            for (int wv = 0; wv < kWaves; ++wv)
-                total += reduction[(kk * kWaves + wv) * slice + c];
-            coherent_store64(partials + k0 * slice + o, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(total));
-        }
+    for (int row = r0 + static_cast<int>(tid()); row < r1; row += kThreads) {
+        const float p = staged[row - r0];
+        if (traced)
+            N::store(L.scratch, L.layout.product + row, p);
+        publish_element<BF16>(L.exchange + L.xl.product, row, p, epoch);
     }
 }
 
-// y rows: the chunks' FP32 down partials summed, rounded before the residual (ops.cuh:820-838).
-// TPR lanes (a power of two <= 64) sum one row; each lane issues up to kPerLane chunk reads
-// at once and re-reads them until all have arrived.
+// Largest intermediate size whose product vector the down projection stages in the work region
+// (bf16 bits, or FP32 values), and the 16-byte vectors of a Wdown row one thread holds at most.
 template <bool BF16>
-__device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
+constexpr int max_product()
+{
+    return BF16 ? 2 * kLdsRegionFloats : kLdsRegionFloats;
+}
+constexpr int kMaxDownVectorsPerThread = 4;
+
+// y rows [begin, end) (ops.cuh:762-838, reorganized for MI355X): the down projection of the FFN's
+// product vector over rows of Wdown, which the runtime re-lays out row-major [hidden][intermediate]
+// at upload (ti_relayout_weights), rounded before the residual: y = round(round(Wdown[row] . p) +
+// r[row]).  The reference has each FFN chunk write an FP32 partial of every output and this wave
+// add the chunks' partials in chunk order; the exact sum is the same and the contract rounds once,
+// after it, so only the FP32 summation order differs.  Split that way the reduce wave moved no
+// weights and waited a whole exchange round for partials (3.1 us per layer at Llama-3.2-1B widths);
+// here the task's Wdown rows (16 KB each, 128 KB per worker) are issued before it waits for p and
+// stream while the slowest FFN chunks finish and p crosses the exchange, and the FFN chunks stream
+// only gate and up.  Thread t holds vectors t, t + 512, ... (VPT of them) of each row, for G = 16 /
+// VPT rows at a time, and its slice of p from LDS; the waves' sums meet in LDS in wave order.
+template <bool BF16, int VPT>
+__device__ __forceinline__ void op_down(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
 {
     using N = Num<BF16>;
-    constexpr int kPerLane = 8;
-    const ti_model_shape& s = L.shape;
-    const int d = s.hidden_size;
+    constexpr int kLoads = 16;
+    constexpr int G = kLoads / VPT;
+    static_assert(G * kWaves <= kMaxTaskRows, "down projection wave sums exceed their LDS slots");
+    const int f = L.shape.intermediate_size;
+    const int d = hidden_size<BF16, 1>(L);
     const int layer = static_cast<int>(t.layer);
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
-    const int rows = end - begin;
-    const uint32_t in_epoch = L.epoch_of(step, layer, kPhaseFfn);
-    const uint64_t present = static_cast<uint64_t>(in_epoch) << 32;
-    int shift = 6;  // log2 of the lanes per row (shifts, not divisions by a run-time value)
-    while (shift > 0 && (rows << shift) > kThreads)
-        --shift;
-    const int tpr = 1 << shift;
-    const int slots = kThreads >> shift;
-    const int slot = static_cast<int>(tid()) >> shift, lane = static_cast<int>(tid()) & (tpr - 1);
-    const uint64_t* base = L.exchange + L.xl.ffn;
-    inject_delay(__LINE__);
-    for (int first = 0; first < rows; first += slots) {
-        const int row = begin + first + slot;
-        const bool row_ok = first + slot < rows;
-        float total = 0.0f;
-        for (int c0 = 0; c0 < s.ffn_chunks; c0 += kPerLane * tpr) {
-            // Every load issues before any result is used; slots past the row's chunks
-            // re-read a real word and are replaced by +0.0 afterwards.
-            uint64_t w[kPerLane];
-            auto read = [&]() {
-#pragma unroll
-                for (int k = 0; k < kPerLane; ++k) {
-                    const int c = c0 + lane + k * tpr;
-                    const bool real = row_ok && c < s.ffn_chunks;
-                    w[k] = coherent_load64(base + static_cast<size_t>(real ? c : 0) * d + (row_ok ? row : begin));
-                }
-                bool ok = true;
-#pragma unroll
-                for (int k = 0; k < kPerLane; ++k) {
-                    const int c = c0 + lane + k * tpr;
-                    if (!(row_ok && c < s.ffn_chunks))
-                        w[k] = present;
-                    ok &= static_cast<uint32_t>(w[k] >> 32) == in_epoch;
-                }
-                return ok;
-            };
-            // Missing chunks are re-read by their own lanes: waiting on witnesses first would add
-            // two round trips to the layer's critical path.
-            uint32_t spins = 0;
-            for (bool ok = read(); !ok && !sh.aborted; ok = read()) {
-                __builtin_amdgcn_s_sleep(2);
-                stuck(L.exchange, L.xl, ++spins, sh);
-            }
-#pragma unroll
-            for (int k = 0; k < kPerLane; ++k)
-                total += __uint_as_float(static_cast<uint32_t>(w[k]));  // absent chunks carry +0.0
+    const int vectors = f / N::kPerVec;  // 16-byte vectors of a Wdown row (the launcher checks f)
+    const size_t row_bytes = static_cast<size_t>(f) * N::kBytes;
+    const char* down = L.layer_weight(layer, L.layout.Wdown);
+    const int me = static_cast<int>(tid());
+    u32x4 w[kLoads];
+    // Rows past the task re-read its first row, vectors past a row its last vector (cached
+    // requests); neither is kept.  Every load issues: a conditional issue would make the compiler
+    // unsure how many are in flight.
+    auto issue = [&](int first) {
+        unroll<G>([&](auto gi) {
+            constexpr int gg = decltype(gi)::value;
+            const int row = first + gg < end ? first + gg : begin;
+            const char* base = down + static_cast<size_t>(row) * row_bytes;
+            unroll<VPT>([&](auto vi) {
+                constexpr int v = decltype(vi)::value;
+                const int j = v * kThreads + me;
+                w[gg * VPT + v] = load_weights(base + static_cast<size_t>(j < vectors ? j : vectors - 1) * 16);
+            });
+        });
+    };
+    issue(begin);
+    issue_fence();
+    uint16_t* p_bits = reinterpret_cast<uint16_t*>(sh.region);  // bf16: p as bits
+    float* p_values = sh.region;                                  // fp32: p as values
+    poll_words<BF16, max_product<BF16>()>(L.exchange + L.xl.product, f, 1, L.epoch_of(step, layer, kPhaseFfn), L.exchange,
+                                         L.xl, sh, [&](int i, uint32_t payload) {
+                                             if constexpr (BF16)
+                                                 p_bits[i] = static_cast<uint16_t>(payload);
+                                             else
+                                                 p_values[i] = __uint_as_float(payload);
+                                         });
+    block_sync(sh);
+    const u32x4* p_vectors = reinterpret_cast<const u32x4*>(sh.region);
+    float* wave_sums = sh.small;  // [row of the group][wave]
+    const int lane = me & 63, wave = wave_id();
+    for (int first = begin; first < end; first += G) {  // block-uniform
+        if (first != begin) {
+            issue(first);
+            wait_vmem<0>();
         }
-        total = group_sum(total, tpr);
-        if (row_ok && lane == tpr - 1) {
+        float acc[G];
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg)
+            acc[gg] = 0.0f;
+        unroll<VPT>([&](auto vi) {
+            constexpr int v = decltype(vi)::value;
+            const int j = v * kThreads + me;
+            const u32x4 pv = j < vectors ? p_vectors[j] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) {
+                const u32x4& wv = w[gg * VPT + v];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if constexpr (BF16)
+                        acc[gg] = dot2_bf16(wv[q], pv[q], acc[gg]);
+                    else
+                        acc[gg] = fmaf(__uint_as_float(wv[q]), __uint_as_float(pv[q]), acc[gg]);
+                }
+            }
+        });
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+            const float total = group_sum<64>(acc[gg]);
+            if (lane == 63)
+                wave_sums[gg * kWaves + wave] = total;
+        }
+        block_sync(sh);
+        if (me < G && first + me < end) {
+            const int row = first + me;
+            float total = 0.0f;
+#pragma unroll
+            for (int wv = 0; wv < kWaves; ++wv)
+                total += wave_sums[me * kWaves + wv];
             const float r = attention_output_element(L, layer, step, row, sh);
             const float projected = N::round(total);
             const float y = N::round(projected + r);
@@ -2005,6 +1999,19 @@ __device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_ta
                 global(L.ffn_trace)[static_cast<size_t>(layer) * d + row] = projected;
             publish_element<BF16>(L.exchange + L.xl.hidden((layer + 1) % 2), row, y, L.epoch_of(step, layer, kPhaseY));
         }
+        block_sync(sh);
+    }
+}
+
+// The down projection for the launch's intermediate size (vectors per thread fixed by the host).
+template <bool BF16>
+__device__ __forceinline__ void op_ffn_reduce(const Launch<BF16>& L, const ti_task_record& t, int step, Shared& sh)
+{
+    switch (L.down_vectors) {
+    case 1: op_down<BF16, 1>(L, t, step, sh); break;
+    case 2: op_down<BF16, 2>(L, t, step, sh); break;
+    case 3: op_down<BF16, 3>(L, t, step, sh); break;
+    default: op_down<BF16, 4>(L, t, step, sh); break;
     }
 }
 
@@ -2280,6 +2287,10 @@ int launch_typed(hipStream_t stream, const ti_worker_program_view& p, const ti_w
     L.timeline = b.timeline;
     L.timeline_fields = b.timeline_fields == TI_TIMELINE_FIELDS ? TI_TIMELINE_FIELDS : TI_TIMELINE_REFERENCE_FIELDS;
     L.spin_limit = worker_spin_limit();
+    {
+        const int row_vectors = p.shape.intermediate_size * (BF16 ? 2 : 4) / 16;
+        L.down_vectors = (row_vectors + kBlockThreads - 1) / kBlockThreads;
+    }
     L.exchange = b.exchange;
     L.xl = exchange_layout(p.shape, p.stack.layers, p.selection_slots);
     L.epoch = b.epoch;

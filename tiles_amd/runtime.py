@@ -110,7 +110,7 @@ EXPORTS = ("ti_error_string", "ti_last_error_message", "ti_abi", "ti_fingerprint
            "ti_context_diagnostic_sizes", "ti_context_collect", "ti_context_intermediate_sizes",
            "ti_context_collect_intermediates", "ti_ticket_free", "ti_context_set_timeline",
            "ti_context_timeline", "ti_context_set_matrix_prefill", "ti_context_lm_head_step",
-           "ti_set_worker_spin_limit")
+           "ti_set_worker_spin_limit", "ti_relayout_weights")
 DEFAULT_SPIN_LIMIT = 1 << 20  # TI_DEFAULT_SPIN_LIMIT
 
 _lib = None

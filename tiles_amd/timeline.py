@@ -100,10 +100,12 @@ def streamed_bytes(task: dict, model: dict, position: int) -> int:
             return 0
         steps = length * (chunk + 1) // chunks - length * chunk // chunks
         return 2 * steps * model["head_dim"] * element
-    if op in ("final_rms_norm", "ffn_reduce"):
+    if op == "final_rms_norm":
         return 0
     begin, end = task["operands"]["rows"]
-    width = {"embedding": 1, "ffn": 3 * d}.get(op, d)
+    # This worker's FFN chunk streams its gate and up rows; the reduction wave streams the Wdown
+    # rows of its outputs (the down projection, re-laid out row-major at upload).
+    width = {"embedding": 1, "ffn": 2 * d, "ffn_reduce": model["intermediate_size"]}.get(op, d)
     return (end - begin) * width * element
 
 
