@@ -39,7 +39,8 @@ def test_controlled_protocol_two_arms(tmp_path):
         assert report["arms"][arm]["library"].endswith("libtileinfer_amd.so")
     for context in ("1", "40"):
         entry = report["contexts"][context]
-        assert entry["spawn_order_by_block"] == {"0": ["A", "B"], "1": ["B", "A"]}
+        order = entry["spawn_order_by_block"]
+        assert sorted(order["0"]) == ["A", "B"] and order["1"] == order["0"][::-1]  # restarted in reverse halfway
         summary = entry["summary"]
         for arm in ("A", "B"):
             assert math.isfinite(summary[arm]["median_us"]) and summary[arm]["median_us"] > 0

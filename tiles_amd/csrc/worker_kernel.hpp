@@ -317,8 +317,8 @@ __device__ inline void wait_witness_words(const uint64_t* src, int count, int st
 // tagged bf16 elements per word (exchange_tag; `count` even).  Block-wide: every thread must
 // call it.
 // The first read is optimistic (one coherent round trip when the producers are done).  If any
-// word is still missing, every thread re-reads its words, with a back-off, until the block has
-// them all.  A probe of 256 one-per-CU blocks exchanging a 2048-element vector measured a round
+// word is still missing, every thread re-reads its missing words, with a back-off, until the
+// block has them all.  A probe of 256 one-per-CU blocks exchanging a 2048-element vector measured a round
 // at 2.46 us this way against 2.64 us with wave 0 first polling one "witness" word per producer
 // and the block re-reading after it (1.98 against 2.32 us with 64 producers): the witness scheme
 // adds a round trip once the data is there.  (`stride`, the witness spacing, is unused.)  Every
@@ -357,8 +357,16 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
             ok &= word_present<kHalves>(w[k], want);
         return ok;
     };
-    auto read = [&]() {
-        issue_reads();
+    // Later rounds re-read only the words still missing: re-reading a whole vector every round,
+    // from every worker, floods the memory channels that hold it while the producers and the
+    // weight streams still need them (the FFN's 8192 products are 32 KB per worker).
+    auto read_missing = [&]() {
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int index = k * kThreads + static_cast<int>(tid());
+            if (k * kThreads < words && !word_present<kHalves>(w[k], want))
+                w[k] = coherent_load64(src + (index < words ? index : words - 1));
+        }
         return check();
     };
     issue_reads();
@@ -369,7 +377,7 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
         sh.mark_read = __builtin_amdgcn_s_memrealtime();
     if (!all_present) {
         uint32_t spins = 0;
-        while (!block_sync_and(sh, read()) && !sh.aborted) {
+        while (!block_sync_and(sh, read_missing()) && !sh.aborted) {
             __builtin_amdgcn_s_sleep(2);
             if (tid() == 0)
                 stuck(exchange, xl, ++spins, sh);
