@@ -1763,7 +1763,7 @@ __device__ __forceinline__ void op_ffn(const Launch<BF16>& L, const ti_task_reco
     using N = Num<BF16>;
     constexpr int PV = N::kPerVec;
     constexpr int NV = 2 * VPL;                      // vectors per lane and row: gate, up
-    constexpr int D = VPL >= 8 ? 1 : (VPL >= 4 ? 3 : 4);
+    constexpr int D = VPL >= 8 ? 1 : (VPL >= 4 ? 2 : 4);  // 2 for Llama-3.2-1B: its 4 passes per chunk in two groups
     constexpr int kOut = VPL * PV;                   // hidden elements per lane of a row
     const int d = hidden_size<BF16, VPL>(L);
     const int layer = static_cast<int>(t.layer);
