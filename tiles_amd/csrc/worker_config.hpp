@@ -80,15 +80,15 @@ struct ExchangeLayout {
     size_t r;            // attention block output
     size_t product;      // the FFN's products p = SiLU(gate) * up, [intermediate] (tagged halves in bf16)
     size_t candidates;   // greedy candidates, 2 words per slot
-    size_t parts;        // split attention, per K/V head and chunk: the group's FP32 partial P V, then (max, sum) per head
+    size_t parts;        // split attention, per K/V head: every chunk's (max, sum) per query head, then the FP32 partials [output][chunk]
     size_t total;
     // A conditional, not an indexed array: a dynamic index into the launch record would put
     // the whole record in scratch memory.
     __host__ __device__ size_t hidden(int index) const { return index % 2 == 0 ? hidden0 : hidden1; }
 };
 
-// Words of one split-attention chunk's partial for one K/V head: group x head_dim outputs, then
-// (max, sum) for each of the group's query heads.
+// Exchange words per split-attention chunk of one K/V head: its (max, sum) for each of the
+// group's query heads and its group x head_dim FP32 partial outputs.
 __host__ __device__ inline size_t attention_part_words(const ti_model_shape& s)
 {
     const size_t group = s.kv_heads > 0 ? static_cast<size_t>(s.query_heads / s.kv_heads) : 0;

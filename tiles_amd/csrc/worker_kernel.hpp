@@ -1324,8 +1324,6 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     // attention rounds whatever the chunking.
     float* stat_max = sh.small;                    // [group] this chunk's statistics
     float* stat_sum = sh.small + kMaxGroup;
-    float* merged_max = sh.small + 2 * kMaxGroup;  // [group] every chunk's, merged
-    float* merged_sum = sh.small + 3 * kMaxGroup;
     const bool fused = chunks == 1;
     // Matrix path: the rounded probabilities also go to LDS as the bf16 operands of P V, each
     // head's positions contiguous and zero up to whole V blocks, so that one 16-byte read is a
@@ -1407,55 +1405,53 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     block_sync(sh);
 
     const int outputs = group * dh;
-    const int part_words = static_cast<int>(attention_part_words(s));
-    uint64_t* blocks = L.exchange + L.xl.parts + static_cast<size_t>(kv_head) * s.attention_chunks * part_words;
+    // The head's split-attention exchange block: every chunk's (max, sum) per query head, then the
+    // FP32 partials output-major, [output][chunk], so that the chunks one output's merger reads
+    // are adjacent words.  Strides use the plan's chunk count; `chunks` of them are active.  (Read
+    // only on the split path: computed before the branch, its launch-record reads cost the fused
+    // path 0.1-0.2 us per layer.)
+    auto stats_block = [&]() {
+        return L.exchange + L.xl.parts + static_cast<size_t>(kv_head) * s.attention_chunks * attention_part_words(s);
+    };
     if (!fused) {
         // This chunk's (max, sum) per head go out as epoch-tagged exchange words; every chunk of
-        // the head then reads all chunks' words, this chunk's own from LDS.  Every read of a round
-        // issues before any is looked at; a round with a word missing is read again.
+        // the head then reads all chunks' words, this chunk's own from LDS: one load per word
+        // (waves past the words issue none), and a round with words missing re-reads only those.
         const uint32_t stat_epoch = L.epoch_of(step, layer, kPhaseAttnStats);
         inject_delay(__LINE__);
         if (tid() < 2 * group) {
             const int g = static_cast<int>(tid()) >> 1;
             const float value = (tid() & 1) ? stat_sum[g] : stat_max[g];
-            coherent_store64(blocks + static_cast<size_t>(chunk) * part_words + outputs + tid(),
+            coherent_store64(stats_block() + static_cast<size_t>(chunk) * 2 * group + tid(),
                              (static_cast<uint64_t>(stat_epoch) << 32) | __float_as_uint(value));
         }
         const int stat_words = stat_floats;  // [chunk][max, sum of each head]
         // After the operands, or after the scores (check_shape: they fit the work region).
         const int stats_offset = packed_p ? (p_offset + (group * span_pad + 1) / 2 + 3) / 4 * 4 : p_offset;
         float* all_stats = scores + stats_offset;
-        constexpr int kStatBatch = 2;
+        const uint64_t* stats = stats_block();
         inject_delay(__LINE__);
-        for (int base = 0; base < stat_words; base += kStatBatch * kThreads) {  // block-uniform
-            uint64_t w[kStatBatch];
-            auto word_index = [&](int u) { return min(base + u * kThreads + static_cast<int>(tid()), stat_words - 1); };
-            auto read = [&]() {
-#pragma unroll
-                for (int u = 0; u < kStatBatch; ++u) {
-                    const int j = word_index(u), c = j / (2 * group);
-                    w[u] = coherent_load64(blocks + static_cast<size_t>(c) * part_words + outputs + (j - c * 2 * group));
-                }
-                bool ok = true;
-#pragma unroll
-                for (int u = 0; u < kStatBatch; ++u)
-                    ok &= word_index(u) / (2 * group) == chunk || static_cast<uint32_t>(w[u] >> 32) == stat_epoch;
-                return ok;
-            };
+        for (int base = 0; base < stat_words; base += kThreads) {  // block-uniform
+            const int j = base + static_cast<int>(tid());
+            const bool wanted = j < stat_words && j / (2 * group) != chunk;
+            uint64_t w = 0;
+            if (wanted)
+                w = coherent_load64(stats + j);
+            bool have = !wanted || static_cast<uint32_t>(w >> 32) == stat_epoch;
             uint32_t spins = 0;
-            while (!block_sync_and(sh, read()) && !sh.aborted) {
+            while (!block_sync_and(sh, have) && !sh.aborted) {
                 __builtin_amdgcn_s_sleep(2);
                 if (tid() == 0)
                     stuck(L.exchange, L.xl, ++spins, sh);
-            }
-#pragma unroll
-            for (int u = 0; u < kStatBatch; ++u) {
-                const int j = base + u * kThreads + static_cast<int>(tid());
-                if (j < stat_words) {
-                    const int c = j / (2 * group), k = j - c * 2 * group;
-                    all_stats[j] = c == chunk ? ((k & 1) ? stat_sum[k >> 1] : stat_max[k >> 1])
-                                              : __uint_as_float(static_cast<uint32_t>(w[u]));
+                if (!have) {
+                    w = coherent_load64(stats + j);
+                    have = static_cast<uint32_t>(w >> 32) == stat_epoch;
                 }
+            }
+            if (j < stat_words) {
+                const int k = j % (2 * group);
+                all_stats[j] = wanted ? __uint_as_float(static_cast<uint32_t>(w))
+                                      : ((k & 1) ? stat_sum[k >> 1] : stat_max[k >> 1]);
             }
         }
         block_sync(sh);
@@ -1474,22 +1470,15 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             for (int c = lane; c < chunks; c += 64)
                 part = fmaf(all_stats[c * 2 * group + 2 * g + 1], expf(all_stats[c * 2 * group + 2 * g] - m), part);
             const float total = lane_value(group_sum<64>(part), 63);
-            if (lane == 0) {
-                merged_max[g] = m;
-                merged_sum[g] = total;
-            }
-        }
-        block_sync(sh);
-        if (wave < group) {
-            const float m = merged_max[wave], total = merged_sum[wave];
-            float* row = scores + wave * span;
+            // The same wave rounds its head's probabilities with the merged statistics.
+            float* row = scores + g * span;
 #pragma unroll 4
             for (int i = lane; i < (packed_p ? span_pad : span); i += 64) {
                 const float p = i < span ? N::round(expf(row[i] - m) / total) : 0.0f;
                 if (i < span)
                     row[i] = p;
                 if (packed_p)
-                    put_p(wave, i, p);
+                    put_p(g, i, p);
             }
         }
         block_sync(sh);
@@ -1548,12 +1537,15 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 }
             }
         }
+        // Every load of the task has returned (the last block loaded no next V tiles; waves past
+        // the live tiles never read theirs): saying so before any store lets the publishes below
+        // issue back to back, and leaves the task with no load in flight.  A task that ended
+        // with loads the compiler still counted as pending made the dispatcher, where every
+        // task's paths merge, wait for vmcnt(2) after each task's end barrier: on a task that
+        // had just published, for its stores to complete (about 1 us).
+        wait_vmem<0>();
         if (fused) {
-            // Lanes 0-15 of wave n hold output dims 16 n + l of every head of the group.  The
-            // last block loaded no next V tiles, so nothing is in flight; saying so lets the
-            // stores issue back to back (the compiler otherwise made each wait for the store
-            // before the previous one, assuming a V tile load might still be pending).
-            wait_vmem<0>();
+            // Lanes 0-15 of wave n hold output dims 16 n + l of every head of the group.
             const uint32_t out_epoch = L.epoch_of(step, layer, kPhaseAttn);
             if (n < dh / 16 && tk == 0)
 #pragma unroll
@@ -1645,9 +1637,11 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const uint32_t part_epoch = L.epoch_of(step, layer, kPhaseAttnPart);
     if (chunk == 0)
         wait_stores();  // the K row chunk 0 stored is in the cache before any output of the head is published
+    const int chunk_stride = s.attention_chunks;
+    uint64_t* partial_block = stats_block() + static_cast<size_t>(chunk_stride) * 2 * group;
     inject_delay(__LINE__);
     if (owner)
-        coherent_store64(blocks + static_cast<size_t>(chunk) * part_words + mine,
+        coherent_store64(partial_block + static_cast<size_t>(mine) * chunk_stride + chunk,
                          (static_cast<uint64_t>(part_epoch) << 32) | __float_as_uint(out));
     const int owned = chunk < outputs ? (outputs - 1 - chunk) / chunks + 1 : 0;  // outputs chunk, chunk + chunks, ...
     const int words = owned * chunks;                                           // [owned output][chunk]
@@ -1657,52 +1651,45 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     block_sync(sh);  // P V's LDS reads are done
     if (owner)
         own[mine] = out;
-    constexpr int kMergeBatch = 2;
+    // Slot j = k chunks + c: output chunk + k chunks from chunk c, adjacent words of the block.
+    // One load per slot (this chunk's own from LDS), and a round re-reads only the missing.
     inject_delay(__LINE__);
-    for (int base = 0; base < words; base += kMergeBatch * kThreads) {  // block-uniform
-        uint64_t w[kMergeBatch];
-        auto slot = [&](int u) { return min(base + u * kThreads + static_cast<int>(tid()), words - 1); };
-        auto read = [&]() {
-#pragma unroll
-            for (int u = 0; u < kMergeBatch; ++u) {
-                const int j = slot(u), k = j / chunks, c = j - k * chunks;
-                w[u] = coherent_load64(blocks + static_cast<size_t>(c) * part_words + chunk + k * chunks);
-            }
-            bool ok = true;
-#pragma unroll
-            for (int u = 0; u < kMergeBatch; ++u)
-                ok &= slot(u) % chunks == chunk || static_cast<uint32_t>(w[u] >> 32) == part_epoch;
-            return ok;
-        };
+    for (int base = 0; base < words; base += kThreads) {  // block-uniform
+        const int j = base + static_cast<int>(tid());
+        const int k = j / chunks, c = j - k * chunks;
+        const bool wanted = j < words && c != chunk;
+        const uint64_t* word = partial_block + static_cast<size_t>(chunk + k * chunks) * chunk_stride + c;
+        uint64_t w = 0;
+        if (wanted)
+            w = coherent_load64(word);
+        bool have = !wanted || static_cast<uint32_t>(w >> 32) == part_epoch;
         uint32_t spins = 0;
-        while (!block_sync_and(sh, read()) && !sh.aborted) {
+        while (!block_sync_and(sh, have) && !sh.aborted) {
             __builtin_amdgcn_s_sleep(1);
             if (tid() == 0)
                 stuck(L.exchange, L.xl, ++spins, sh);
-        }
-#pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u) {
-            const int j = base + u * kThreads + static_cast<int>(tid());
-            if (j < words) {
-                const int k = j / chunks, c = j - k * chunks;
-                merge[j] = c == chunk ? own[chunk + k * chunks] : __uint_as_float(static_cast<uint32_t>(w[u]));
+            if (!have) {
+                w = coherent_load64(word);
+                have = static_cast<uint32_t>(w >> 32) == part_epoch;
             }
         }
+        if (j < words)
+            merge[j] = wanted ? __uint_as_float(static_cast<uint32_t>(w)) : own[chunk + k * chunks];
     }
     block_sync(sh);
     if (static_cast<int>(tid()) < owned) {
-        // In chunk order, 8 LDS reads issued at a time (a loop of read-then-add would pay one
+        // In chunk order, 16 LDS reads issued at a time (a loop of read-then-add would pay one
         // LDS round trip per chunk).
         const int k = tid();
         const float* column = merge + k * chunks;
         float total = 0.0f;
-        for (int c0 = 0; c0 < chunks; c0 += 8) {
-            float v[8];
+        for (int c0 = 0; c0 < chunks; c0 += 16) {
+            float v[16];
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
+            for (int u = 0; u < 16; ++u)
                 v[u] = column[c0 + u < chunks ? c0 + u : 0];
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
+            for (int u = 0; u < 16; ++u)
                 if (c0 + u < chunks)
                     total += v[u];
         }
