@@ -197,6 +197,10 @@ struct Shared {
     alignas(16) float small[kMaxTaskRows];  // reductions over waves, softmax statistics, residual rows
     float rotated[(kMaxGroup + 1) * kMaxHeadDim];
     float vcur[kMaxHeadDim];
+    // The same rotated Q heads and K row, and V row, as bf16 bits (bf16 storage): a lane's
+    // 16-byte matrix operand is then one LDS read instead of eight floats to pack.
+    alignas(16) uint16_t rotated_bits[(kMaxGroup + 1) * kMaxHeadDim];
+    alignas(16) uint16_t vcur_bits[kMaxHeadDim];
     float rope_cs[kMaxHeadDim];  // the position's RoPE cos (first half) and sin (second half)
     int rope_position;           // the position rope_cs holds, -1 when none
     ti_candidate candidates[kWaves];
@@ -1105,8 +1109,11 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                L.qkv_stride, L.epoch_of(step, layer, kPhaseQKV), L.exchange, L.xl, sh,
                [&](int i, uint32_t p) {
                    const float v = N::from_payload(p);
-                   if (i >= qk)
+                   if (i >= qk) {
                        sh.vcur[i - qk] = v;
+                       if constexpr (kMfma)
+                           sh.vcur_bits[i - qk] = static_cast<uint16_t>(p);
+                   }
                    if constexpr (kRopeInWave)
                        held = v;  // i == tid(): block <= kThreads
                    else if (i < qk)
@@ -1141,6 +1148,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             const float value = d < half ? N::round(N::round(held * c) - N::round(partner * sn))
                                          : N::round(N::round(held * c) + N::round(partner * sn));
             sh.rotated[t] = value;
+            if constexpr (kMfma)
+                sh.rotated_bits[t] = static_cast<uint16_t>(__float_as_uint(value) >> 16);
             if (chunk == 0) {
                 wait_stores();
                 store_rotated(t, value);
@@ -1153,8 +1162,14 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             const int head = index / half, pair = index - head * half;
             const float c = sh.rope_cs[pair], sn = sh.rope_cs[half + pair];
             const float a = sh.region[head * dh + pair], b = sh.region[head * dh + pair + half];
-            sh.rotated[head * dh + pair] = N::round(N::round(a * c) - N::round(b * sn));
-            sh.rotated[head * dh + pair + half] = N::round(N::round(b * c) + N::round(a * sn));
+            const float lo = N::round(N::round(a * c) - N::round(b * sn));
+            const float hi = N::round(N::round(b * c) + N::round(a * sn));
+            sh.rotated[head * dh + pair] = lo;
+            sh.rotated[head * dh + pair + half] = hi;
+            if constexpr (kMfma) {
+                sh.rotated_bits[head * dh + pair] = static_cast<uint16_t>(__float_as_uint(lo) >> 16);
+                sh.rotated_bits[head * dh + pair + half] = static_cast<uint16_t>(__float_as_uint(hi) >> 16);
+            }
         }
         block_sync(sh);  // the region is dead: the scores may overwrite it
         if (chunk == 0)
@@ -1191,7 +1206,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         const bool current = begin + (first_tile + tile) * kTile + tr == position;
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
-            const u32x4 now = pack8(sh.vcur + 32 * k + 8 * tk);
+            const u32x4 now = *reinterpret_cast<const u32x4*>(sh.vcur_bits + 32 * k + 8 * tk);
             *reinterpret_cast<u32x4*>(vt + row * kVRow + 32 * k + 8 * tk) = current ? now : vb[k];
         }
     };
@@ -1219,9 +1234,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         const int qrow = tr < group ? tr : 0;
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
-            const u32x4 q = pack8(sh.rotated + qrow * dh + 32 * k + 8 * tk);
+            const u32x4 q = *reinterpret_cast<const u32x4*>(sh.rotated_bits + qrow * dh + 32 * k + 8 * tk);
             qa[k] = tr < group ? q : zero;
-            kc[k] = pack8(sh.rotated + group * dh + 32 * k + 8 * tk);
+            kc[k] = *reinterpret_cast<const u32x4*>(sh.rotated_bits + group * dh + 32 * k + 8 * tk);
         }
         auto tile_scores = [&](int tile, const u32x4* kb) {
             const int time = begin + tile * kTile + tr;
@@ -1545,14 +1560,16 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         // had just published, for its stores to complete (about 1 us).
         wait_vmem<0>();
         if (fused) {
-            // Lanes 0-15 of wave n hold output dims 16 n + l of every head of the group.
+            // Lanes 0-15 of wave n hold output dims 16 n + l of every head of the group.  The
+            // destination and epoch are read from the LDS launch record once, before the stores
+            // (after each store the compiler would read them again).
             const uint32_t out_epoch = L.epoch_of(step, layer, kPhaseAttn);
+            uint64_t* const attn_words = L.exchange + L.xl.attn;
             if (n < dh / 16 && tk == 0)
 #pragma unroll
                 for (int g = 0; g < MG; ++g)
                     if (g < group)
-                        publish_element<BF16>(L.exchange + L.xl.attn, (first_head + g) * dh + 16 * n + tr, N::round(o[g]),
-                                              out_epoch);
+                        publish_element<BF16>(attn_words, (first_head + g) * dh + 16 * n + tr, N::round(o[g]), out_epoch);
             return;
         }
         float* results = sh.rotated;  // [group][dh]: the unrotated heads are dead
