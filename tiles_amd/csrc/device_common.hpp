@@ -261,6 +261,37 @@ __device__ inline float group_sum(float v)
     return v;
 }
 
+// group_sum<W> of N independent values, one DPP step of all of them at a time: the chains
+// interleave instead of each paying its dependent-step latency in turn.
+template <int W, int N>
+__device__ inline void group_sum_all(float (&v)[N])
+{
+    if constexpr (W >= 2)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppQuadXor1>(v[n]);
+    if constexpr (W >= 4)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppQuadXor2>(v[n]);
+    if constexpr (W >= 8)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowHalfMirror>(v[n]);
+    if constexpr (W >= 16)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowMirror>(v[n]);
+    if constexpr (W >= 32)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowBcast15, 0xA>(v[n]);
+    if constexpr (W >= 64)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+            v[n] += dpp<kDppRowBcast31, 0xC>(v[n]);
+}
+
 // Maximum with the same lane layout as group_sum.
 __device__ inline float group_max(float v, int width)
 {

@@ -885,11 +885,34 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
             issue(pass0 + s + D, w[s]);
         }
     }
+    // The last group: each pass's dot products as its loads arrive, then the reductions of all of
+    // them together and the staged stores after those.  Reducing and storing each pass in turn
+    // made every pass a serial chain of its own (the masked store between passes split the code
+    // into blocks the scheduler does not interleave), also for passes past the task.
+    float parts[D * NM];
     unroll<D>([&](auto step) {
         constexpr int s = decltype(step)::value;
         wait_vmem<(D - 1 - s) * K>();
-        compute(s, pass0 + s);
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+            parts[s * NM + m] = in.template dot<BF16>(&w[s][m * VPL]);
     });
+    if constexpr (VPL > 1) {
+        group_sum_all<64>(parts);
+    } else {
+#pragma unroll
+        for (int j = 0; j < D * NM; ++j)
+            parts[j] = group_sum(parts[j], g.lr);
+    }
+    if (g.col == g.lr - 1)
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int row = g.first_row(r0, pass0 + s) + g.sub;
+            if (row < r1)
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+                    staged[(row - r0) * NM + m] = parts[s * NM + m];
+        }
     block_sync(sh);
     for (int row = r0 + static_cast<int>(tid()); row < r1; row += kThreads) {
         float dots[NM];
@@ -1949,6 +1972,15 @@ __device__ __forceinline__ void op_down(const Launch<BF16>& L, const ti_task_rec
     };
     issue(begin);
     issue_fence();
+    // What the rows' emission needs from the LDS launch record, read while the loads are in
+    // flight: after the poll's stores and barriers the compiler would read each field again, a
+    // chain of LDS round trips between the last product's arrival and the publish.
+    const uint32_t y_epoch = L.epoch_of(step, layer, kPhaseY);
+    const uint32_t r_epoch = L.epoch_of(step, layer, kPhaseR);
+    uint64_t* const y_words = L.exchange + L.xl.hidden((layer + 1) % 2);
+    void* const hidden = (layer + 1) % 2 == 0 ? L.input : L.output;
+    float* const block_trace = L.block_trace;
+    float* const ffn_trace = L.ffn_trace;
     uint16_t* p_bits = reinterpret_cast<uint16_t*>(sh.region);  // bf16: p as bits
     float* p_values = sh.region;                                  // fp32: p as values
     poll_words<BF16, max_product<BF16>()>(L.exchange + L.xl.product, f, 1, L.epoch_of(step, layer, kPhaseFfn), L.exchange,
@@ -1987,12 +2019,13 @@ __device__ __forceinline__ void op_down(const Launch<BF16>& L, const ti_task_rec
                 }
             }
         });
+        // All G reductions first, then the stores: a store under a lane mask between them made
+        // each row's dot products and DPP steps a serial chain of its own (0.5 us per task).
+        group_sum_all<64>(acc);
+        if (lane == 63)
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) {
-            const float total = group_sum<64>(acc[gg]);
-            if (lane == 63)
-                wave_sums[gg * kWaves + wave] = total;
-        }
+            for (int gg = 0; gg < G; ++gg)
+                wave_sums[gg * kWaves + wave] = acc[gg];
         block_sync(sh);
         if (me < G && first + me < end) {
             const int row = first + me;
@@ -2000,16 +2033,18 @@ __device__ __forceinline__ void op_down(const Launch<BF16>& L, const ti_task_rec
 #pragma unroll
             for (int wv = 0; wv < kWaves; ++wv)
                 total += wave_sums[me * kWaves + wv];
-            const float r = attention_output_element(L, layer, step, row, sh);
+            // The residual r: in LDS when this worker's FFN task of the layer read it.
+            const float r = sh.rsave_tag == r_epoch
+                                ? sh.rsave[row]
+                                : N::from_payload(poll_element<BF16>(L.exchange + L.xl.r, row, r_epoch, L.exchange, L.xl, sh));
             const float projected = N::round(total);
             const float y = N::round(projected + r);
-            void* hidden = (layer + 1) % 2 == 0 ? L.input : L.output;
             N::store(hidden, row, y);
-            if (L.block_trace)
-                global(L.block_trace)[static_cast<size_t>(layer) * d + row] = y;
-            if (L.ffn_trace)
-                global(L.ffn_trace)[static_cast<size_t>(layer) * d + row] = projected;
-            publish_element<BF16>(L.exchange + L.xl.hidden((layer + 1) % 2), row, y, L.epoch_of(step, layer, kPhaseY));
+            if (block_trace)
+                global(block_trace)[static_cast<size_t>(layer) * d + row] = y;
+            if (ffn_trace)
+                global(ffn_trace)[static_cast<size_t>(layer) * d + row] = projected;
+            publish_element<BF16>(y_words, row, y, y_epoch);
         }
         block_sync(sh);
     }
