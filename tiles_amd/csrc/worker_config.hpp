@@ -80,7 +80,7 @@ struct ExchangeLayout {
     size_t r;            // attention block output
     size_t product;      // the FFN's products p = SiLU(gate) * up, [intermediate] (tagged halves in bf16)
     size_t candidates;   // greedy candidates, 2 words per slot
-    size_t parts;        // split attention, per K/V head: every chunk's (max, sum) per query head, then the FP32 partials [output][chunk]
+    size_t parts;        // split attention, per K/V head: every chunk's (max, sum) per query head, then its FP32 partials [chunk][output]
     size_t total;
     // A conditional, not an indexed array: a dynamic index into the launch record would put
     // the whole record in scratch memory.

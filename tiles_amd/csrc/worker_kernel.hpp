@@ -1443,9 +1443,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     block_sync(sh);
 
     const int outputs = group * dh;
-    // The head's split-attention exchange block: every chunk's (max, sum) per query head, then the
-    // FP32 partials output-major, [output][chunk], so that the chunks one output's merger reads
-    // are adjacent words.  Strides use the plan's chunk count; `chunks` of them are active.  (Read
+    // The head's split-attention exchange block: every chunk's (max, sum) per query head, then
+    // every chunk's FP32 partials, [chunk][output].  Strides use the plan's chunk count; `chunks`
+    // of them are active.  (Read
     // only on the split path: computed before the branch, its launch-record reads cost the fused
     // path 0.1-0.2 us per layer.)
     auto stats_block = [&]() {
@@ -1668,12 +1668,13 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         return;
     }
     // Split context: every chunk publishes its FP32 partial P V as exchange words, then merges a
-    // slice of the group's outputs.  Output o belongs to chunk o mod chunks, which reads that
-    // output's partial from every chunk, adds them in chunk order (output_projection,
-    // ops.cuh:718-728), rounds the sum once and publishes it.  The merge's reads are spread over
-    // all the head's chunk workers (one merger reading every chunk's whole partial finished about
-    // 6 us after the other chunks at ctx 4096), and no arrival counter stands between a chunk and
-    // the merge: the words carry the epoch.
+    // block of the group's outputs.  Chunk m merges outputs [m per, (m + 1) per): it reads those
+    // outputs' partials from every chunk (a run of `per` adjacent words per chunk, where a
+    // cyclic assignment read every word from its own line), adds them in chunk order
+    // (output_projection, ops.cuh:718-728), rounds the sum once and publishes it.  The merge is
+    // spread over all the head's chunk workers (one merger reading every chunk's whole partial
+    // finished about 6 us after the other chunks at ctx 4096), and no arrival counter stands
+    // between a chunk and the merge: the words carry the epoch.
     const uint32_t part_epoch = L.epoch_of(step, layer, kPhaseAttnPart);
     if (chunk == 0)
         wait_stores();  // the K row chunk 0 stored is in the cache before any output of the head is published
@@ -1681,24 +1682,25 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     uint64_t* partial_block = stats_block() + static_cast<size_t>(chunk_stride) * 2 * group;
     inject_delay(__LINE__);
     if (owner)
-        coherent_store64(partial_block + static_cast<size_t>(mine) * chunk_stride + chunk,
+        coherent_store64(partial_block + static_cast<size_t>(chunk) * outputs + mine,
                          (static_cast<uint64_t>(part_epoch) << 32) | __float_as_uint(out));
-    const int owned = chunk < outputs ? (outputs - 1 - chunk) / chunks + 1 : 0;  // outputs chunk, chunk + chunks, ...
-    const int words = owned * chunks;                                           // [owned output][chunk]
+    const int per = (outputs + chunks - 1) / chunks;  // outputs per merging chunk
+    const int first_out = chunk * per;
+    const int owned = max(0, min(per, outputs - first_out));
+    const int words = chunks * per;                    // [chunk][output of the block]
     float* own = sh.region;                  // [outputs]: this chunk's partial, for its own slots
-    float* merge = sh.region + kMaxThreadsPadded;  // [owned output][chunk]
+    float* merge = sh.region + kMaxThreadsPadded;  // [chunk][per]
     static_assert(2 * kMaxThreadsPadded <= kLdsRegionFloats, "merge slots exceed the work region");
     block_sync(sh);  // P V's LDS reads are done
     if (owner)
         own[mine] = out;
-    // Slot j = k chunks + c: output chunk + k chunks from chunk c, adjacent words of the block.
     // One load per slot (this chunk's own from LDS), and a round re-reads only the missing.
     inject_delay(__LINE__);
     for (int base = 0; base < words; base += kThreads) {  // block-uniform
         const int j = base + static_cast<int>(tid());
-        const int k = j / chunks, c = j - k * chunks;
-        const bool wanted = j < words && c != chunk;
-        const uint64_t* word = partial_block + static_cast<size_t>(chunk + k * chunks) * chunk_stride + c;
+        const int c = j / per, k = j - c * per;
+        const bool wanted = j < words && k < owned && c != chunk;
+        const uint64_t* word = partial_block + static_cast<size_t>(c) * outputs + first_out + k;
         uint64_t w = 0;
         if (wanted)
             w = coherent_load64(word);
@@ -1714,26 +1716,25 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             }
         }
         if (j < words)
-            merge[j] = wanted ? __uint_as_float(static_cast<uint32_t>(w)) : own[chunk + k * chunks];
+            merge[j] = wanted ? __uint_as_float(static_cast<uint32_t>(w)) : (k < owned ? own[first_out + k] : 0.0f);
     }
     block_sync(sh);
     if (static_cast<int>(tid()) < owned) {
         // In chunk order, 16 LDS reads issued at a time (a loop of read-then-add would pay one
         // LDS round trip per chunk).
         const int k = tid();
-        const float* column = merge + k * chunks;
         float total = 0.0f;
         for (int c0 = 0; c0 < chunks; c0 += 16) {
             float v[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u)
-                v[u] = column[c0 + u < chunks ? c0 + u : 0];
+                v[u] = merge[(c0 + u < chunks ? c0 + u : 0) * per + k];
 #pragma unroll
             for (int u = 0; u < 16; ++u)
                 if (c0 + u < chunks)
                     total += v[u];
         }
-        publish_element<BF16>(attn, first_head * dh + chunk + k * chunks, N::round(total), out_epoch);
+        publish_element<BF16>(attn, first_head * dh + first_out + k, N::round(total), out_epoch);
     }
 }
 
