@@ -204,7 +204,8 @@ struct Shared {
     float rope_cs[kMaxHeadDim];  // the position's RoPE cos (first half) and sin (second half)
     int rope_position;           // the position rope_cs holds, -1 when none
     ti_candidate candidates[kWaves];
-    ti_task_record stream[kLdsStreamRecords];  // this worker's instructions, when they fit
+    ti_task_record stream[kLdsStreamRecords];  // this worker's instructions but barriers, when they fit
+    uint16_t stream_index[kLdsStreamRecords];  // each one's position in the worker's stream
     uint32_t xsave_tag;  // epoch_of(step, layer, kPhaseQKV) of xsave's contents, 0 when empty
     uint32_t rsave_tag;  // epoch_of(step, layer, kPhaseR) of rsave's contents
     int flag;
@@ -2226,11 +2227,42 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
         return;
     const ti_worker_task_range stream = load_record(L.streams + blockIdx.x);
     // The worker's instruction records move to LDS once: read from memory as each task
-    // starts, every record would cost a dependent memory round trip between two tasks.
+    // starts, every record would cost a dependent memory round trip between two tasks.  The
+    // barrier records stay behind (waves synchronize through the exchange words; stepping over
+    // each one cost an LDS round trip between two tasks), each kept record with its position in
+    // the stream, which indexes the timeline.
     const bool cached = stream.count <= static_cast<uint32_t>(kLdsStreamRecords);
-    if (cached)
-        for (uint32_t i = tid(); i < stream.count; i += kBlockThreads)
-            sh.stream[i] = load_record(L.instructions + stream.begin + i);
+    uint32_t tasks = 0;  // records in sh.stream when cached
+    if (cached) {
+        for (uint32_t first = 0; first < stream.count; first += kBlockThreads) {  // block-uniform
+            const uint32_t i = first + tid();
+            const bool inside = i < stream.count;
+            const ti_task_record r = load_record(L.instructions + stream.begin + (inside ? i : 0));
+            const bool keep = inside && r.opcode != TI_OP_BARRIER;
+            // Position among the kept records: kept lanes below in this wave, then earlier waves.
+            const uint64_t kept = __ballot(keep);
+            const uint32_t lane = tid() & 63;
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(kept >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(kept), 0u));
+            if (lane == 0)
+                sh.candidates[wave_id()].id = static_cast<int>(__builtin_popcountll(kept));  // free until the first step
+            __syncthreads();
+            uint32_t before = tasks;
+            for (int w = 0; w < wave_id(); ++w)
+                before += static_cast<uint32_t>(sh.candidates[w].id);
+            uint32_t total = tasks;
+            for (int w = 0; w < kWaves; ++w)
+                total += static_cast<uint32_t>(sh.candidates[w].id);
+            if (keep) {
+                sh.stream[before + below] = r;
+                sh.stream_index[before + below] = static_cast<uint16_t>(i);
+            }
+            tasks = total;
+            __syncthreads();  // the wave counts are read before the next round writes them
+        }
+    }
+    // Read once: the launch record in LDS would be read again at every task's start and end.
+    const bool timeline = L.timeline != nullptr;
     __syncthreads();
     for (int step = 0; step < L.steps; ++step) {
         // The previous step's K/V cache stores complete before this step publishes anything.
@@ -2246,16 +2278,17 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
         if (L.stack.full_stack && (token < 0 || token >= L.stack.vocab_size)) {
             return;
         }
-        for (uint32_t index = stream.begin; index < stream.begin + stream.count; ++index) {
-            const ti_task_record task = cached ? sh.stream[index - stream.begin] : load_record(L.instructions + index);
+        const uint32_t records = cached ? tasks : stream.count;
+        for (uint32_t k = 0; k < records; ++k) {
+            const ti_task_record task = cached ? sh.stream[k] : load_record(L.instructions + stream.begin + k);
             if (task.opcode == TI_OP_BARRIER)
-                continue;  // waves synchronize through the exchange words
+                continue;  // (uncached streams only) waves synchronize through the exchange words
             // Optional timeline of every instruction, the last step's left in the buffer
             // (diagnostic_context.cu:257-285): this build's record, the 100 MHz device clock
             // (s_memrealtime) at the start, when the first exchange read returned, when the inputs
             // were complete and at the end; or the reference's (launch.cuh:25-28), the shader
             // cycle counter (s_memtime) at the start and end and the device clock at the start in ns.
-            if (L.timeline && tid() == 0) {
+            if (timeline && tid() == 0) {
                 sh.mark_start_cycles = __builtin_amdgcn_s_memtime();
                 sh.mark_start = __builtin_amdgcn_s_memrealtime();
                 sh.mark_read = 0;
@@ -2280,7 +2313,8 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
             default: break;  // attention_values: merged inside the scores tasks
             }
             block_sync(sh);
-            if (L.timeline && tid() == 0) {
+            if (timeline && tid() == 0) {
+                const uint32_t index = stream.begin + (cached ? static_cast<uint32_t>(sh.stream_index[k]) : k);
                 if (L.timeline_fields == TI_TIMELINE_FIELDS) {
                     TILES_GLOBAL uint64_t* record = global(L.timeline) + TI_TIMELINE_FIELDS * static_cast<size_t>(index);
                     record[0] = sh.mark_start;
