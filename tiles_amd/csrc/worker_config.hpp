@@ -19,6 +19,7 @@ inline constexpr int kMaxHeadDim = 128;
 inline constexpr int kMaxGroup = 4;                 // query heads per K/V head (registers hold them all)
 inline constexpr int kMaxGroupTimesHeadDim = 512;   // attention P*V reduction in LDS (4 x 128)
 inline constexpr int kMaxTaskRows = 512;            // rows of one GEMV task kept in LDS
+inline constexpr int kWarmPositions = 128;          // positions below which an output projection warms its worker's next FFN rows
 inline constexpr int kMaxStreamRecords = 1536;      // a worker's instruction stream cached in LDS (longer ones are read from memory)
 // Shared bytes for one attention task's scores of all its query heads, in the package's
 // element type (the planner's chunk capacity, plan_core.py:91-97).  Held as FP32 in LDS.

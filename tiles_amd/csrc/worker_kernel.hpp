@@ -2279,9 +2279,10 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
     }
     // Read once: the launch record in LDS would be read again at every task's start and end.
     const bool timeline = L.timeline != nullptr;
-    // Positions below this have an attention of one chunk and one staged V block (see the
+    // Positions below this have a short attention of one chunk and one staged V block (see the
     // output projection case below).
-    const int quiet_attention = min(L.shape.attention_fused_steps, vt_block_positions(L.shape.head_dim));
+    const int quiet_attention =
+        min(kWarmPositions, min(L.shape.attention_fused_steps, vt_block_positions(L.shape.head_dim)));
     __syncthreads();
     for (int step = 0; step < L.steps; ++step) {
         // The previous step's K/V cache stores complete before this step publishes anything.
@@ -2321,9 +2322,11 @@ __global__ __launch_bounds__(kBlockThreads, 1) void decoder_worker(Launch<BF16> 
                 // The first weight pass of the worker's next FFN task comes into L2 while the
                 // projection awaits the attention output, but only while the attention is one
                 // chunk of at most one staged V block, which reads no memory after its input
-                // arrives: the burst then delays nothing the token waits for (at ctx 1-64 the
-                // step took 11.5 us less; with a second V block, or split chunks, whose reads it
-                // delayed, 10 and 24 us more).  Cached streams only.
+                // arrives, and short: the burst then delays little the token waits for.  Measured
+                // per 64-token launch on Llama-3.2-1B: -10.9 / -5.1 / +3.6 us per token starting at
+                // positions 1 / 64 / 128 (the K/V rows the attention loads before its input poll
+                // return later behind it), +16 with a second V block and +24 with split chunks.
+                // Cached streams only.
                 int warm_begin = -1, warm_end = -1;
                 if (cached && L.position + step < quiet_attention)
                     for (uint32_t n = k + 1; n < tasks && n < k + 3u; ++n) {
