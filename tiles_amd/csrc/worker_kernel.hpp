@@ -2001,6 +2001,11 @@ __device__ __forceinline__ void op_down(const Launch<BF16>& L, const ti_task_rec
     float* const ffn_trace = L.ffn_trace;
     uint16_t* p_bits = reinterpret_cast<uint16_t*>(sh.region);  // bf16: p as bits
     float* p_values = sh.region;                                  // fp32: p as values
+    // The products' first read goes out once half of the rows have arrived: a read samples the
+    // exchange when it is issued and returns after the loads before it, so one issued with the
+    // rows found the slowest FFN chunks' products missing when it came back, and a second round
+    // followed the rows' arrival.
+    wait_vmem<kLoads / 2>();
     poll_words<BF16, max_product<BF16>()>(L.exchange + L.xl.product, f, 1, L.epoch_of(step, layer, kPhaseFfn), L.exchange,
                                          L.xl, sh, [&](int i, uint32_t payload) {
                                              if constexpr (BF16)
