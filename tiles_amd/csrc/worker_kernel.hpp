@@ -853,6 +853,11 @@ __device__ __forceinline__ void gemv(const void* base, RowOffset row_offset, int
     for (int s = 0; s < D; ++s)
         issue(s, w[s]);
     issue_fence();
+    // The input's first read goes out once the first pass has arrived: a read samples the
+    // exchange when it is issued and returns after the loads before it, so one issued with the
+    // weights found late producers' words missing when it came back, and a second round followed.
+    if constexpr (D > 1)
+        wait_vmem<(D - 1) * K>();
     prepare();
     const InputSlice<VPL> in = make_slice();
     // Whole groups of D passes without branches (passes past the task compute values nobody
