@@ -142,10 +142,19 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
     static_assert(kTile * kVectors % kAttnThreads == 0, "whole vectors per thread");
     __shared__ __attribute__((aligned(16))) uint16_t vs[kTile * kVStride];
     __shared__ __attribute__((aligned(16))) uint16_t ks[kTile * kKStride];
-    const int h = blockIdx.y, group = nq / nkv;
+    // Causal blocks differ in work by their row block (block x reads x + 1 key tiles at position
+    // 0).  Every block is resident at once, two per CU, and the dispatcher gives blocks L and L + H
+    // (H = half the grid) the same CU; launched in row-block order those two were alike, and the
+    // CUs holding two of the last row blocks set the kernel's time.  So block L takes the L-th
+    // heaviest (row block, head) and block L + H the L-th lightest: the two add up to one
+    // average pair.  Any assignment covers every (row block, head) once.
+    const int row_blocks = gridDim.x, items = gridDim.x * gridDim.y, half = (items + 1) / 2;
+    const int linear = blockIdx.x + gridDim.x * blockIdx.y;
+    const int heaviest = linear < half ? linear : items - 1 - (linear - half);  // index in descending weight
+    const int h = heaviest % nkv, group = nq / nkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x / 64;
     const int col = lane & 15, g4 = lane >> 4;
-    const int r0 = blockIdx.x * kAttnRows;
+    const int r0 = (row_blocks - 1 - heaviest / nkv) * kAttnRows;
     const int last_row = min(r0 + kAttnRows, rows) - 1;
     const int last_key = position + last_row;  // the block's last key: every load stays at or below it
     const int tiles = last_key / kTile + 1;
