@@ -954,15 +954,18 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     const int position = L.position + step;
     const int begin = static_cast<int>(t.begin), end = static_cast<int>(t.end);
     const uint32_t epoch = L.epoch_of(step, layer, kPhaseQKV);
-    // Rows may span Wq, Wk and Wv, which are separate regions of the layer's weights.  The
-    // region is a select of values read once (a select of the fields themselves became branches
-    // around their loads).
-    const uint32_t wq = L.layout.Wq, wk = L.layout.Wk, wv = L.layout.Wv;
+    // Rows may span Wq, Wk and Wv, which are separate regions of the layer's weights: row r of
+    // a region that starts at row `first` lies at region + (r - first) d = base + r d, with base
+    // = region - first d (mod 2^32).  The base is the V region's plus differences selected
+    // against zero: a select among the captured bases became an indexed load from a copy of
+    // them in scratch memory, and a select of the launch record's fields branches around loads.
+    const uint32_t ud = static_cast<uint32_t>(d), ukvw = static_cast<uint32_t>(kvw);
+    const uint32_t base_q = L.layout.Wq, base_k = L.layout.Wk - ud * ud, base_v = L.layout.Wv - (ud + ukvw) * ud;
+    const uint32_t to_k = base_k - base_v, to_q = base_q - base_k;
     auto row_offset = [=](int, int row) {
         const bool q = row < d, k = row < d + kvw;
-        const uint32_t region = q ? wq : (k ? wk : wv);
-        const uint32_t first = q ? 0u : static_cast<uint32_t>(k ? d : d + kvw);
-        return (region + (static_cast<uint32_t>(row) - first) * static_cast<uint32_t>(d)) * N::kBytes;
+        const uint32_t base = base_v + (k ? to_k : 0u) + (q ? to_q : 0u);
+        return (base + static_cast<uint32_t>(row) * ud) * N::kBytes;
     };
     const NormInput<BF16, VPL> norm(L.layer_weight(layer, L.layout.attn_norm), d);
     auto prepare = [&]() { load_hidden<BF16, hidden_slots<BF16, VPL>()>(L, d, layer, step, token, sh); };
