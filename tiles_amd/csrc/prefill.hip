@@ -22,6 +22,7 @@
 #include "prefill.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <string>
 
 #include "device_common.hpp"
@@ -109,12 +110,44 @@ __global__ void __launch_bounds__(kRowThreads) rope_rows(const uint16_t* qkv, in
         value_cache[static_cast<size_t>(pos) * nkv * dh + index] = src[(nq + nkv) * dh + index];
 }
 
+// e^x for x <= 0, bit for bit the device library's expf (verified over every non-positive float
+// on gfx950): x log2(e) as a head ph = x * c and a tail pl (the product's rounding error by FMA
+// plus x times the tail of log2(e)), then 2^(ph - rint(ph) + pl) by v_exp_f32 scaled by
+// 2^rint(ph), and 0 below ln(2^-149).  Without expf's overflow branch, which no x <= 0 takes: 3
+// of its 15 instructions.  The constants are the ones that library's code on gfx950 uses.
+__device__ __forceinline__ float exp_nonpositive(float x)
+{
+#pragma clang fp contract(off)
+    constexpr float kLog2eHead = 0x1.715476p+0f, kLog2eTail = 0x1.4ae0bep-26f, kUnderflow = -0x1.9d1da0p+6f;
+    const float ph = x * kLog2eHead;
+    float pl = fmaf(x, kLog2eHead, -ph);
+    pl = fmaf(x, kLog2eTail, pl);
+    const float e = rintf(ph);
+    const float r = __builtin_ldexpf(__builtin_amdgcn_exp2f((ph - e) + pl), static_cast<int>(e));
+    return x < kUnderflow ? 0.0f : r;
+}
+
+// a / b correctly rounded, from r = 1 / b (itself correctly rounded): q0 = a r is within an ulp of
+// a / b, the FMA residual a - b q0 is exact, and q0 + residual * r rounds to a / b (Markstein's
+// theorem) while a / b is a normal number, which for b in [1, 2^31) holds from a = kQuotientFloor
+// up (callers divide smaller a in full).  Three instructions instead of the division's eleven;
+// equal to IEEE division on 2^32 sampled pairs with b in [1, 4096) and a in [2^-30, 1], and on
+// 2^32 with a in [2^-94, 2^-30).
+constexpr float kQuotientFloor = 0x1p-94f;
+__device__ __forceinline__ float divide_by(float a, float b, float r)
+{
+#pragma clang fp contract(off)
+    const float q0 = a * r;
+    return fmaf(fmaf(-b, q0, a), r, q0);
+}
+
 // Causal attention on the matrix cores, for 64 rows (positions position + r0 ..) and every
 // query head of K/V head blockIdx.y: wave w takes rows r0 + 16 w .. + 15.  Scores are
 // computed transposed, S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A: 16 key rows, B: the 16
 // query rows of one head), so that lane l holds query l % 16 against keys 4 (l / 16) + i of each
 // 16-key subtile.  Each score is bf16(bf16(dot) * scale) (the decode worker's score_of), keys past
-// the query's position are masked.  Pass 1 keeps each lane's running maximum and exp-sum per
+// the query's position are masked (tiles past the block's first row only; rows past the chunk
+// compute finite values nobody stores).  Pass 1 keeps each lane's running maximum and exp-sum per
 // head, rescaled when the maximum grows, and merges the four lanes of a query at the end (exact
 // maximum M, FP32 S).  Pass 2 recomputes the scores, rounds P = exp(s - M) / S to bf16 in
 // registers and takes P V on the matrix cores with P as the A operand straight from the score
@@ -128,8 +161,11 @@ __global__ void __launch_bounds__(kRowThreads) rope_rows(const uint16_t* qkv, in
 constexpr int kAttnThreads = 256;
 constexpr int kAttnRows = 64;  // query positions per block: 16 per wave
 
+// Two waves per SIMD for head_dim 64 (256 registers a lane at most; unbounded, the compiler
+// took 276 and ran one); 128 needs more than 256 in either case.
 template <int DH>
-__global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* q_rot, int position, int rows, int nq, int nkv,
+__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(DH == 64 ? 2 : 1)))
+attention_tiles(const uint16_t* q_rot, int position, int rows, int nq, int nkv,
                                                                 const uint16_t* key_cache, const uint16_t* value_cache,
                                                                 float scale, uint16_t* out)
 {
@@ -158,6 +194,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
     const int last_row = min(r0 + kAttnRows, rows) - 1;
     const int last_key = position + last_row;  // the block's last key: every load stays at or below it
     const int tiles = last_key / kTile + 1;
+    const int full_tiles = (position + r0 + 1) / kTile;  // tiles every row of the block sees whole
     const int qrow = r0 + 16 * wave + col;     // this lane's query row (B operand, output column)
     const int qpos = position + qrow;
 
@@ -213,7 +250,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
         return out;
     };
     // Scores of subtile j of the staged tile kt for every head: s[g][i] at key 64 kt + 16 j + 4 g4 + i.
-    auto scores = [&](int kt, int j, float (&s)[kMaxGroup][4]) {
+    auto scores = [&](auto masked, int kt, int j, float (&s)[kMaxGroup][4]) {
         u32x4 ka[KS];
 #pragma unroll
         for (int k = 0; k < KS; ++k)
@@ -226,8 +263,13 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
                 acc = mfma_16x16x32_bf16(ka[k], qb[g][k], acc);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int t = kt * kTile + 16 * j + 4 * g4 + i;
-                s[g][i] = t <= qpos && qrow < rows ? Bf::round(Bf::round(acc[i]) * scale) : -INFINITY;
+                // With head_dim 64 the scale is 2^-3: the product of a bf16 value and it is a bf16
+                // value already (short of the subnormal range), so the second rounding is the identity.
+                const float score = DH == 64 ? Bf::round(acc[i]) * 0.125f : Bf::round(Bf::round(acc[i]) * scale);
+                if constexpr (decltype(masked)::value)
+                    s[g][i] = kt * kTile + 16 * j + 4 * g4 + i <= qpos ? score : -INFINITY;
+                else
+                    s[g][i] = score;
             }
         }
     };
@@ -240,8 +282,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
         total[g] = 0.0f;
     }
     u32x4 kr[kLoads], vr[kLoads];
-    load_rows(key_cache, 0, kr);
-    for (int kt = 0; kt < tiles; ++kt) {
+    auto pass1_tile = [&](auto masked, int kt) {
         __syncthreads();  // the previous tile's K reads are done
         stage_k(kr);
         load_rows(key_cache, kt + 1, kr);  // the next tile (clamped past the last) in flight
@@ -249,21 +290,32 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float s[kMaxGroup][4];
-            scores(kt, j, s);
+            scores(masked, kt, j, s);
 #pragma unroll
             for (int g = 0; g < kMaxGroup; ++g) {
                 const float grown = fmaxf(m[g], fmaxf(fmaxf(s[g][0], s[g][1]), fmaxf(s[g][2], s[g][3])));
-                if (grown == -INFINITY)
-                    continue;  // every key so far masked
-                float sum = total[g] * expf(m[g] - grown);
+                if constexpr (decltype(masked)::value)
+                    if (grown == -INFINITY)
+                        continue;  // every key so far masked
+                // Rescaled by exp(m - grown) (0 for the first subtile's m = -inf), which is exactly 1
+                // where the maximum held: skipped when it held in every lane of the wave.
+                float sum = total[g];
+                if (__builtin_amdgcn_ballot_w64(grown != m[g]) != 0)
+                    sum *= exp_nonpositive(m[g] - grown);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    sum += expf(s[g][i] - grown);
+                    sum += exp_nonpositive(s[g][i] - grown);
                 total[g] = sum;
                 m[g] = grown;
             }
         }
-    }
+    };
+    load_rows(key_cache, 0, kr);
+    int kt = 0;
+    for (; kt < full_tiles; ++kt)
+        pass1_tile(std::false_type{}, kt);
+    for (; kt < tiles; ++kt)
+        pass1_tile(std::true_type{}, kt);
     // The four lanes of a query (lane groups g4 = 0..3) merge: M exact, S rescaled to it.
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g)
@@ -272,10 +324,14 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
             const float om = __shfl_xor(m[g], offset), ot = __shfl_xor(total[g], offset);
             const float grown = fmaxf(m[g], om);
             if (grown != -INFINITY) {
-                total[g] = total[g] * expf(m[g] - grown) + ot * expf(om - grown);
+                total[g] = total[g] * exp_nonpositive(m[g] - grown) + ot * exp_nonpositive(om - grown);
                 m[g] = grown;
             }
         }
+    float inverse[kMaxGroup];  // 1 / S, correctly rounded
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g)
+        inverse[g] = 1.0f / total[g];
 
     // Pass 2: P = bf16(exp(s - M) / S) as A operands, P V against the staged V rows.
     f32x4 o[kMaxGroup][NT];
@@ -284,9 +340,7 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
 #pragma unroll
         for (int n = 0; n < NT; ++n)
             o[g][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    load_rows(key_cache, 0, kr);
-    load_rows(value_cache, 0, vr);
-    for (int kt = 0; kt < tiles; ++kt) {
+    auto pass2_tile = [&](auto masked, int kt) {
         __syncthreads();  // the previous tile's K and V reads are done
         stage_k(kr);
         stage_v(vr);
@@ -296,8 +350,8 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
 #pragma unroll
         for (int step = 0; step < 2; ++step) {  // keys 32 step .. + 31 of the tile
             float s0[kMaxGroup][4], s1[kMaxGroup][4];
-            scores(kt, 2 * step, s0);
-            scores(kt, 2 * step + 1, s1);
+            scores(masked, kt, 2 * step, s0);
+            scores(masked, kt, 2 * step + 1, s1);
             u32x4 vb[NT];
 #pragma unroll
             for (int n = 0; n < NT; ++n)
@@ -306,19 +360,37 @@ __global__ void __launch_bounds__(kAttnThreads) attention_tiles(const uint16_t* 
             for (int g = 0; g < kMaxGroup; ++g) {
                 if (g >= group)
                     continue;
-                float p[8];
+                float p[8];  // exp(s - M), masked keys exp(-inf) = 0; then P
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    p[i] = s0[g][i] == -INFINITY ? 0.0f : Bf::round(expf(s0[g][i] - m[g]) / total[g]);
-                    p[4 + i] = s1[g][i] == -INFINITY ? 0.0f : Bf::round(expf(s1[g][i] - m[g]) / total[g]);
+                    p[i] = exp_nonpositive(s0[g][i] - m[g]);
+                    p[4 + i] = exp_nonpositive(s1[g][i] - m[g]);
                 }
-                const u32x4 pa = {pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
+                const float least = fminf(fminf(fminf(p[0], p[1]), fminf(p[2], p[3])), fminf(fminf(p[4], p[5]), fminf(p[6], p[7])));
+                if (__builtin_expect(least >= kQuotientFloor, 1)) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        p[i] = divide_by(p[i], total[g], inverse[g]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        p[i] = p[i] / total[g];
+                }
+                // Rounded to bf16 in pairs (v_cvt_pk_bf16_f32).
+                auto pair = [](float lo, float hi) { return __builtin_bit_cast(uint32_t, bf16x2{static_cast<__bf16>(lo), static_cast<__bf16>(hi)}); };
+                const u32x4 pa = {pair(p[0], p[1]), pair(p[2], p[3]), pair(p[4], p[5]), pair(p[6], p[7])};
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
                     o[g][n] = mfma_16x16x32_bf16(pa, vb[n], o[g][n]);
             }
         }
-    }
+    };
+    load_rows(key_cache, 0, kr);
+    load_rows(value_cache, 0, vr);
+    for (kt = 0; kt < full_tiles; ++kt)
+        pass2_tile(std::false_type{}, kt);
+    for (; kt < tiles; ++kt)
+        pass2_tile(std::true_type{}, kt);
     // o[g][n]: lane l holds query rows r0 + 16 wave + 4 g4 + i, dim 16 n + col.
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g)

@@ -957,8 +957,9 @@ __device__ __forceinline__ void op_qkv(const Launch<BF16>& L, const ti_task_reco
     // Rows may span Wq, Wk and Wv, which are separate regions of the layer's weights: row r of
     // a region that starts at row `first` lies at region + (r - first) d = base + r d, with base
     // = region - first d (mod 2^32).  The base is the V region's plus differences selected
-    // against zero: a select among the captured bases became an indexed load from a copy of
-    // them in scratch memory, and a select of the launch record's fields branches around loads.
+    // against zero: a select among the captured bases became an indexed load from a per-thread
+    // copy of them (20 bytes a thread, which the compiler placed in LDS, or in scratch memory
+    // once LDS was short), and a select of the launch record's fields branches around loads.
     const uint32_t ud = static_cast<uint32_t>(d), ukvw = static_cast<uint32_t>(kvw);
     const uint32_t base_q = L.layout.Wq, base_k = L.layout.Wk - ud * ud, base_v = L.layout.Wv - (ud + ukvw) * ud;
     const uint32_t to_k = base_k - base_v, to_q = base_q - base_k;
