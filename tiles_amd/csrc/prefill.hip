@@ -621,10 +621,16 @@ int MatrixPrefill::layer(hipStream_t stream, void* kv, int layer, int position, 
     };
 
     hipLaunchKernelGGL(rms_rows, dim3(rows), dim3(kRowThreads), 0, stream, v.x, base + w.attn_norm, d, eps, v.u);
-    if (!gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wq, qw, v.qkv, qkvw)) ||
-        !gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wk, kvw, v.qkv + qw, qkvw)) ||
-        !gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wv, kvw, v.qkv + qw + kvw, qkvw)))
+    // Wq, Wk and Wv are consecutive in the package's layer layout (plan.cpp checks the regions):
+    // one GEMM over their rows, which also fills the chip (Wk and Wv alone are 4 column tiles).
+    if (w.Wk == w.Wq + static_cast<uint32_t>(qw) * d && w.Wv == w.Wk + static_cast<uint32_t>(kvw) * d) {
+        if (!gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wq, qkvw, v.qkv, qkvw)))
+            return code;
+    } else if (!gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wq, qw, v.qkv, qkvw)) ||
+               !gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wk, kvw, v.qkv + qw, qkvw)) ||
+               !gemm_ok(gemm(stream, true, v.u, rows, d, base + w.Wv, kvw, v.qkv + qw + kvw, qkvw))) {
         return code;
+    }
     hipLaunchKernelGGL(rope_rows, dim3(rows), dim3(kRowThreads), 0, stream, v.qkv, position, p_.rotary_frequencies, nq, nkv, dh,
                        v.q, cache + w.key, cache + w.value);
     const float scale = 1.0f / sqrtf(static_cast<float>(dh));
