@@ -377,17 +377,20 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
     issue_reads();
     issue_fence();
     overlap();
-    const bool all_present = block_sync_and(sh, check());
+    // Each wave re-reads its own missing words until it has them all, and the block meets once
+    // at the end: a barrier in every round made each wave's next read wait for the slowest wave's
+    // last one (a probe of 256 blocks exchanging a 1024-word vector: 2.03 against 2.38 us a round).
+    bool mine = check();
     if (tid() == 0 && sh.mark_read == 0)
         sh.mark_read = __builtin_amdgcn_s_memrealtime();
-    if (!all_present) {
-        uint32_t spins = 0;
-        while (!block_sync_and(sh, read_missing()) && !sh.aborted) {
-            __builtin_amdgcn_s_sleep(2);
-            if (tid() == 0)
-                stuck(exchange, xl, ++spins, sh);
-        }
+    uint32_t spins = 0;
+    while (!__all(mine) && !sh.aborted) {
+        __builtin_amdgcn_s_sleep(1);
+        if ((tid() & 63) == 0)
+            stuck(exchange, xl, ++spins, sh);
+        mine = read_missing();
     }
+    block_sync(sh);
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
         const int index = k * kThreads + static_cast<int>(tid());
