@@ -1490,9 +1490,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 w = coherent_load64(stats + j);
             bool have = !wanted || static_cast<uint32_t>(w >> 32) == stat_epoch;
             uint32_t spins = 0;
-            while (!block_sync_and(sh, have) && !sh.aborted) {
-                __builtin_amdgcn_s_sleep(2);
-                if (tid() == 0)
+            while (!__all(have) && !sh.aborted) {  // per wave, the block meets after the loop
+                __builtin_amdgcn_s_sleep(1);
+                if ((tid() & 63) == 0)
                     stuck(L.exchange, L.xl, ++spins, sh);
                 if (!have) {
                     w = coherent_load64(stats + j);
@@ -1719,9 +1719,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             w = coherent_load64(word);
         bool have = !wanted || static_cast<uint32_t>(w >> 32) == part_epoch;
         uint32_t spins = 0;
-        while (!block_sync_and(sh, have) && !sh.aborted) {
+        while (!__all(have) && !sh.aborted) {  // per wave, the block meets after the loop
             __builtin_amdgcn_s_sleep(1);
-            if (tid() == 0)
+            if ((tid() & 63) == 0)
                 stuck(L.exchange, L.xl, ++spins, sh);
             if (!have) {
                 w = coherent_load64(word);
