@@ -43,3 +43,15 @@ def test_spawn_order_effect_is_separated_from_the_difference():
     effect = C.spawn_order_effect(a, b, 3)
     assert abs(effect["first_half_mean_us"] - 1.6) < 1e-9 and abs(effect["second_half_mean_us"] - 0.4) < 1e-9
     assert abs(effect["spawn_order_effect_us"] - 0.6) < 1e-9
+
+
+def test_outlier_exclusion_never_empties_a_block():
+    """Rounds further than OUTLIER_FRACTION from the arm's median are dropped, but a block with no
+    round inside keeps them all: its median stays finite, and so does the paired comparison (a tiny
+    package at 45 us/token put a whole 2-round block outside a 1% band)."""
+    blocks = [[100.0, 100.2], [103.0, 104.0], [99.9, 150.0]]
+    kept = C.kept_rounds(blocks, 100.0)
+    assert kept == [[100.0, 100.2], [103.0, 104.0], [99.9]]
+    medians = [float(np.median(k)) for k in kept]
+    result = C.paired(medians, [m + 1.0 for m in medians], seed=0)
+    assert np.isfinite(result["mean_us"]) and all(np.isfinite(result["ci95_us"]))

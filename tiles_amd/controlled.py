@@ -15,7 +15,8 @@ power, clocks and temperatures, joined to every block by time.
 Every arm is compared with the first through paired block differences: block i of two arms ran
 next to each other in time, and a bootstrap over the pairs gives the 95% interval of the mean
 difference.  Two arms of one package (an A/A run) measure the protocol's own resolution.  Rounds
-further than OUTLIER_FRACTION from their arm's median at one context are excluded and counted.
+further than OUTLIER_FRACTION from their arm's median at one context are excluded and counted
+(a block none of whose rounds lies inside keeps them all).
 
 Server placement biases a comparison: in an A/A run on MI355X the server started first was
 0.4-0.8% faster than the second, steadily (each process uploads its own weights and buffers).
@@ -199,6 +200,13 @@ def paired(reference: list[float], other: list[float], seed: int) -> dict:
             "ci95_percent": [100 * float(low) / base, 100 * float(high) / base], "pairs": len(d)}
 
 
+def kept_rounds(blocks: list[list[float]], median: float) -> list[list[float]]:
+    """Each block's rounds within OUTLIER_FRACTION of the arm's median at the context; a block
+    with none inside keeps all of its rounds, so that every block has a median to pair."""
+    kept = [[t for t in block if abs(t - median) <= OUTLIER_FRACTION * median] for block in blocks]
+    return [k if k else list(block) for k, block in zip(kept, blocks)]
+
+
 def spawn_order_effect(reference: list[float], other: list[float], half: int) -> dict:
     """The paired means of the blocks before and after the servers were restarted in the reverse
     order (block `half` on), and half their difference: the placement effect that the mean over
@@ -258,9 +266,9 @@ def main() -> int:
             for name in names:
                 every = [t for block in raw[name] for t in block]
                 median = statistics.median(every)
-                kept = [[t for t in block if abs(t - median) <= OUTLIER_FRACTION * median] for block in raw[name]]
+                kept = kept_rounds(raw[name], median)
                 summary[name] = {"median_us": median, "excluded_rounds": sum(len(x) for x in raw[name]) - sum(len(k) for k in kept),
-                                 "block_medians_us": [statistics.median(k) if k else float("nan") for k in kept]}
+                                 "block_medians_us": [statistics.median(k) for k in kept]}
             reference = names[0]
             half = a.blocks // 2
             for name in names[1:]:
