@@ -297,13 +297,17 @@ attention_tiles(const uint16_t* q_rot, int position, int rows, int nq, int nkv,
                 if constexpr (decltype(masked)::value)
                     if (grown == -INFINITY)
                         continue;  // every key so far masked
-                // Rescaled by exp(m - grown) (0 for the first subtile's m = -inf), which is exactly 1
-                // where the maximum held: skipped when it held in every lane of the wave.
-                float sum = total[g];
+                // total exp(m - grown) + e_0 + ... + e_3, the first two terms as one FMA; the factor
+                // (0 for the first subtile's m = -inf) is exactly 1 where the maximum held, and is
+                // skipped when it held in every lane of the wave.
+                const float first = exp_nonpositive(s[g][0] - grown);
+                float sum;
                 if (__builtin_amdgcn_ballot_w64(grown != m[g]) != 0)
-                    sum *= exp_nonpositive(m[g] - grown);
+                    sum = fmaf(total[g], exp_nonpositive(m[g] - grown), first);
+                else
+                    sum = total[g] + first;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 1; i < 4; ++i)
                     sum += exp_nonpositive(s[g][i] - grown);
                 total[g] = sum;
                 m[g] = grown;
