@@ -110,37 +110,6 @@ __global__ void __launch_bounds__(kRowThreads) rope_rows(const uint16_t* qkv, in
         value_cache[static_cast<size_t>(pos) * nkv * dh + index] = src[(nq + nkv) * dh + index];
 }
 
-// e^x for x <= 0, bit for bit the device library's expf (verified over every non-positive float
-// on gfx950): x log2(e) as a head ph = x * c and a tail pl (the product's rounding error by FMA
-// plus x times the tail of log2(e)), then 2^(ph - rint(ph) + pl) by v_exp_f32 scaled by
-// 2^rint(ph), and 0 below ln(2^-149).  Without expf's overflow branch, which no x <= 0 takes: 3
-// of its 15 instructions.  The constants are the ones that library's code on gfx950 uses.
-__device__ __forceinline__ float exp_nonpositive(float x)
-{
-#pragma clang fp contract(off)
-    constexpr float kLog2eHead = 0x1.715476p+0f, kLog2eTail = 0x1.4ae0bep-26f, kUnderflow = -0x1.9d1da0p+6f;
-    const float ph = x * kLog2eHead;
-    float pl = fmaf(x, kLog2eHead, -ph);
-    pl = fmaf(x, kLog2eTail, pl);
-    const float e = rintf(ph);
-    const float r = __builtin_ldexpf(__builtin_amdgcn_exp2f((ph - e) + pl), static_cast<int>(e));
-    return x < kUnderflow ? 0.0f : r;
-}
-
-// a / b correctly rounded, from r = 1 / b (itself correctly rounded): q0 = a r is within an ulp of
-// a / b, the FMA residual a - b q0 is exact, and q0 + residual * r rounds to a / b (Markstein's
-// theorem) while a / b is a normal number, which for b in [1, 2^31) holds from a = kQuotientFloor
-// up (callers divide smaller a in full).  Three instructions instead of the division's eleven;
-// equal to IEEE division on 2^32 sampled pairs with b in [1, 4096) and a in [2^-30, 1], and on
-// 2^32 with a in [2^-94, 2^-30).
-constexpr float kQuotientFloor = 0x1p-94f;
-__device__ __forceinline__ float divide_by(float a, float b, float r)
-{
-#pragma clang fp contract(off)
-    const float q0 = a * r;
-    return fmaf(fmaf(-b, q0, a), r, q0);
-}
-
 // Causal attention on the matrix cores, for 64 rows (positions position + r0 ..) and every
 // query head of K/V head blockIdx.y: wave w takes rows r0 + 16 w .. + 15.  Scores are
 // computed transposed, S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A: 16 key rows, B: the 16
