@@ -334,7 +334,7 @@ struct NoOverlap {
     __device__ void operator()() const {}
 };
 
-template <bool kHalves, int kMaxCount = kLdsHidden, typename Sink, typename Overlap = NoOverlap>
+template <bool kHalves, int kMaxCount = kLdsHidden, bool kMeet = true, typename Sink, typename Overlap = NoOverlap>
 __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
                                           const ExchangeLayout& xl, Shared& sh, Sink sink, Overlap overlap = {})
 {
@@ -378,8 +378,9 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
     issue_fence();
     overlap();
     // Each wave re-reads its own missing words until it has them all, and the block meets once
-    // at the end: a barrier in every round made each wave's next read wait for the slowest wave's
-    // last one (a probe of 256 blocks exchanging a 1024-word vector: 2.03 against 2.38 us a round).
+    // at the end (kMeet; without it, the caller's barrier after the sink is the meeting): a
+    // barrier in every round made each wave's next read wait for the slowest wave's last one (a
+    // probe of 256 blocks exchanging a 1024-word vector: 2.03 against 2.38 us a round).
     bool mine = check();
     if (tid() == 0 && sh.mark_read == 0)
         sh.mark_read = __builtin_amdgcn_s_memrealtime();
@@ -390,7 +391,8 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int count, int s
             stuck(exchange, xl, ++spins, sh);
         mine = read_missing();
     }
-    block_sync(sh);
+    if constexpr (kMeet)
+        block_sync(sh);
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
         const int index = k * kThreads + static_cast<int>(tid());
@@ -419,7 +421,7 @@ template <bool BF16, typename Sink>
 __device__ __forceinline__ void poll_input(const uint64_t* src, int count, int stride, uint32_t epoch, uint64_t* exchange,
                                           const ExchangeLayout& xl, Shared& sh, Sink sink)
 {
-    poll_words<BF16>(src, count, stride, epoch, exchange, xl, sh, sink);
+    poll_words<BF16, kLdsHidden, false>(src, count, stride, epoch, exchange, xl, sh, sink);
     block_sync(sh);
 }
 
@@ -628,7 +630,7 @@ __device__ __forceinline__ void load_hidden(const Launch<BF16>& L, int d, int la
             }
         }
     } else {
-        poll_words<BF16>(L.exchange + L.xl.hidden(layer % 2), d, L.hidden_stride, L.epoch_of(step, layer - 1, kPhaseY),
+        poll_words<BF16, kLdsHidden, false>(L.exchange + L.xl.hidden(layer % 2), d, L.hidden_stride, L.epoch_of(step, layer - 1, kPhaseY),
                          L.exchange, L.xl, sh, [&](int i, uint32_t p) {
                              const float x = Num<BF16>::from_payload(p);
                              sh.xsave[i] = x;
@@ -2018,7 +2020,7 @@ __device__ __forceinline__ void op_down(const Launch<BF16>& L, const ti_task_rec
     // rows found the slowest FFN chunks' products missing when it came back, and a second round
     // followed the rows' arrival.
     wait_vmem<kLoads / 2>();
-    poll_words<BF16, max_product<BF16>()>(L.exchange + L.xl.product, f, 1, L.epoch_of(step, layer, kPhaseFfn), L.exchange,
+    poll_words<BF16, max_product<BF16>(), false>(L.exchange + L.xl.product, f, 1, L.epoch_of(step, layer, kPhaseFfn), L.exchange,
                                          L.xl, sh, [&](int i, uint32_t payload) {
                                              if constexpr (BF16)
                                                  p_bits[i] = static_cast<uint16_t>(payload);
