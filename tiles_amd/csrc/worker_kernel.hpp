@@ -283,40 +283,6 @@ __device__ inline bool word_present(uint64_t w, uint32_t want)
         return static_cast<uint32_t>(w >> 32) == want;
 }
 
-// Wave 0 alone: waits until one "witness" word every `stride` words of src[0, count) carries
-// `want` (8 loads in flight per lane, a back-off between rounds).
-template <bool kHalves>
-__device__ inline void wait_witness_words(const uint64_t* src, int count, int stride, uint32_t want, uint64_t* exchange,
-                                          const ExchangeLayout& xl, Shared& sh)
-{
-    constexpr int kWitnessBatch = 8;
-    const int lane = tid() & 63;
-    const int witnesses = (count + stride - 1) / stride;
-    uint32_t spins = 0;
-    while (true) {
-        bool mine = true;
-        // Witness j is word j * stride; lanes past the last witness check the last word.
-        for (int j0 = 0; j0 <= witnesses; j0 += 64 * kWitnessBatch) {
-            uint64_t v[kWitnessBatch];
-#pragma unroll
-            for (int u = 0; u < kWitnessBatch; ++u) {
-                const int j = j0 + u * 64 + lane;
-                v[u] = coherent_load64(src + (j < witnesses ? j * stride : count - 1));
-            }
-#pragma unroll
-            for (int u = 0; u < kWitnessBatch; ++u)
-                mine &= word_present<kHalves>(v[u], want);
-        }
-        if (__all(mine))
-            break;
-        __builtin_amdgcn_s_sleep(2);
-        if (lane == 0)
-            stuck(exchange, xl, ++spins, sh);
-        if (__any(sh.aborted))
-            break;
-    }
-}
-
 // Reads `count` (at most kMaxCount) exchange elements from `src` until each carries `epoch`
 // and hands each payload to `sink(index, payload)`: one element per word, or with kHalves two
 // tagged bf16 elements per word (exchange_tag; `count` even).  Block-wide: every thread must
@@ -425,9 +391,9 @@ __device__ __forceinline__ void poll_input(const uint64_t* src, int count, int s
     block_sync(sh);
 }
 
-// A vector exchange read by the calling wave alone (poll_words's optimistic read, witness wait
-// and re-read, with up to kMaxElements elements), into `sink`; the caller meets the other waves
-// at a barrier afterwards.  Its loads return only after every load the wave issued before them,
+// A vector exchange read by the calling wave alone (poll_words's optimistic read and re-reads of
+// the missing words, with up to kMaxElements elements), into `sink`; the caller meets the other
+// waves at a barrier afterwards.  Its loads return only after every load the wave issued before them,
 // so a wave that polls this way keeps few loads of its own in flight.
 template <bool BF16, int kMaxElements, typename Sink>
 __device__ __forceinline__ void poll_words_one_wave(const uint64_t* src, int count, int stride, uint32_t epoch,
@@ -441,7 +407,7 @@ __device__ __forceinline__ void poll_words_one_wave(const uint64_t* src, int cou
     inject_delay(__LINE__);
     const int lane = static_cast<int>(tid() & 63);
     const int words = kHalves ? count / 2 : count;
-    const int stride_words = kHalves ? (stride > 1 ? stride / 2 : 1) : stride;
+    (void)stride;
     const uint32_t want = kHalves ? exchange_tag(epoch) : epoch;
     for (int w0 = 0; w0 < words; w0 += 64 * kBatch) {
         uint64_t w[kBatch];
@@ -461,17 +427,30 @@ __device__ __forceinline__ void poll_words_one_wave(const uint64_t* src, int cou
                 ok &= word_present<kHalves>(w[k], want);
             return ok;
         };
-        const bool all_present = __all(read());
+        // Later rounds re-read only the missing words, at once (a witness word per producer
+        // first, then every word again, cost a round trip more once the data was there).
+        auto read_missing = [&]() {
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int index = w0 + k * 64 + lane;
+                if (w0 + k * 64 < words && !word_present<kHalves>(w[k], want))
+                    w[k] = coherent_load64(src + (index < words ? index : words - 1));
+            }
+            bool ok = true;
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k)
+                ok &= word_present<kHalves>(w[k], want);
+            return ok;
+        };
+        bool mine = read();
         if (lane == 0 && sh.mark_read == 0)
             sh.mark_read = __builtin_amdgcn_s_memrealtime();
-        if (!all_present) {
-            wait_witness_words<kHalves>(src, words, stride_words, want, exchange, xl, sh);
-            uint32_t spins = 0;
-            while (!__all(read()) && !sh.aborted) {
-                __builtin_amdgcn_s_sleep(2);
-                if (lane == 0)
-                    stuck(exchange, xl, ++spins, sh);
-            }
+        uint32_t spins = 0;
+        while (!__all(mine) && !sh.aborted) {
+            __builtin_amdgcn_s_sleep(1);
+            if (lane == 0)
+                stuck(exchange, xl, ++spins, sh);
+            mine = read_missing();
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
