@@ -1113,6 +1113,22 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 sh.rope_cs[half + pair] = N::round(sinf(angle));
             }
     };
+    // Matrix path: the first block's cached V rows go to LDS, as stored, while the first read is
+    // in flight too (the current position's row, loaded as zeros, is written once it arrives).
+    // V rows past the chunk's last 32-position step are never read: P V stops there.
+    const int live0 = min(kBlockTiles, 2 * ((min(span, PB) + 31) / 32));
+    auto stage_v = [&]() {
+        if constexpr (kMfma) {
+#pragma unroll
+            for (int j = 0; j < TW; ++j)
+                if (wave + j * kWaves < live0) {
+                    const int row = (wave + j * kWaves) * kTile + tr;
+#pragma unroll
+                    for (int k = 0; k < KS; ++k)
+                        *reinterpret_cast<u32x4*>(sh.vt + row * kVRow + 32 * k + 8 * tk) = vfirst[j][k];
+                }
+        }
+    };
 
     // This token's Q heads, K and V of the head group: one packed exchange block.  With
     // head_dim <= 64, thread t polls element t and finds its RoPE partner (element t +- dh / 2)
@@ -1135,7 +1151,10 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                        held = v;  // i == tid(): block <= kThreads
                    else if (i < qk)
                        sh.region[i] = v;
-               }, rope_table);
+               }, [&]() {
+                   rope_table();
+                   stage_v();
+               });
     if (tid() == 0)
         sh.rope_position = position;
     // Chunk 0 stores the rotated K row into the cache and the rotated Q heads into scratch.  Every
@@ -1286,12 +1305,16 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
                 if ((tile0 + gi * kWaves) * kTile < span)
                     tile_scores(tile0 + gi * kWaves, kb[gi]);
         }
-        // V rows past the chunk's last 32-position step are never read: P V stops there.
-        const int live0 = min(kBlockTiles, 2 * ((min(span, PB) + 31) / 32));
+        // The current position's V row, where it lies in the first block (staged during the poll).
 #pragma unroll
-        for (int j = 0; j < TW; ++j)
-            if (wave + j * kWaves < live0)
-                write_v(0, j, vfirst[j]);
+        for (int j = 0; j < TW; ++j) {
+            const int tile = wave + j * kWaves;
+            if (tile < live0 && begin + tile * kTile + tr == position)
+#pragma unroll
+                for (int k = 0; k < KS; ++k)
+                    *reinterpret_cast<u32x4*>(vt + (tile * kTile + tr) * kVRow + 32 * k + 8 * tk) =
+                        *reinterpret_cast<const u32x4*>(sh.vcur_bits + 32 * k + 8 * tk);
+        }
     } else {
         // Scores of rows [begin, end).  Every lane holds its slice of all MG query heads (heads
         // past the group compute values that are never stored) and of the current K row.
