@@ -1390,27 +1390,32 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const bool packed_p = kMfma && (p_offset + (group * span_pad + 1) / 2 + 3 + stat_floats) <= kLdsRegionFloats;
     uint16_t* pbits = reinterpret_cast<uint16_t*>(scores + p_offset);  // [group][span_pad]
     auto put_p = [&](int g, int i, float v) { pbits[g * span_pad + i] = static_cast<uint16_t>(__float_as_uint(v) >> 16); };
-    if (wave < group && packed_p && span_pad <= 3 * 64) {
-        // At most one V block: the wave's scores stay in registers (3 per lane), read once.
+    // Chunks of at most 4 x 64 positions: the wave's scores stay in registers (R per lane), read
+    // once; sums in the same order as the loop below.
+    auto register_softmax = [&](auto count) {
+        constexpr int R = decltype(count)::value;
         const float* row = scores + wave * span;
-        float v[3], e[3];
+        float v[R], e[R];
 #pragma unroll
-        for (int k = 0; k < 3; ++k) {
+        for (int k = 0; k < R; ++k) {
             const int i = lane + 64 * k;
             v[k] = i < span ? row[i] : -INFINITY;
         }
-        float m = fmaxf(fmaxf(v[0], v[1]), v[2]);
+        float m = v[0];
+#pragma unroll
+        for (int k = 1; k < R; ++k)
+            m = fmaxf(m, v[k]);
         m = lane_value(group_max(m, 64), 63);
         float sum = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 3; ++k) {
+        for (int k = 0; k < R; ++k) {
             e[k] = lane + 64 * k < span ? expf(v[k] - m) : 0.0f;
             sum += e[k];
         }
         sum = lane_value(group_sum<64>(sum), 63);
         if (fused)
 #pragma unroll
-            for (int k = 0; k < 3; ++k) {
+            for (int k = 0; k < R; ++k) {
                 const int i = lane + 64 * k;
                 if (i < span_pad)
                     put_p(wave, i, N::round(e[k] / sum));  // 0 past the span
@@ -1419,6 +1424,11 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             stat_max[wave] = m;
             stat_sum[wave] = sum;
         }
+    };
+    if (wave < group && packed_p && span_pad <= 3 * 64) {
+        register_softmax(std::integral_constant<int, 3>{});  // one V block
+    } else if (wave < group && packed_p && span <= 4 * 64) {
+        register_softmax(std::integral_constant<int, 4>{});  // P V reads P up to the span's last 32-step
     } else if (wave < group) {
         // Longer chunks: unrolled, so that several LDS reads are in flight.
         float* row = scores + wave * span;
