@@ -1390,7 +1390,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     const bool packed_p = kMfma && (p_offset + (group * span_pad + 1) / 2 + 3 + stat_floats) <= kLdsRegionFloats;
     uint16_t* pbits = reinterpret_cast<uint16_t*>(scores + p_offset);  // [group][span_pad]
     auto put_p = [&](int g, int i, float v) { pbits[g * span_pad + i] = static_cast<uint16_t>(__float_as_uint(v) >> 16); };
-    // Chunks of at most 4 x 64 positions: the wave's scores stay in registers (R per lane), read
+    // Chunks of at most 6 x 64 positions: the wave's scores stay in registers (R per lane), read
     // once; sums in the same order as the loop below.
     auto register_softmax = [&](auto count) {
         constexpr int R = decltype(count)::value;
@@ -1429,6 +1429,8 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         register_softmax(std::integral_constant<int, 3>{});  // one V block
     } else if (wave < group && packed_p && span <= 4 * 64) {
         register_softmax(std::integral_constant<int, 4>{});  // P V reads P up to the span's last 32-step
+    } else if (wave < group && packed_p && span <= 6 * 64) {
+        register_softmax(std::integral_constant<int, 6>{});
     } else if (wave < group) {
         // Longer chunks: unrolled, so that several LDS reads are in flight.
         float* row = scores + wave * span;
