@@ -170,6 +170,7 @@ def check_bf16_logits(got, want, exact, floor=2e-2):
     (64, 130, 130, 130),   # a second tile for waves 0 and 1 (ten tiles in one block)
     (64, 160, 160, 300),   # two chunks of 150 positions
     (64, 256, 256, 250),   # one fused chunk over two V^T blocks and three rounds of score tiles
+    (64, 384, 384, 380),   # one fused chunk of up to 380 positions: softmax with 3, 4 and 6 scores per lane
     (32, 160, 160, 160),   # one slice per head; a fused chunk ending on a block boundary
     (128, 128, 128, 120),  # 64-position V^T blocks: two in one chunk
     (128, 64, 64, 200),    # 128 dims over four 50-position chunks
@@ -178,7 +179,7 @@ def check_bf16_logits(got, want, exact, floor=2e-2):
 ])
 def test_bf16_matrix_attention(target, tmp, head_dim, chunk_steps, fused_steps, context):
     """bf16 heads of 32-128 dims (the matrix-core attention) against the oracle: fused chunks of
-    up to 256 positions and split chunks, logits within the calibrated bf16 bound and the same
+    up to 384 positions and split chunks, logits within the calibrated bf16 bound and the same
     greedy token."""
     block = P.BlockSpec(hidden_size=4 * head_dim, intermediate_size=512, num_attention_heads=4, num_key_value_heads=1,
                         head_dim=head_dim, max_context=max(320, context + 8))
