@@ -1537,15 +1537,32 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
             for (int c = lane; c < chunks; c += 64)
                 part = fmaf(all_stats[c * 2 * group + 2 * g + 1], expf(all_stats[c * 2 * group + 2 * g] - m), part);
             const float total = lane_value(group_sum<64>(part), 63);
-            // The same wave rounds its head's probabilities with the merged statistics.
+            // The same wave rounds its head's probabilities with the merged statistics: into the
+            // packed P V operands only (up to three per lane read at once), or back into the
+            // scores, which P V then reads.
             float* row = scores + g * span;
+            if (packed_p && span_pad <= 3 * 64) {
+                float v[3];
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    const int i = lane + 64 * k;
+                    v[k] = i < span ? row[i] : 0.0f;
+                }
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    const int i = lane + 64 * k;
+                    if (i < span_pad)
+                        put_p(g, i, i < span ? N::round(expf(v[k] - m) / total) : 0.0f);
+                }
+            } else {
 #pragma unroll 4
-            for (int i = lane; i < (packed_p ? span_pad : span); i += 64) {
-                const float p = i < span ? N::round(expf(row[i] - m) / total) : 0.0f;
-                if (i < span)
-                    row[i] = p;
-                if (packed_p)
-                    put_p(g, i, p);
+                for (int i = lane; i < (packed_p ? span_pad : span); i += 64) {
+                    const float p = i < span ? N::round(expf(row[i] - m) / total) : 0.0f;
+                    if (i < span && !packed_p)
+                        row[i] = p;
+                    if (packed_p)
+                        put_p(g, i, p);
+                }
             }
         }
         block_sync(sh);
