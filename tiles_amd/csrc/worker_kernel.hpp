@@ -168,12 +168,13 @@ constexpr int hidden_slots()
 
 // bf16 elements of the attention's staged V block: one row of (head_dim + 8) per position.  It
 // shares LDS with the input vector.  A block holds the most positions (a multiple of 32, at most
-// 192) whose rows fit: 192 for 64-dim heads.
-constexpr int kVtElements = 192 * (64 + 8) > kLdsHidden * 3 ? 192 * (64 + 8) : kLdsHidden * 3;
+// 256) whose rows fit: 256 for 64-dim heads, as many as the K tiles issued before the input wait,
+// so that a fused chunk of up to 256 positions stages one block.
+constexpr int kVtElements = 256 * (64 + 8) > kLdsHidden * 3 ? 256 * (64 + 8) : kLdsHidden * 3;
 constexpr int kMaxThreadsPadded = kThreads;  // floats of a split chunk's own partial in the work region
 constexpr int vt_block_positions(int dh)
 {
-    int positions = 192;
+    int positions = 256;
     while (positions > 32 && positions * (dh + 8) > kVtElements)
         positions -= 32;
     return positions;
@@ -1381,9 +1382,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     float* stat_sum = sh.small + kMaxGroup;
     const bool fused = chunks == 1;
     // Matrix path: the rounded probabilities also go to LDS as the bf16 operands of P V, each
-    // head's positions contiguous and zero up to whole V blocks, so that one 16-byte read is a
-    // lane's 8 positions.  Chunks too long for the work region pack them from the FP32 values.
-    const int span_pad = (span + PB - 1) / PB * PB;
+    // head's positions contiguous and zero up to the span's last 32-position step, so that one
+    // 16-byte read is a lane's 8 positions.  Chunks too long for the work region pack them from the FP32 values.
+    const int span_pad = (span + 31) / 32 * 32;  // P V reads P up to the span's last 32-step
     const int p_offset = (group * span + 7) / 8 * 8;  // floats: after the scores, 16-byte aligned
     // A split chunk also keeps every chunk's statistics after the operands (2 group per chunk).
     const int stat_floats = fused ? 0 : chunks * 2 * group;
@@ -1426,7 +1427,7 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
         }
     };
     if (wave < group && packed_p && span_pad <= 3 * 64) {
-        register_softmax(std::integral_constant<int, 3>{});  // one V block
+        register_softmax(std::integral_constant<int, 3>{});  // spans up to 192
     } else if (wave < group && packed_p && span <= 4 * 64) {
         register_softmax(std::integral_constant<int, 4>{});  // P V reads P up to the span's last 32-step
     } else if (wave < group && packed_p && span <= 6 * 64) {
