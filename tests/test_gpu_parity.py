@@ -169,12 +169,15 @@ def check_bf16_logits(got, want, exact, floor=2e-2):
     (64, 128, 128, 300),   # three chunks of 100 positions: statistics merged, then probabilities
     (64, 130, 130, 130),   # a second tile for waves 0 and 1 (ten tiles in one block)
     (64, 160, 160, 300),   # two chunks of 150 positions
-    (64, 256, 256, 250),   # one fused chunk over two V^T blocks and three rounds of score tiles
-    (64, 384, 384, 380),   # one fused chunk of up to 380 positions: softmax with 3, 4 and 6 scores per lane
-    (32, 160, 160, 160),   # one slice per head; a fused chunk ending on a block boundary
-    (128, 128, 128, 120),  # 64-position V^T blocks: two in one chunk
+    (64, 256, 256, 250),   # one fused chunk of up to 250 positions: one 256-position V block
+    (64, 384, 384, 380),   # one fused chunk of up to 380 positions: softmax with 3, 4 and 6 scores per
+                           # lane, a second V block and K tiles loaded after the input wait
+    (32, 160, 160, 160),   # one slice per head
+    (32, 384, 384, 300),   # 32 dims: a fused chunk over two 256-position V blocks
+    (128, 128, 128, 120),  # 128-position V blocks: one per chunk
+    (128, 384, 384, 300),  # 128 dims: a fused chunk over three 128-position V blocks
     (128, 64, 64, 200),    # 128 dims over four 50-position chunks
-    (64, 1024, 1024, 2100),  # three chunks of 700 positions: five V^T blocks and many score tiles per chunk
+    (64, 1024, 1024, 2100),  # three chunks of 700 positions: three V blocks and many score tiles per chunk
     (64, 1056, 1056, 2100),  # two chunks of 1050 positions: the longest chunk the worker takes
 ])
 def test_bf16_matrix_attention(target, tmp, head_dim, chunk_steps, fused_steps, context):
