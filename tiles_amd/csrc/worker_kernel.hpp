@@ -1479,7 +1479,9 @@ __device__ __forceinline__ void op_attention(const Launch<BF16>& L, const ti_tas
     // only on the split path: computed before the branch, its launch-record reads cost the fused
     // path 0.1-0.2 us per layer.)
     auto stats_block = [&]() {
-        return L.exchange + L.xl.parts + static_cast<size_t>(kv_head) * s.attention_chunks * attention_part_words(s);
+        // attention_part_words(s) from the group and the compile-time head width, without its
+        // division of the head counts.
+        return L.exchange + L.xl.parts + static_cast<size_t>(kv_head) * s.attention_chunks * static_cast<size_t>(group * (dh + 2));
     };
     if (!fused) {
         // This chunk's (max, sum) per head go out as epoch-tagged exchange words; every chunk of
